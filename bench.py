@@ -1,0 +1,165 @@
+"""Benchmark of the HSA forward at the Wan-1.3B chunk shape on one GPU.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+A step is one ``hsa_forward`` call (routing + sparse branch + elu(x)+1 linear branch + fusion) on
+synthetic seeded inputs already resident in HBM: B=1, H=12 (8 sparse heads with per-head top-k
+from {8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16.
+
+Prints one JSON line: ``value`` is the effective sparse TFLOP/s (useful sparse FLOP of one call /
+time of the whole call); ``ms_per_step`` is the HSA forward ms per chunk-call; ``roofline`` is the
+sparse kernel's own rate measured with HIP events on the stream it runs on; ``cpu_baseline`` times
+the CPU oracle (the reference algorithm restated in torch, fp32 math) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0
+METRIC = "HSA fwd ms/chunk + sparse TFLOP/s (%MFMA peak) at Wan-1.3B shape; HKV GB/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-calls", type=int, default=12)
+    return ap.parse_args()
+
+
+def event_time_ms(fn, iters: int) -> float:
+    """Average duration of ``fn`` (launches on torch's current stream) over ``iters`` runs."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path shards by "
+                                   "head across GPUs by design, but no multi-GPU run is part of it)"}))
+        sys.exit(2)
+
+    from worldattention_amd import _lib, workloads
+    from worldattention_amd.hsa import attention as WA
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = workloads.cfg2(device=dev, seed=args.seed)
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    d = q.shape[-1]
+    gate = torch.nn.Linear(d, d).to(dev)
+    with torch.no_grad():
+        gate.weight.zero_()
+        gate.bias.zero_()
+    proj = torch.zeros(13, 1560, dtype=torch.bfloat16, device=dev)
+    kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate,
+              block_size=cfg["block_size"], tau_min=0.35, tau_max=1.0, proj_segment_len=cfg["proj_segment_len"],
+              routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
+
+    def step():
+        with torch.no_grad():
+            return WA.hsa_forward(q, k, v, **kw)
+
+    save = {}
+    with torch.no_grad():
+        WA.hsa_forward(q, k, v, save=save, **kw)
+    route = save["route"]
+    sparse_heads = [h for h, m in enumerate(cfg["head_modes"]) if m != "linear"]
+    useful_flop, tile_flop = workloads.sparse_flops(route.num, route.index, q.shape[1], k.shape[1],
+                                                    cfg["block_size"], d, heads=sparse_heads)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # dominant kernel: the sparse forward alone, same arguments as inside the step
+    plan = WA.HeadPlan(q.shape[2], cfg["head_modes"], dev)
+    out = torch.empty_like(q)
+
+    def sparse_only():
+        bsa_forward(q, k, v, index=route.index, num=route.num, block_size=cfg["block_size"], layout="blhd",
+                    heads=plan.t["sparse_only"], out=out, lq=q.shape[1], lkv=k.shape[1], attn_round_bf16=True)
+
+    for _ in range(3):
+        sparse_only()
+    sparse_ms = event_time_ms(sparse_only, max(args.steps, 20))
+    achieved = useful_flop / (sparse_ms * 1e-3) / 1e12
+
+    result = {
+        "metric": METRIC,
+        "value": round(useful_flop / (ms_per_step * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) + per-frame key offsets + Wan 3-D RoPE)",
+        "config": {"workload": "cfg2: Wan-1.3B chunk HSA forward, B=1 H=12 D=128 Lq=4680 Lkv=32760 block=128, "
+                               "8 sparse heads top-k from {8,16,32} + 4 elu1 linear heads",
+                   "topk": cfg["topk"], "head_modes": cfg["head_modes"], "seed": args.seed},
+        "hsa_fwd_ms_per_chunk": round(ms_per_step, 4),
+        "sparse_kernel_ms": round(sparse_ms, 4),
+        "sparse_useful_gflop": round(useful_flop / 1e9, 3),
+        "sparse_tile_gflop": round(tile_flop / 1e9, 3),
+        "pct_mfma_peak_sparse": round(100 * achieved / MFMA_BF16_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "kernel": "bsa_fwd_kernel<128,128>", "achieved": round(achieved, 3),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+    if not args.no_cpu_baseline:
+        from oracle import hsa as O
+        cpu = {k2: (t.cpu() if torch.is_tensor(t) else t) for k2, t in cfg.items()}
+        projc = proj.cpu()
+        zw, zb = torch.zeros(d, d), torch.zeros(d)
+        times = []
+        for i in range(args.cpu_sample_calls + 1):
+            t1 = time.perf_counter()
+            O.hsa_attention(cpu["q"], cpu["k"], cpu["v"], k_proj_mat=projc, v_proj_mat=projc, gate_weight=zw,
+                            gate_bias=zb, block_size=cfg["block_size"], routing="topk", topk=cfg["topk"],
+                            head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
+            if i:
+                times.append(time.perf_counter() - t1)
+        cpu_s = statistics.median(times)
+        result["cpu_baseline"] = {
+            "value": round(useful_flop / cpu_s / 1e12, 4), "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{args.cpu_sample_calls} full cfg2 HSA forward calls of the CPU oracle (fp32 math), "
+                      f"median {cpu_s * 1e3:.1f} ms/call after 1 warm-up",
+            "ms_per_call": round(cpu_s * 1e3, 2)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

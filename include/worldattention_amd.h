@@ -1,0 +1,176 @@
+/*
+ * worldattention_amd — C ABI of the MI355X (gfx950) HSA + HKV attention path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, launches on the
+ * caller's HIP stream (`stream` is a hipStream_t passed as void*), allocates nothing and keeps no
+ * global device state. Inputs, outputs and workspaces are owned by the caller; workspace sizes
+ * come from the matching *_workspace_bytes query.
+ *
+ * Return value: WA_OK (0) on success; a negative WA_ERR_* for argument errors; a positive
+ * hipError_t for runtime failures. wa_last_error() returns the calling thread's last message.
+ *
+ * Tensor convention ("BLHD"): element (b, t, h, c) of a [B, L, H, C] tensor lives at
+ * ptr + b*sb + t*st + h*sh + c, with strides in elements and the channel dim contiguous — the
+ * layout of the reference's q/k/v and KV-cache slices, so no transposes or pad copies are needed.
+ *
+ * Reference: alibaba-damo-academy/WorldAttention (paths relative to its repository root).
+ */
+#ifndef WORLDATTENTION_AMD_H
+#define WORLDATTENTION_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WA_OK 0
+#define WA_ERR_ARG (-1)
+#define WA_ERR_UNSUPPORTED (-2)
+
+enum { WA_F32 = 0, WA_BF16 = 1 };
+enum { WA_ROUTE_GINI = 0, WA_ROUTE_TOPK = 1 };
+enum { WA_EPI_PLAIN = 0, WA_EPI_FUSE = 1, WA_EPI_GATED = 2 };
+
+/* Library version (major*10000 + minor*100 + patch) and the last error message of this thread. */
+int wa_version(void);
+const char* wa_last_error(void);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Routing                                                                                     */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Block mean pooling of a BLHD tensor into [B, H, num_blocks, D] fp32.
+ * Replaces block_mean_pool, wan/modules/hsa/routing.py:45-61 (called at attention.py:214-215).
+ * The last block may be partial (L < num_blocks*block_size); it averages its real tokens only.
+ * With emulate_rounding set, the reference's rounding is reproduced for a bf16 input: a
+ * block-aligned L gives bf16(sum/block_size); otherwise fp32(bf16(sum)) / real_count.
+ * Only the heads listed in `heads` (device int32[n_heads]; NULL = all) are written. */
+typedef struct wa_pool_args {
+  const void* x; int64_t x_sb, x_st, x_sh; int32_t x_dtype;
+  int64_t B, L, H, D, block_size, num_blocks;
+  const int32_t* heads; int64_t n_heads;
+  float* out;
+  int32_t emulate_rounding;
+} wa_pool_args;
+int wa_block_mean_pool(const wa_pool_args* args, void* stream);
+
+/* Block routing for one call: the block attention map softmax(qp kp^T / sqrt(D)) (or a given
+ * map), the stable descending permutation of every row, and the selected count per row.
+ * Replaces block_attention_map + build_block_routing, wan/modules/hsa/routing.py:64-118
+ * (called at attention.py:212-222), and adds the north-star per-head top-k rule.
+ *   GINI: thresholds[h] = tau_min + mean_{b,i} gini[b,h,i] * tau_span; num counts the sorted
+ *         slots whose exclusive prefix (fp32 of a sequential double cumsum, minus the slot) is
+ *         below the threshold — the reference's rounding points (routing.py:95-113).
+ *   TOPK: num = min(head_k[h], Nkv).
+ * index: [B, H, Nq, Nkv] int32, descending by weight, ties lowest block id first.
+ * num:   [B, H, Nq] int32. mask (optional): [B, H, Nq, Nkv] uint8 selection mask.
+ * probs (optional input) replaces the q_pooled/k_pooled map computation; probs_out (optional)
+ * receives the computed map. Rows of heads not listed in `heads` are not written. */
+typedef struct wa_route_args {
+  const float* probs;
+  const float* q_pooled;
+  const float* k_pooled;
+  int64_t B, H, Nq, Nkv, D;
+  int32_t mode;
+  float tau_min, tau_span;
+  const int32_t* head_k;
+  const int32_t* heads; int64_t n_heads;
+  int32_t* index;
+  int32_t* num;
+  float* thresholds;
+  uint8_t* mask;
+  float* probs_out;
+  void* workspace;
+} wa_route_args;
+int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nkv);
+int wa_route(const wa_route_args* args, void* stream);
+
+/* Boolean selection mask [rows, ncols] (uint8) -> ascending (index [rows, ncols], num [rows]),
+ * index padded with -1. Replaces map_to_index, wan/modules/hsa/block_sparse_triton.py:20-57. */
+int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* index,
+                    int32_t* num, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Block-sparse attention                                                                      */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Forward of block-sparse flash attention (bf16 q/k/v, fp32 accumulation).
+ * Replaces _fwd_kernel/_forward, wan/modules/hsa/block_sparse_triton.py:67-139, 303-320, and the
+ * torch gather path block_sparse_attention_reference, block_sparse_torch.py:16-64.
+ * Query block i (block_size rows) attends to key blocks index[b,h,i,0:num[b,h,i]] (ids clamped
+ * to [0, Nkv-1]); key tokens past min(block_sizes[j], Lkv - j*block_size) are masked; a row with
+ * num = 0 yields 0 (and lse = -inf). index == NULL selects every key block (dense attention).
+ * lse (optional): [B, H, Lq] natural-log log-sum-exp of the scaled logits.
+ * Epilogue (per element, gate g = sigmoid(q . gate_w[d] + gate_b[d]) or sigmoid(q) when gate_w
+ * is NULL, optionally rounded to bf16 before/after the sigmoid):
+ *   PLAIN: o = attn;  FUSE: o = attn + g * x;  GATED: o = g * attn
+ * — the gated fusion of attention.py:246-254 done in registers. */
+typedef struct wa_bsa_fwd_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  void* o; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  float* lse;
+  const int32_t* index; const int32_t* num; int64_t index_width;
+  const int32_t* block_sizes;
+  const int32_t* heads; int64_t n_heads;
+  int64_t B, H, Lq, Lkv, D, block_size;
+  float scale;
+  int32_t epilogue;
+  const void* x; int64_t x_sb, x_st, x_sh; int32_t x_dtype;
+  const void* gate_w; const float* gate_b;
+  int32_t gate_pre_bf16, gate_out_bf16, attn_round_bf16;
+} wa_bsa_fwd_args;
+int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Linear branch                                                                               */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Low-rank sequence projection per segment: for each segment of at most segment_len tokens,
+ * out[seg rows] = proj[0:r, 0:seg_len] @ x[seg], r = min(proj_rank, ceil(seg_len/block_size)),
+ * fp32 accumulation, output rows concatenated along the token axis (out is BLHD, Lc rows).
+ * Replaces compress_kv, wan/modules/hsa/attention.py:64-110. */
+typedef struct wa_compress_args {
+  const void* x; int64_t x_sb, x_st, x_sh; int32_t x_dtype;
+  const void* proj; int32_t proj_dtype; int64_t proj_rank, proj_len;
+  int64_t B, L, H, D, segment_len, block_size;
+  void* out; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+} wa_compress_args;
+int wa_compress_kv(const wa_compress_args* args, void* stream);
+
+/* Kernelized linear attention state (north star, no reference counterpart):
+ * state[b,s,d,e] = sum_t v[t,d] * phi(k[t,e]) and zsum[b,s,e] = sum_t phi(k[t,e]) with
+ * phi(x) = elu(x) + 1, for each listed head heads[s] (fp32 outputs, [B, n_heads, D, D] / [B, n_heads, D]). */
+typedef struct wa_elu1_state_args {
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  int32_t dtype;
+  int64_t B, H, L, D;
+  const int32_t* heads; int64_t n_heads;
+  float* state; float* zsum;
+  void* workspace;
+} wa_elu1_state_args;
+int64_t wa_elu1_state_workspace_bytes(int64_t B, int64_t n_heads, int64_t L, int64_t D);
+int wa_elu1_state(const wa_elu1_state_args* args, void* stream);
+
+/* Kernelized linear attention readout: o[t] = phi(q[t]) S / (phi(q[t]) . z) per listed head,
+ * with the same epilogue options as wa_bsa_fwd (GATED: o = g * o_lin). */
+typedef struct wa_elu1_readout_args {
+  const void* q; int64_t q_sb, q_st, q_sh; int32_t q_dtype;
+  const float* state; const float* zsum;
+  void* o; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  int64_t B, H, L, D;
+  const int32_t* heads; int64_t n_heads;
+  int32_t epilogue;
+  const void* gate_w; const float* gate_b;
+  int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
+} wa_elu1_readout_args;
+int wa_elu1_readout(const wa_elu1_readout_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WORLDATTENTION_AMD_H */

@@ -1,0 +1,86 @@
+"""The C ABI library loads, exports every function ``include/*.h`` declares, its ctypes mirrors match
+the C struct layouts, and argument errors come back as status codes without touching a GPU."""
+import ctypes
+import glob
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from worldattention_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = open(h).read()
+        names += re.findall(r"^\s*(?:int|int64_t|const char\s*\*)\s+(wa_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def declared_structs():
+    names = []
+    for h in HEADERS:
+        names += re.findall(r"typedef struct (wa_\w+_args)\s*\{", open(h).read())
+    return names
+
+
+def test_library_loads_and_reports_version():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    assert _lib.lib().wa_version() >= 100
+
+
+def test_every_declared_function_is_exported_and_bound():
+    funcs = declared_functions()
+    assert len(funcs) >= 10
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    for name in funcs:
+        assert hasattr(handle, name), f"{name} declared but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_ctypes_structs_match_the_c_layout():
+    structs = declared_structs()
+    mirrors = {cls._name: cls for cls in (getattr(_lib, n) for n in dir(_lib))
+               if isinstance(cls, type) and issubclass(cls, ctypes.Structure)
+               for cls._name in [cls.__name__]}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADERS[0]}"', "int main(void) {"]
+    for s in structs:
+        lines.append(f'  printf("{s} size %zu\\n", sizeof({s}));')
+        for field, _ in mirrors[s]._fields_:
+            lines.append(f'  printf("{s} {field} %zu\\n", offsetof({s}, {field}));')
+    lines.append("  return 0; }")
+    with tempfile.TemporaryDirectory() as tmp:
+        src, exe = os.path.join(tmp, "layout.c"), os.path.join(tmp, "layout")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-o", exe, src], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, out):
+        s, field, val = line.split()
+        cls = mirrors[s]
+        if field == "size":
+            assert ctypes.sizeof(cls) == int(val), f"{s} size"
+        else:
+            assert getattr(cls, field).offset == int(val), f"{s}.{field}"
+
+
+def test_argument_errors_return_status_without_a_gpu():
+    handle = _lib.lib()
+    assert handle.wa_bsa_fwd(None, None) == -1
+    assert b"null" in handle.wa_last_error()
+    args = _lib.BsaFwdArgs()
+    args.D, args.block_size = 96, 64
+    assert handle.wa_bsa_fwd(ctypes.byref(args), None) == -1
+    assert b"head dim" in handle.wa_last_error()
+    rargs = _lib.RouteArgs()
+    rargs.index = rargs.num = 16
+    rargs.probs = 16
+    rargs.Nkv, rargs.H = 5000, 1
+    assert handle.wa_route(ctypes.byref(rargs), None) == -1
+    assert handle.wa_map_to_index(None, 1, 1, None, None, None) == -1
+    assert handle.wa_route_workspace_bytes(1, 12, 37, 256) >= 12 * 37 * 257 * 4

@@ -1,0 +1,265 @@
+"""GPU parity of the forward path against the CPU oracle (and the reference's own golden outputs).
+
+Tolerances: integer/index outputs bit-exact; attention outputs max-abs <= 2e-2 and mean-abs <= 2e-3
+against the fp32 oracle (the north-star bf16 tolerance)."""
+import os
+
+import pytest
+import torch
+
+from oracle import hsa as O
+from worldattention_amd import hsa as W
+from worldattention_amd import workloads
+from worldattention_amd.hsa import attention as WA
+from worldattention_amd.hsa import routing as WR
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def assert_close(got, want, max_abs=2e-2, mean_abs=2e-3, what=""):
+    diff = (got.detach().float().cpu() - want.detach().float().cpu()).abs()
+    assert torch.isfinite(got.float()).all(), f"{what}: non-finite output"
+    assert diff.max().item() <= max_abs, f"{what}: max-abs {diff.max().item():.3e} > {max_abs}"
+    assert diff.mean().item() <= mean_abs, f"{what}: mean-abs {diff.mean().item():.3e} > {mean_abs}"
+
+
+# ----------------------------------------------------------------------------------------------
+# routing
+# ----------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("logical", [512, 470])
+def test_block_mean_pool_matches_oracle(dtype, logical):
+    torch.manual_seed(0)
+    x = (torch.randn(2, 3, 512, 64) * 2).to(dtype)
+    x[:, :, logical:] = 0
+    want = O.block_mean_pool(x, logical, 4, 128)
+    got = W.block_mean_pool(x.to(DEV), logical, 4, 128)
+    assert got.dtype == want.dtype
+    if dtype == torch.bfloat16:
+        # the reference rounds the bf16 block mean (or block sum); the kernel reproduces it
+        assert (got.cpu() == want).float().mean().item() >= 0.999
+        assert torch.allclose(got.cpu().float(), want.float(), rtol=2 ** -7, atol=0)
+    else:
+        assert torch.allclose(got.cpu(), want, atol=1e-5, rtol=1e-5)
+
+
+def test_gini_routing_is_bit_exact_on_reference_golden_maps():
+    for c in torch.load(os.path.join(GOLDEN, "routing_gini.pt"), weights_only=True):
+        r = W.build_block_routing(c["block_attn"].to(DEV), c["tau_min"], c["tau_max"], return_mask=True)
+        assert torch.equal(r.index.cpu(), c["index"])
+        assert torch.equal(r.num.cpu(), c["num"])
+        assert torch.equal(r.mask.cpu(), c["mask"])
+        assert torch.allclose(r.thresholds.cpu(), c["thresholds"], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("nkv", [16, 37, 256, 512, 1100])
+def test_routing_is_bit_exact_given_identical_maps_with_ties(nkv):
+    torch.manual_seed(nkv)
+    attn = torch.softmax(torch.randn(2, 3, 9, nkv) * 3, -1)
+    # inject exact ties: quantize one head's weights
+    attn[:, 1] = (attn[:, 1] * 64).round() / 64
+    want_g = O.build_block_routing(attn, 0.35, 1.0, return_mask=True)
+    got_g = W.build_block_routing(attn.to(DEV), 0.35, 1.0, return_mask=True)
+    assert torch.equal(got_g.index.cpu(), want_g.index)
+    assert torch.equal(got_g.num.cpu(), want_g.num)
+    assert torch.equal(got_g.mask.cpu(), want_g.mask)
+    ks = [3, min(17, nkv), 0]
+    want_t = O.build_topk_routing(attn, ks, return_mask=True)
+    got_t = W.build_topk_routing(attn.to(DEV), ks, return_mask=True)
+    assert torch.equal(got_t.index.cpu(), want_t.index)
+    assert torch.equal(got_t.num.cpu(), want_t.num)
+    assert torch.equal(got_t.mask.cpu(), want_t.mask)
+
+
+def test_block_attention_map_matches_oracle():
+    torch.manual_seed(2)
+    qp, kp = torch.randn(1, 4, 37, 128), torch.randn(1, 4, 256, 128)
+    got = W.block_attention_map(qp.to(DEV), kp.to(DEV)).cpu()
+    want = O.block_attention_map(qp, kp)
+    assert torch.allclose(got, want, rtol=1e-5, atol=1e-7)
+
+
+def test_map_to_index_matches_oracle():
+    torch.manual_seed(4)
+    m = torch.rand(2, 3, 5, 200) < 0.3
+    idx, num = W.map_to_index(m.to(DEV))
+    widx, wnum = O.map_to_index(m)
+    assert torch.equal(idx.cpu(), widx) and torch.equal(num.cpu(), wnum)
+
+
+# ----------------------------------------------------------------------------------------------
+# block-sparse forward
+# ----------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("bs", [64, 128])
+def test_block_sparse_attention_matches_oracle(d, bs):
+    torch.manual_seed(d + bs)
+    nq, nkv = 5, 9
+    lkv = nkv * bs - bs // 3          # partial trailing key block
+    q = torch.randn(2, 3, nq * bs, d).bfloat16()
+    k = torch.randn(2, 3, nkv * bs, d).bfloat16()
+    v = torch.randn(2, 3, nkv * bs, d).bfloat16()
+    k[:, :, lkv:] = 0
+    v[:, :, lkv:] = 0
+    index = torch.stack([torch.randperm(nkv) for _ in range(2 * 3 * nq)]).view(2, 3, nq, nkv).int()
+    num = torch.randint(0, nkv + 1, (2, 3, nq), dtype=torch.int32)
+    num[0, 0, 0] = 0                   # empty row -> 0
+    index[1, 2, 1, :3] = torch.tensor([4, 4, 4])   # duplicates count
+    num[1, 2, 1] = 3
+    index[1, 1, 2, 0] = 99             # out of range -> clamped
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    want, lse_want = O.block_sparse_attention(q, k, v, index, num, sizes, bs, return_lse=True)
+    got = W.block_sparse_attention_reference(q.to(DEV), k.to(DEV), v.to(DEV), index.to(DEV), num.to(DEV),
+                                             sizes.to(DEV), bs)
+    assert got.dtype == torch.bfloat16
+    assert_close(got, want, what=f"bsa d={d} bs={bs}")
+    assert torch.count_nonzero(got[0, 0, :bs]) == 0
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    from worldattention_amd import _lib
+    _, lse = bsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), index=index.to(DEV), num=num.to(DEV), block_size=bs,
+                         block_sizes=sizes.to(DEV), want_lse=True)
+    finite = torch.isfinite(lse_want)
+    assert torch.equal(torch.isfinite(lse.cpu()), finite)
+    assert torch.allclose(lse.cpu()[finite], lse_want[finite].float(), atol=2e-2)
+
+
+def test_full_selection_is_dense_attention():
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(1, 2, 256, 64).bfloat16() for _ in range(3))
+    index = torch.arange(4, dtype=torch.int32).view(1, 1, 1, 4).expand(1, 2, 4, 4).contiguous()
+    num = torch.full((1, 2, 4), 4, dtype=torch.int32)
+    got = W.block_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), block_sizes=torch.full((4,), 64, device=DEV),
+                                   q2k_index=index.to(DEV), q2k_num=num.to(DEV))
+    want = torch.nn.functional.scaled_dot_product_attention(q.double(), k.double(), v.double())
+    assert_close(got, want, what="dense")
+
+
+# ----------------------------------------------------------------------------------------------
+# linear branches
+# ----------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compress_kv_matches_oracle(dtype):
+    torch.manual_seed(1)
+    k, v = torch.randn(1, 3, 3200, 128).to(dtype), torch.randn(1, 3, 3200, 128).to(dtype)
+    pk = (torch.rand(25, 1560) / 40).bfloat16()
+    pv = O.init_projection(25, 1560, 64)
+    wk, wv = O.compress_kv(k, v, segment_len=1560, k_proj_mat=pk, v_proj_mat=pv, block_size=64)
+    gk, gv = W.compress_kv(k.to(DEV), v.to(DEV), segment_len=1560, k_proj_mat=pk.to(DEV), v_proj_mat=pv.to(DEV),
+                           block_size=64)
+    assert gk.shape == wk.shape == (1, 3, 25 + 25 + 2, 128)
+    assert_close(gk, wk, max_abs=1e-2, mean_abs=1e-3, what="compress k")
+    assert_close(gv, wv, max_abs=1e-2, mean_abs=1e-3, what="compress v")
+
+
+def test_lowrank_linear_branch_matches_oracle():
+    torch.manual_seed(3)
+    q, kc, vc = torch.randn(1, 2, 300, 64), torch.randn(1, 2, 77, 64), torch.randn(1, 2, 77, 64)
+    got = WA._linear_branch(q.to(DEV), kc.to(DEV), vc.to(DEV))
+    assert_close(got, O.linear_branch_lowrank(q, kc, vc), what="lowrank")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_elu1_linear_branch_matches_oracle(d):
+    torch.manual_seed(d)
+    q, k, v = (torch.randn(1, n, 4, d).bfloat16() for n in (700, 5000, 5000))
+    heads = torch.tensor([0, 2, 3], dtype=torch.int32, device=DEV)
+    s, z = WA.elu1_state(k.to(DEV), v.to(DEV), heads)
+    out = torch.zeros(1, 700, 4, d, dtype=torch.float32, device=DEV)
+    WA.elu1_readout(q.to(DEV), s, z, heads, out)
+    want = O.linear_branch_elu1(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                                compute_dtype=torch.float64).transpose(1, 2)
+    for h in (0, 2, 3):
+        assert_close(out[:, :, h], want[:, :, h], max_abs=1e-2, mean_abs=1e-3, what=f"elu1 head {h}")
+    assert torch.count_nonzero(out[:, :, 1]) == 0
+
+
+# ----------------------------------------------------------------------------------------------
+# hsa_attention end to end
+# ----------------------------------------------------------------------------------------------
+def test_hsa_attention_matches_reference_golden_outputs():
+    """The reference module's own outputs (Gini routing, low-rank branch, trained-looking gate)."""
+    for c in torch.load(os.path.join(GOLDEN, "hsa_attention.pt"), weights_only=True):
+        gate = torch.nn.Linear(c["q"].shape[-1], c["q"].shape[-1]).to(c["q"].dtype)
+        with torch.no_grad():
+            gate.weight.copy_(c["gate_weight"])
+            gate.bias.copy_(c["gate_bias"])
+        with torch.no_grad():
+            got = W.hsa_attention(c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV), k_proj_mat=c["k_proj_mat"].to(DEV),
+                                  v_proj_mat=c["v_proj_mat"].to(DEV), gate_lin=gate.to(DEV), block_size=c["block_size"],
+                                  tau_min=c["tau_min"], tau_max=c["tau_max"], proj_segment_len=c["proj_segment_len"])
+        assert got.dtype == c["out"].dtype and got.shape == c["out"].shape
+        assert_close(got, c["out"], what=f"golden {tuple(c['q'].shape)} {c['q'].dtype}")
+
+
+def _run_both(cfg, oracle_kwargs=None, gate=None):
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    kw = dict(block_size=cfg["block_size"], routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"],
+              linear_mode=cfg["linear_mode"], proj_segment_len=cfg["proj_segment_len"])
+    d = q.shape[-1]
+    rank = -(-cfg["proj_segment_len"] // cfg["block_size"])
+    proj = O.init_projection(rank, cfg["proj_segment_len"], cfg["block_size"])
+    w = torch.zeros(d, d) if gate is None else gate[0]
+    b = torch.zeros(d) if gate is None else gate[1]
+    want, parts = O.hsa_attention(q.cpu(), k.cpu(), v.cpu(), k_proj_mat=proj, v_proj_mat=proj, gate_weight=w,
+                                  gate_bias=b, return_parts=True, **kw)
+    lin = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        lin.bias.copy_(b)
+    save = {}
+    with torch.no_grad():
+        got = WA.hsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), k_coarse=None, v_coarse=None, k_proj_mat=proj.to(DEV),
+                             v_proj_mat=proj.to(DEV), gate_lin=lin, tau_min=0.35, tau_max=1.0, save=save, **kw)
+    return got, want, parts, save
+
+
+def test_hsa_cfg1_split_heads_match_oracle():
+    cfg = workloads.cfg1()
+    got, want, parts, save = _run_both(cfg, gate=(torch.randn(64, 64) * 0.1, torch.full((64,), 0.2)))
+    r = save["route"]
+    assert torch.equal(r.num.cpu()[:, 0], parts["routing"].num[:, 0])
+    assert torch.equal(r.index.cpu()[:, 0, :, :4], parts["routing"].index[:, 0, :, :4])
+    assert_close(got, want, what="cfg1")
+
+
+def test_hsa_cfg2_wan_chunk_matches_oracle():
+    cfg = workloads.cfg2()
+    got, want, parts, save = _run_both(cfg)
+    sparse = [h for h, m in enumerate(cfg["head_modes"]) if m == "sparse"]
+    r = save["route"]
+    for h in sparse:
+        assert torch.equal(r.num.cpu()[:, h], parts["routing"].num[:, h])
+        kk = cfg["topk"][h]
+        same = (r.index.cpu()[:, h, :, :kk] == parts["routing"].index[:, h, :, :kk]).all(-1).float().mean()
+        assert same.item() == 1.0, f"head {h}: {same.item()}"
+    assert_close(got, want, what="cfg2")
+
+
+def test_hsa_reference_mode_bf16_matches_oracle():
+    torch.manual_seed(7)
+    q = torch.randn(1, 1000, 4, 128).bfloat16()
+    k = torch.randn(1, 3000, 4, 128).bfloat16()
+    v = torch.randn(1, 3000, 4, 128).bfloat16()
+    proj = (torch.rand(8, 1000) / 100).bfloat16()
+    gate = torch.nn.Linear(128, 128).bfloat16()
+    with torch.no_grad():
+        want = O.hsa_attention(q, k, v, k_proj_mat=proj, v_proj_mat=proj, gate_weight=gate.weight, gate_bias=gate.bias,
+                               block_size=128, proj_segment_len=1000)
+        got = W.hsa_attention(q.to(DEV), k.to(DEV), v.to(DEV), k_proj_mat=proj.to(DEV), v_proj_mat=proj.to(DEV),
+                              gate_lin=gate.to(DEV), block_size=128, proj_segment_len=1000)
+    assert_close(got, want, what="reference mode bf16")
+
+
+def test_coarse_cache_equals_inline_compression_on_gpu():
+    torch.manual_seed(9)
+    hsa = W.HSAAttention(num_heads=2, head_dim=64, block_size=64, proj_segment_len=100).to(DEV)
+    from worldattention_amd.hsa_stage import init_hsa_parameters
+    init_hsa_parameters(hsa)
+    q, k, v = (torch.randn(1, n, 2, 64, device=DEV) for n in (150, 400, 400))
+    with torch.no_grad():
+        inline = hsa(q, k, v)
+        kc, vc = hsa.compress_kv_cache(k, v)
+        cached = hsa(q, k, v, k_coarse=kc, v_coarse=vc)
+    assert torch.allclose(inline, cached, atol=1e-5)

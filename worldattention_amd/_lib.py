@@ -1,0 +1,198 @@
+"""ctypes binding of ``libworldattention_amd.so`` (declared in ``include/worldattention_amd.h``).
+
+The library is the only compute path: if it is missing, or a tensor is not on a ROCm GPU, the
+calls raise — there is no CPU fallback. Argument structs mirror the C header field for field.
+"""
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libworldattention_amd.so")
+
+WA_F32, WA_BF16 = 0, 1
+WA_ROUTE_GINI, WA_ROUTE_TOPK = 0, 1
+WA_EPI_PLAIN, WA_EPI_FUSE, WA_EPI_GATED = 0, 1, 2
+
+
+def _struct(name, fields):
+    return type(name, (ctypes.Structure,), {"_fields_": fields})
+
+
+PoolArgs = _struct("wa_pool_args", [
+    ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
+    ("B", c_int64), ("L", c_int64), ("H", c_int64), ("D", c_int64), ("block_size", c_int64),
+    ("num_blocks", c_int64), ("heads", c_void_p), ("n_heads", c_int64), ("out", c_void_p),
+    ("emulate_rounding", c_int32),
+])
+
+RouteArgs = _struct("wa_route_args", [
+    ("probs", c_void_p), ("q_pooled", c_void_p), ("k_pooled", c_void_p),
+    ("B", c_int64), ("H", c_int64), ("Nq", c_int64), ("Nkv", c_int64), ("D", c_int64),
+    ("mode", c_int32), ("tau_min", c_float), ("tau_span", c_float),
+    ("head_k", c_void_p), ("heads", c_void_p), ("n_heads", c_int64),
+    ("index", c_void_p), ("num", c_void_p), ("thresholds", c_void_p), ("mask", c_void_p),
+    ("probs_out", c_void_p), ("workspace", c_void_p),
+])
+
+BsaFwdArgs = _struct("wa_bsa_fwd_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("o", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("lse", c_void_p),
+    ("index", c_void_p), ("num", c_void_p), ("index_width", c_int64),
+    ("block_sizes", c_void_p),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64), ("block_size", c_int64),
+    ("scale", c_float),
+    ("epilogue", c_int32),
+    ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
+    ("gate_w", c_void_p), ("gate_b", c_void_p),
+    ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("attn_round_bf16", c_int32),
+])
+
+CompressArgs = _struct("wa_compress_args", [
+    ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
+    ("proj", c_void_p), ("proj_dtype", c_int32), ("proj_rank", c_int64), ("proj_len", c_int64),
+    ("B", c_int64), ("L", c_int64), ("H", c_int64), ("D", c_int64), ("segment_len", c_int64),
+    ("block_size", c_int64),
+    ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+])
+
+Elu1StateArgs = _struct("wa_elu1_state_args", [
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("H", c_int64), ("L", c_int64), ("D", c_int64),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("state", c_void_p), ("zsum", c_void_p), ("workspace", c_void_p),
+])
+
+Elu1ReadoutArgs = _struct("wa_elu1_readout_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64), ("q_dtype", c_int32),
+    ("state", c_void_p), ("zsum", c_void_p),
+    ("o", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("B", c_int64), ("H", c_int64), ("L", c_int64), ("D", c_int64),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("epilogue", c_int32),
+    ("gate_w", c_void_p), ("gate_b", c_void_p),
+    ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
+])
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "wa_version": (c_int, []),
+    "wa_last_error": (c_char_p, []),
+    "wa_block_mean_pool": (c_int, [POINTER(PoolArgs), c_void_p]),
+    "wa_route_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
+    "wa_route": (c_int, [POINTER(RouteArgs), c_void_p]),
+    "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
+    "wa_compress_kv": (c_int, [POINTER(CompressArgs), c_void_p]),
+    "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
+    "wa_elu1_state": (c_int, [POINTER(Elu1StateArgs), c_void_p]),
+    "wa_elu1_readout": (c_int, [POINTER(Elu1ReadoutArgs), c_void_p]),
+}
+
+
+@functools.lru_cache(maxsize=None)
+def lib() -> ctypes.CDLL:
+    """Load the HIP library once; raise with build instructions when it is absent."""
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"worldattention_amd: {LIB_PATH} is missing; build it with "
+            "`python -m worldattention_amd.csrc.build` (hipcc, gfx950)")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().wa_last_error().decode(errors="replace")
+        if rc < 0:
+            raise ValueError(f"{name}: {msg}")
+        raise RuntimeError(f"{name} failed (hip error {rc}): {msg}")
+
+
+# ----------------------------------------------------------------------------------------------
+# tensor helpers
+# ----------------------------------------------------------------------------------------------
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one ROCm GPU; there is no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "worldattention_amd runs its HIP kernels on a ROCm GPU only; got a tensor on "
+                f"{t.device}. Move inputs to the GPU (there is no CPU fallback).")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return WA_BF16
+    if t.dtype == torch.float32:
+        return WA_F32
+    raise TypeError(f"unsupported dtype {t.dtype}; expected bfloat16 or float32")
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def blhd(t: torch.Tensor):
+    """(ptr, sb, st, sh) of a [B, L, H, C] tensor whose channel dim is contiguous."""
+    if t.stride(-1) != 1:
+        raise ValueError("channel dimension must be contiguous")
+    return t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)
+
+
+def bhld(t: torch.Tensor):
+    """(ptr, sb, st, sh) of a [B, H, L, C] tensor (reference sparse-kernel layout)."""
+    if t.stride(-1) != 1:
+        raise ValueError("channel dimension must be contiguous")
+    return t.data_ptr(), t.stride(0), t.stride(2), t.stride(1)
+
+
+def kernel_ready(t: torch.Tensor, dtype=torch.bfloat16, align_elems: int = 8) -> torch.Tensor:
+    """Cast to ``dtype`` and make the channel dim contiguous with 16-byte aligned rows."""
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    if t.stride(-1) != 1 or any(s % align_elems for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        t = t.contiguous()
+        if t.data_ptr() % 16 or any(s % align_elems for s in t.stride()[:-1]):
+            t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+_HEAD_CACHE: dict = {}
+
+
+def head_list(heads, device: torch.device) -> torch.Tensor:
+    """Device int32 tensor of head ids, cached per (device, heads)."""
+    key = (str(device), tuple(int(h) for h in heads))
+    t = _HEAD_CACHE.get(key)
+    if t is None:
+        t = torch.tensor(key[1], dtype=torch.int32, device=device)
+        _HEAD_CACHE[key] = t
+    return t

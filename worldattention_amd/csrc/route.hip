@@ -1,0 +1,384 @@
+// Block routing kernels: block mean pooling, block attention map + stable descending sort +
+// selection (Gini cumulative mass or per-head top-k), and mask -> index compaction.
+//
+// Reference semantics: wan/modules/hsa/routing.py:45-118 and block_sparse_triton.py:20-57.
+#include "common.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------------------------
+// Block mean pooling (routing.py:45-61). One workgroup per (block, head, batch); every thread
+// reads 16 bytes per token row and accumulates in fp32; the row slots are summed through LDS.
+// ---------------------------------------------------------------------------------------------
+struct PoolParams {
+  const void* x; int64_t sb, st, sh; int dtype;
+  int L, H, D, Bs, N;
+  const int32_t* heads;
+  float* out;
+  int emulate;
+};
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
+  extern __shared__ float red[];  // [rows_per_pass][D]
+  const int blk = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tpr = p.D / VEC;             // threads per token row
+  const int rpp = 256 / tpr;             // token rows per pass
+  const int tid = threadIdx.x;
+  const int slot = tid / tpr, col = (tid % tpr) * VEC;
+  const int real = max(0, min(p.Bs, p.L - blk * p.Bs));
+  float acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+  if (slot < rpp) {
+    const T* base = (const T*)p.x + (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)blk * p.Bs * p.st + col;
+    for (int t = slot; t < real; t += rpp) {
+      const T* src = base + (int64_t)t * p.st;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] += (float)src[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) red[slot * p.D + col + i] = acc[i];
+  }
+  __syncthreads();
+  for (int d = tid; d < p.D; d += 256) {
+    float s = 0.f;
+    for (int r = 0; r < rpp; ++r) s += red[r * p.D + d];
+    float m;
+    const bool bf = p.emulate && p.dtype == WA_BF16;
+    if (p.L % p.Bs == 0) {
+      m = s / (float)p.Bs;
+      if (bf) m = wa_bf16_round(m);
+    } else {
+      if (bf) s = wa_bf16_round(s);
+      m = s / (float)real;
+    }
+    p.out[(((int64_t)b * p.H + h) * p.N + blk) * p.D + d] = m;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Routing of one row (batch, head, query block): probabilities, bitonic sort of
+// (probability desc, block id asc) keys in LDS, permutation + count (+ Gini inputs).
+// ---------------------------------------------------------------------------------------------
+struct RouteParams {
+  const float* probs; const float* qp; const float* kp;
+  int B, H, Nq, Nkv, D, NP;
+  int mode;
+  float tau_min, tau_span, scale;
+  const int32_t* head_k;
+  const int32_t* heads;
+  int32_t* index; int32_t* num; float* thresholds; uint8_t* mask; float* probs_out;
+  float* ws_sorted; float* ws_gini;
+};
+
+__device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
+  v = wa_wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float r = scratch[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = fmaxf(r, scratch[i]);
+  return r;
+}
+
+__device__ __forceinline__ double block_reduce_sum_d(double v, double* scratch) {
+  v = wa_wave_sum_d(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  double r = 0.0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += scratch[i];
+  return r;
+}
+
+__device__ __forceinline__ float key_to_float(uint64_t key) {
+  const uint32_t u = (uint32_t)(key >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
+}
+
+__global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
+  extern __shared__ uint64_t keys[];        // [NP]
+  __shared__ float qrow[256];
+  __shared__ double dscratch[8];
+  __shared__ float fscratch[8];
+  const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x;
+  const int64_t row = ((int64_t)b * p.H + h) * p.Nq + i;
+  const int N = p.Nkv;
+
+  // 1. block attention probabilities of this row
+  float* pr = (float*)keys;  // reuse the key buffer for the fp32 row (NP*8 bytes >= N*4)
+  if (p.probs) {
+    for (int j = tid; j < N; j += 256) pr[j] = p.probs[row * N + j];
+    __syncthreads();
+  } else {
+    const float* qsrc = p.qp + row * p.D;
+    for (int d = tid; d < p.D; d += 256) qrow[d] = qsrc[d];
+    __syncthreads();
+    // 8 threads per key row: thread tg of the group reads d = 32k + 4tg .. +3 (coalesced float4).
+    const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * p.D;
+    const int grp = tid >> 3, tg = tid & 7;
+    const bool vec = (p.D & 31) == 0;
+    for (int j0 = 0; j0 < N; j0 += 32) {
+      const int j = j0 + grp;
+      float s = 0.f;
+      if (j < N) {
+        const float* kr = kbase + (int64_t)j * p.D;
+        if (vec) {
+          for (int d = 4 * tg; d < p.D; d += 32) {
+            const f32x4 kv = *(const f32x4*)(kr + d);
+            s = fmaf(qrow[d], kv[0], s);
+            s = fmaf(qrow[d + 1], kv[1], s);
+            s = fmaf(qrow[d + 2], kv[2], s);
+            s = fmaf(qrow[d + 3], kv[3], s);
+          }
+        } else {
+          for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], kr[d], s);
+        }
+      }
+      s += __shfl_xor(s, 1, 64);
+      s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 4, 64);
+      if (j < N && tg == 0) pr[j] = s * p.scale;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = tid; j < N; j += 256) mx = fmaxf(mx, pr[j]);
+    mx = block_reduce_max(mx, fscratch);
+    double se = 0.0;
+    for (int j = tid; j < N; j += 256) {
+      const float e = expf(pr[j] - mx);
+      pr[j] = e;
+      se += (double)e;
+    }
+    se = block_reduce_sum_d(se, dscratch);
+    const float inv_sum = (float)(1.0 / se);
+    for (int j = tid; j < N; j += 256) {
+      const float pj = pr[j] * inv_sum;
+      pr[j] = pj;
+      if (p.probs_out) p.probs_out[row * N + j] = pj;
+    }
+    __syncthreads();
+  }
+
+  // 2. composite keys: (probability ascending-order bits) << 32 | ~block id; padding = 0.
+  uint64_t mine[16];
+  const int per = p.NP / 256 > 0 ? p.NP / 256 : 1;
+  for (int e = 0; e < per; ++e) {
+    const int j = tid + e * 256;
+    uint64_t kv = 0;
+    if (j < N) kv = ((uint64_t)wa_float_key(pr[j]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)j);
+    mine[e] = kv;
+  }
+  __syncthreads();
+  for (int e = 0; e < per; ++e) {
+    const int j = tid + e * 256;
+    if (j < p.NP) keys[j] = mine[e];
+  }
+  __syncthreads();
+
+  // 3. bitonic sort, descending
+  for (int size = 2; size <= p.NP; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < p.NP / 2; t += 256) {
+        const int lo = 2 * t - (t & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = ((lo & size) == 0);
+        const uint64_t a = keys[lo], c = keys[hi];
+        if ((a < c) == desc) {
+          keys[lo] = c;
+          keys[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // 4. permutation, count, gini inputs
+  int32_t* idx_row = p.index + row * N;
+  for (int m = tid; m < N; m += 256) idx_row[m] = (int32_t)(0xFFFFFFFFu - (uint32_t)keys[m]);
+  if (p.mode == WA_ROUTE_TOPK) {
+    const int kk = p.head_k ? p.head_k[h] : N;
+    const int n = max(0, min(kk, N));
+    if (tid == 0) p.num[row] = n;
+    if (p.mask) {
+      uint8_t* mrow = p.mask + row * N;
+      for (int m = tid; m < N; m += 256) mrow[(int32_t)(0xFFFFFFFFu - (uint32_t)keys[m])] = m < n ? 1 : 0;
+    }
+  } else {
+    double gs = 0.0;
+    for (int m = tid; m < N; m += 256) {
+      const float pm = key_to_float(keys[m]);
+      p.ws_sorted[row * N + m] = pm;
+      const float coef = (float)(N + 1 - 2 * (m + 1));
+      gs += (double)(coef * pm);
+    }
+    gs = block_reduce_sum_d(gs, dscratch);
+    if (tid == 0) p.ws_gini[row] = (float)gs / (float)N;
+  }
+}
+
+// Gini second pass: per-head threshold (mean of the head's row Ginis), then the count of sorted
+// slots whose exclusive prefix is below it. The prefix is the reference's: a sequential double
+// running sum rounded to fp32, minus the slot's own weight in fp32 (routing.py:95-113).
+__global__ void __launch_bounds__(64) gini_count_kernel(RouteParams p) {
+  extern __shared__ float sp[];  // [N] sorted probabilities, then keep flags
+  const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int lane = threadIdx.x;
+  const int64_t row = ((int64_t)b * p.H + h) * p.Nq + i;
+  const int N = p.Nkv;
+
+  double s = 0.0;
+  for (int r = lane; r < p.B * p.Nq; r += 64) {
+    const int bb = r / p.Nq, ii = r % p.Nq;
+    s += (double)p.ws_gini[((int64_t)bb * p.H + h) * p.Nq + ii];
+  }
+  s = wa_wave_sum_d(s);
+  const float mean = (float)(s / (double)(p.B * p.Nq));
+  const float thr = __fadd_rn(p.tau_min, __fmul_rn(mean, p.tau_span));
+  if (b == 0 && i == 0 && lane == 0) p.thresholds[h] = thr;
+
+  for (int m = lane; m < N; m += 64) sp[m] = p.ws_sorted[row * N + m];
+  __syncthreads();
+  if (lane == 0) {
+    double c = 0.0;
+    int count = 0;
+    for (int m = 0; m < N; ++m) {
+      const float pm = sp[m];
+      c += (double)pm;
+      const float excl = __fsub_rn((float)c, pm);
+      const bool keep = excl < thr;
+      count += keep;
+      sp[m] = keep ? 1.f : 0.f;
+    }
+    p.num[row] = count;
+  }
+  __syncthreads();
+  if (p.mask) {
+    uint8_t* mrow = p.mask + row * N;
+    const int32_t* idx_row = p.index + row * N;
+    for (int m = lane; m < N; m += 64) mrow[idx_row[m]] = sp[m] != 0.f ? 1 : 0;
+  }
+}
+
+// Mask -> ascending (index, num) per row, padded with -1 (block_sparse_triton.py:20-57).
+__global__ void __launch_bounds__(64) map_to_index_kernel(const uint8_t* mask, int64_t ncols,
+                                                          int32_t* index, int32_t* num) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const uint8_t* mrow = mask + row * ncols;
+  int32_t* irow = index + row * ncols;
+  int count = 0;
+  for (int64_t base = 0; base < ncols; base += 64) {
+    const int64_t c = base + lane;
+    const bool bit = c < ncols && mrow[c] != 0;
+    const uint64_t ballot = __ballot(bit);
+    const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (bit) irow[count + before] = (int32_t)c;
+    count += __popcll(ballot);
+  }
+  for (int64_t c = count + lane; c < ncols; c += 64) irow[c] = -1;
+  if (lane == 0) num[row] = count;
+}
+
+}  // namespace
+
+extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->x && a->out, "wa_block_mean_pool: null argument");
+  WA_CHECK_ARG(a->x_dtype == WA_F32 || a->x_dtype == WA_BF16, "wa_block_mean_pool: bad dtype");
+  WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->D > 0 && a->D <= 1024 && a->block_size > 0 && a->num_blocks >= 0,
+               "wa_block_mean_pool: bad sizes");
+  WA_CHECK_ARG(a->L <= a->num_blocks * a->block_size && a->L > (a->num_blocks - 1) * a->block_size,
+               "wa_block_mean_pool: L=%lld does not fill %lld blocks of %lld", (long long)a->L,
+               (long long)a->num_blocks, (long long)a->block_size);
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  if (a->B == 0 || nh == 0 || a->num_blocks == 0) return WA_OK;
+  PoolParams pp{a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype, (int)a->L, (int)a->H, (int)a->D,
+                (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding};
+  dim3 grid((unsigned)a->num_blocks, (unsigned)nh, (unsigned)a->B);
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec_ok = wa_aligned16(a->x);
+  if (a->x_dtype == WA_BF16) {
+    const bool v8 = vec_ok && a->D % 8 == 0 && a->x_sb % 8 == 0 && a->x_st % 8 == 0 && a->x_sh % 8 == 0 && a->D / 8 <= 256;
+    if (v8) {
+      const int rpp = 256 / (int)(a->D / 8);
+      hipLaunchKernelGGL((pool_kernel<bf16_t, 8>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+    } else {
+      WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned bf16 input needs D <= 256");
+      const int rpp = 256 / (int)a->D;
+      hipLaunchKernelGGL((pool_kernel<bf16_t, 1>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+    }
+  } else {
+    const bool v4 = vec_ok && a->D % 4 == 0 && a->x_sb % 4 == 0 && a->x_st % 4 == 0 && a->x_sh % 4 == 0 && a->D / 4 <= 256;
+    if (v4) {
+      const int rpp = 256 / (int)(a->D / 4);
+      hipLaunchKernelGGL((pool_kernel<float, 4>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+    } else {
+      WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned fp32 input needs D <= 256");
+      const int rpp = 256 / (int)a->D;
+      hipLaunchKernelGGL((pool_kernel<float, 1>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+    }
+  }
+  return wa_launch_status("block_mean_pool");
+}
+
+static int64_t next_pow2(int64_t n) {
+  int64_t p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+extern "C" int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nkv) {
+  const int64_t rows = B * H * Nq;
+  return ((rows * Nkv + rows) * 4 + 255) / 256 * 256;
+}
+
+extern "C" int wa_route(const wa_route_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->index && a->num, "wa_route: null output");
+  WA_CHECK_ARG(a->probs || (a->q_pooled && a->k_pooled), "wa_route: need probs or pooled q/k");
+  WA_CHECK_ARG(a->mode == WA_ROUTE_GINI || a->mode == WA_ROUTE_TOPK, "wa_route: bad mode");
+  WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->Nq >= 0 && a->Nkv > 0 && a->Nkv <= 4096,
+               "wa_route: Nkv=%lld outside [1, 4096]", (long long)a->Nkv);
+  WA_CHECK_ARG(a->probs || (a->D > 0 && a->D <= 256), "wa_route: head dim must be <= 256");
+  if (a->mode == WA_ROUTE_GINI) WA_CHECK_ARG(a->workspace && a->thresholds, "wa_route: GINI needs workspace and thresholds");
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  if (a->B == 0 || a->Nq == 0 || nh == 0) return WA_OK;
+  RouteParams rp{};
+  rp.probs = a->probs; rp.qp = a->q_pooled; rp.kp = a->k_pooled;
+  rp.B = (int)a->B; rp.H = (int)a->H; rp.Nq = (int)a->Nq; rp.Nkv = (int)a->Nkv; rp.D = (int)a->D;
+  rp.NP = (int)(next_pow2(a->Nkv) < 256 ? 256 : next_pow2(a->Nkv));
+  rp.mode = a->mode; rp.tau_min = a->tau_min; rp.tau_span = a->tau_span;
+  rp.scale = (float)pow((double)a->D, -0.5);
+  rp.head_k = a->head_k; rp.heads = a->heads;
+  rp.index = a->index; rp.num = a->num; rp.thresholds = a->thresholds; rp.mask = a->mask;
+  rp.probs_out = a->probs_out;
+  const int64_t rows = a->B * a->H * a->Nq;
+  rp.ws_sorted = (float*)a->workspace;
+  rp.ws_gini = a->workspace ? (float*)a->workspace + rows * a->Nkv : nullptr;
+  dim3 grid((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);
+  int rc = wa_launch_status("route");
+  if (rc != WA_OK || a->mode != WA_ROUTE_GINI) return rc;
+  hipLaunchKernelGGL(gini_count_kernel, grid, dim3(64), (size_t)a->Nkv * sizeof(float), s, rp);
+  return wa_launch_status("route_gini_count");
+}
+
+extern "C" int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* index,
+                               int32_t* num, void* stream) {
+  WA_CHECK_ARG(mask && index && num, "wa_map_to_index: null argument");
+  WA_CHECK_ARG(rows >= 0 && ncols >= 0 && rows < ((int64_t)1 << 31), "wa_map_to_index: bad sizes");
+  if (rows == 0) return WA_OK;
+  hipLaunchKernelGGL(map_to_index_kernel, dim3((unsigned)rows), dim3(64), 0, (hipStream_t)stream, mask,
+                     ncols, index, num);
+  return wa_launch_status("map_to_index");
+}

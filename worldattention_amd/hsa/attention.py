@@ -1,0 +1,470 @@
+"""Hybrid Sparse Attention (HSA) on MI355X, with the reference's call signatures.
+
+Mirrors ``wan/modules/hsa/attention.py``: ``resolve_backend`` (:47-61), ``compress_kv`` (:64-110),
+``_linear_branch`` (:113-118), ``hsa_parameter_names`` (:121-132), ``require_trained_hsa``
+(:135-150), ``hsa_attention`` (:153-259) and ``HSAAttention`` (:262-380).
+
+Every branch runs in ``libworldattention_amd`` on ``[B, L, H, D]`` tensors in place (no transposes,
+no pad copies): routing (``wa_block_mean_pool`` + ``wa_route``), the sparse branch (``wa_bsa_fwd``
+over the routed lists), the linear branch (``wa_compress_kv`` + dense ``wa_bsa_fwd`` over the
+compressed keys, or ``wa_elu1_state`` + ``wa_elu1_readout``), and the gated fusion (in the
+epilogue of whichever kernel writes a head's output last).
+
+North-star extensions (keyword-only, defaults give the reference behaviour):
+
+* ``routing="topk"`` with ``topk`` (int or per-head list) instead of Gini routing;
+* ``linear_mode="elu1"``: kernelized linear attention ``phi(q) S / (phi(q) . z)``,
+  ``phi = elu + 1``, over the full-resolution KV window;
+* ``head_modes``: per head ``"both"`` (reference), ``"sparse"`` or ``"linear"``; a head adds only
+  the branches it runs: ``out_h = [sparse] sparse_h + [linear] gate_h * linear_h``.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+from . import distill
+from .block_sparse import bsa_forward
+from .routing import _route, block_counts, pool_blhd
+
+__all__ = [
+    "HSAAttention",
+    "hsa_attention",
+    "compress_kv",
+    "resolve_backend",
+    "hsa_parameter_names",
+    "require_trained_hsa",
+]
+
+_BACKENDS = ("auto", "triton", "torch")
+_HSA_ATTR = "hsa_attention"
+_HEAD_MODES = ("both", "sparse", "linear")
+_LINEAR_MODES = ("lowrank", "elu1")
+_ROUTING_MODES = ("gini", "topk")
+SUPPORTED_BLOCK_SIZES = (64, 128)
+
+
+def resolve_backend(backend: str) -> str:
+    """Validate a backend name (``attention.py:47-61``).
+
+    Accepts ``"auto"``, ``"triton"`` and ``"torch"`` and rejects anything else, as the reference
+    does. Every name runs the same HIP kernels; the name is kept so existing configs load.
+    """
+    backend = str(backend or "auto").lower()
+    if backend not in _BACKENDS:
+        raise ValueError(f"unknown HSA backend {backend!r}; expected one of {_BACKENDS}")
+    if backend != "auto":
+        return backend
+    return "triton" if torch.cuda.is_available() else "torch"
+
+
+# ----------------------------------------------------------------------------------------------
+# Low-rank compression
+# ----------------------------------------------------------------------------------------------
+def coarse_length(kv_len: int, segment_len: int, proj_rank: int, block_size: int) -> int:
+    """Rows produced by compressing ``kv_len`` tokens (sum of per-segment ranks)."""
+    if segment_len <= 0:
+        segment_len = kv_len
+    total = 0
+    for start in range(0, kv_len, segment_len):
+        seg = min(segment_len, kv_len - start)
+        total += min(proj_rank, math.ceil(seg / block_size))
+    return total
+
+
+def _compress(x: torch.Tensor, proj: torch.Tensor, *, segment_len: int, block_size: int, layout: str) -> torch.Tensor:
+    dev = _lib.require_gpu(x, proj)
+    if layout == "bhld":
+        bsz, heads, length, d = x.shape
+    else:
+        bsz, length, heads, d = x.shape
+    if segment_len <= 0:
+        segment_len = length
+    for start in range(0, length, segment_len):
+        seg = min(segment_len, length - start)
+        if seg > proj.shape[1]:
+            raise ValueError(
+                f"segment length {seg} exceeds projection length {proj.shape[1]}; increase proj_segment_len")
+    lc = coarse_length(length, segment_len, proj.shape[0], block_size)
+    src = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+    if src.stride(-1) != 1:
+        src = src.contiguous()
+    pj = proj if proj.dtype in (torch.float32, torch.bfloat16) else proj.float()
+    pj = pj.contiguous()
+    if layout == "bhld":
+        out = torch.empty((bsz, heads, lc, d), dtype=x.dtype, device=dev)
+        xp, x_sb, x_st, x_sh = _lib.bhld(src)
+        op, o_sb, o_st, o_sh = _lib.bhld(out)
+    else:
+        out = torch.empty((bsz, lc, heads, d), dtype=x.dtype, device=dev)
+        xp, x_sb, x_st, x_sh = _lib.blhd(src)
+        op, o_sb, o_st, o_sh = _lib.blhd(out)
+    args = _lib.CompressArgs(xp, x_sb, x_st, x_sh, _lib.dtype_code(src), pj.data_ptr(), _lib.dtype_code(pj),
+                             pj.shape[0], pj.shape[1], bsz, length, heads, d, segment_len, block_size,
+                             op, o_sb, o_st, o_sh, _lib.dtype_code(out))
+    _lib.call("wa_compress_kv", args, _lib.stream_ptr(dev))
+    return out
+
+
+def compress_kv(k: torch.Tensor, v: torch.Tensor, *, segment_len: int, k_proj_mat: torch.Tensor,
+                v_proj_mat: torch.Tensor, block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Project ``[B, H, L, D]`` keys and values onto the low-rank sequence basis (``attention.py:64-110``)."""
+    if k_proj_mat.shape != v_proj_mat.shape:
+        raise ValueError(
+            "k_proj_mat and v_proj_mat must have the same shape, got "
+            f"{tuple(k_proj_mat.shape)} and {tuple(v_proj_mat.shape)}")
+    return (_compress(k, k_proj_mat, segment_len=segment_len, block_size=block_size, layout="bhld"),
+            _compress(v, v_proj_mat, segment_len=segment_len, block_size=block_size, layout="bhld"))
+
+
+def _linear_branch(q: torch.Tensor, k_coarse: torch.Tensor, v_coarse: torch.Tensor) -> torch.Tensor:
+    """Softmax attention of ``[B, H, L, D]`` queries over compressed keys (``attention.py:113-118``)."""
+    block = 128 if q.shape[-1] == 128 else 64
+    out, _ = bsa_forward(_lib.kernel_ready(q), _lib.kernel_ready(k_coarse), _lib.kernel_ready(v_coarse),
+                         index=None, num=None, block_size=block, out_dtype=v_coarse.dtype)
+    return out
+
+
+# ----------------------------------------------------------------------------------------------
+# Parameter bookkeeping (pure Python, identical behaviour)
+# ----------------------------------------------------------------------------------------------
+def hsa_parameter_names(model: nn.Module) -> list[str]:
+    """State-dict keys of every HSA parameter in ``model``, found by module type (``:121-132``)."""
+    names = []
+    for module_name, module in model.named_modules():
+        if isinstance(module, HSAAttention):
+            prefix = f"{module_name}." if module_name else ""
+            names.extend(prefix + name for name, _ in module.named_parameters())
+    return names
+
+
+def require_trained_hsa(missing_keys, checkpoint_path: str = "") -> None:
+    """Raise if a checkpoint load left any HSA parameter unfilled (``:135-150``)."""
+    missing_hsa = [key for key in missing_keys if _HSA_ATTR in key]
+    if not missing_hsa:
+        return
+    where = f" in {checkpoint_path}" if checkpoint_path else ""
+    raise RuntimeError(
+        f"{len(missing_hsa)} HSA parameters are absent{where}, so this checkpoint has not been "
+        f"through HSA training. Load a checkpoint from the HSA stage, or set attn_backend=flash to "
+        f"run the dense baseline. First missing keys: {missing_hsa[:6]}")
+
+
+# ----------------------------------------------------------------------------------------------
+# Orchestration
+# ----------------------------------------------------------------------------------------------
+class HeadPlan:
+    """Which heads run which branch, as cached device id lists."""
+
+    def __init__(self, heads: int, head_modes: Optional[Sequence[str]], device):
+        modes = list(head_modes) if head_modes is not None else ["both"] * heads
+        if len(modes) != heads or any(m not in _HEAD_MODES for m in modes):
+            raise ValueError(f"head_modes must list one of {_HEAD_MODES} for each of the {heads} heads")
+        self.modes = modes
+        self.both = [h for h, m in enumerate(modes) if m == "both"]
+        self.sparse_only = [h for h, m in enumerate(modes) if m == "sparse"]
+        self.linear_only = [h for h, m in enumerate(modes) if m == "linear"]
+        self.sparse = sorted(self.both + self.sparse_only)
+        self.linear = sorted(self.both + self.linear_only)
+        self.t = {name: (_lib.head_list(lst, device) if lst else None)
+                  for name, lst in (("both", self.both), ("sparse_only", self.sparse_only),
+                                    ("linear_only", self.linear_only), ("sparse", self.sparse),
+                                    ("linear", self.linear))}
+
+
+def elu1_state(k: torch.Tensor, v: torch.Tensor, heads_t: torch.Tensor):
+    """``S^T`` ([B, n, D, D], fp32) and ``z`` ([B, n, D]) of the listed heads (``wa_elu1_state``)."""
+    dev = _lib.require_gpu(k, v)
+    if k.dtype != v.dtype:
+        v = v.to(k.dtype)
+    if k.dtype not in (torch.float32, torch.bfloat16):
+        k, v = k.float(), v.float()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    bsz, length, heads, d = k.shape
+    n = heads_t.numel()
+    state = torch.empty((bsz, n, d, d), dtype=torch.float32, device=dev)
+    zsum = torch.empty((bsz, n, d), dtype=torch.float32, device=dev)
+    ws = torch.empty((_lib.lib().wa_elu1_state_workspace_bytes(bsz, n, length, d),), dtype=torch.uint8, device=dev)
+    kp, k_sb, k_st, k_sh = _lib.blhd(k)
+    vp, v_sb, v_st, v_sh = _lib.blhd(v)
+    args = _lib.Elu1StateArgs(kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh, _lib.dtype_code(k), bsz, heads, length, d,
+                              heads_t.data_ptr(), n, state.data_ptr(), zsum.data_ptr(), ws.data_ptr())
+    _lib.call("wa_elu1_state", args, _lib.stream_ptr(dev))
+    return state, zsum
+
+
+def elu1_readout(q, state, zsum, heads_t, out, *, epilogue=_lib.WA_EPI_PLAIN, gate_w=None, gate_b=None,
+                 gate_pre_bf16=False, gate_out_bf16=False, lin_round_bf16=False):
+    dev = _lib.require_gpu(q, state, out)
+    q = q if q.dtype in (torch.float32, torch.bfloat16) else q.float()
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    bsz, length, heads, d = q.shape
+    qp, q_sb, q_st, q_sh = _lib.blhd(q)
+    op, o_sb, o_st, o_sh = _lib.blhd(out)
+    args = _lib.Elu1ReadoutArgs(qp, q_sb, q_st, q_sh, _lib.dtype_code(q), state.data_ptr(), zsum.data_ptr(),
+                                op, o_sb, o_st, o_sh, _lib.dtype_code(out), bsz, heads, length, d,
+                                heads_t.data_ptr(), heads_t.numel(), epilogue, _lib.ptr(gate_w), _lib.ptr(gate_b),
+                                int(gate_pre_bf16), int(gate_out_bf16), int(lin_round_bf16))
+    _lib.call("wa_elu1_readout", args, _lib.stream_ptr(dev))
+    return out
+
+
+class GateSpec:
+    """Kernel-side view of the fusion gate (``attention.py:246-251``)."""
+
+    def __init__(self, gate_lin: Optional[nn.Module], comp_dtype: torch.dtype):
+        if gate_lin is not None:
+            w = gate_lin.weight
+            self.w = w.detach().to(torch.bfloat16).contiguous()
+            b = getattr(gate_lin, "bias", None)
+            self.b = b.detach().float().contiguous() if b is not None else None
+            self.pre_bf16 = w.dtype == torch.bfloat16
+            self.out_bf16 = w.dtype == torch.bfloat16 or comp_dtype == torch.bfloat16
+        else:
+            self.w, self.b = None, None
+            self.pre_bf16 = comp_dtype == torch.bfloat16
+            self.out_bf16 = comp_dtype == torch.bfloat16
+
+    def kwargs(self):
+        return dict(gate_w=self.w, gate_b=self.b, gate_pre_bf16=self.pre_bf16, gate_out_bf16=self.out_bf16)
+
+
+def _per_head_k(topk, heads: int):
+    if topk is None:
+        raise ValueError("routing='topk' needs topk (an int or one budget per head)")
+    ks = [int(topk)] * heads if isinstance(topk, int) else [int(x) for x in topk]
+    if len(ks) != heads:
+        raise ValueError(f"expected {heads} per-head top-k budgets, got {len(ks)}")
+    return ks
+
+
+def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
+                tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, save=None):
+    """Forward of HSA on the GPU; ``save`` (a dict) receives what the backward needs."""
+    bsz, q_len, heads, head_dim = q.shape
+    kv_len = k.shape[1]
+    dev = _lib.require_gpu(q, k, v, k_coarse, v_coarse)
+    if block_size not in SUPPORTED_BLOCK_SIZES:
+        raise ValueError(f"block_size must be one of {SUPPORTED_BLOCK_SIZES}, got {block_size}")
+    if head_dim not in (64, 128):
+        raise ValueError(f"head_dim must be 64 or 128 for the gfx950 kernels, got {head_dim}")
+    if routing not in _ROUTING_MODES:
+        raise ValueError(f"routing must be one of {_ROUTING_MODES}")
+    if linear_mode not in _LINEAR_MODES:
+        raise ValueError(f"linear_mode must be one of {_LINEAR_MODES}")
+    plan = HeadPlan(heads, head_modes, dev)
+
+    out_dtype = q.dtype
+    if linear_mode == "lowrank":
+        comp_dtype = v_coarse.dtype if v_coarse is not None else v.dtype
+    else:
+        comp_dtype = v.dtype
+    if comp_dtype not in (torch.float32, torch.bfloat16):
+        comp_dtype = torch.float32
+    gate = GateSpec(gate_lin, comp_dtype)
+    lin_round = comp_dtype == torch.bfloat16
+
+    qb = _lib.kernel_ready(q)
+    kb = _lib.kernel_ready(k)
+    vb = _lib.kernel_ready(v)
+    out = torch.empty((bsz, q_len, heads, head_dim), dtype=comp_dtype, device=dev)
+    lin_tmp = torch.empty_like(out) if plan.both else None
+
+    # ---- linear branch -------------------------------------------------------------------
+    if plan.linear:
+        if linear_mode == "lowrank":
+            if k_coarse is None:
+                kc = _compress(k, k_proj_mat, segment_len=proj_segment_len, block_size=block_size, layout="blhd")
+                vc = _compress(v, v_proj_mat, segment_len=proj_segment_len, block_size=block_size, layout="blhd")
+            else:
+                kc, vc = k_coarse, v_coarse
+            kcb, vcb = _lib.kernel_ready(kc), _lib.kernel_ready(vc)
+            if save is not None:
+                save.update(kc=kc, vc=vc)
+            if plan.both:
+                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
+                            heads=plan.t["both"], out=lin_tmp, lq=q_len)
+            if plan.linear_only:
+                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
+                            heads=plan.t["linear_only"], out=out, lq=q_len, epilogue=_lib.WA_EPI_GATED,
+                            attn_round_bf16=lin_round, **gate.kwargs())
+        else:
+            if plan.both:
+                s_b, z_b = elu1_state(k, v, plan.t["both"])
+                elu1_readout(q, s_b, z_b, plan.t["both"], lin_tmp)
+            if plan.linear_only:
+                s_l, z_l = elu1_state(k, v, plan.t["linear_only"])
+                elu1_readout(q, s_l, z_l, plan.t["linear_only"], out, epilogue=_lib.WA_EPI_GATED,
+                             lin_round_bf16=lin_round, **gate.kwargs())
+
+    # ---- sparse branch -------------------------------------------------------------------
+    if plan.sparse:
+        _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+        sp_t = plan.t["sparse"]
+        qp = pool_blhd(q, q_len, nq, block_size, heads=sp_t)
+        kp = pool_blhd(k, kv_len, nkv, block_size, heads=sp_t)
+        if routing == "gini":
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t)
+        else:
+            ks = _per_head_k(topk, heads)
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t)
+        if save is not None:
+            save.update(route=route)
+        if plan.sparse_only:
+            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
+                        heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True)
+        if plan.both:
+            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
+                        heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
+                        x=lin_tmp, attn_round_bf16=True, **gate.kwargs())
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def hsa_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    k_coarse: Optional[torch.Tensor] = None,
+    v_coarse: Optional[torch.Tensor] = None,
+    k_proj_mat: torch.Tensor,
+    v_proj_mat: torch.Tensor,
+    gate_lin: Optional[nn.Module] = None,
+    block_size: int = 64,
+    tau_min: float = 0.35,
+    tau_max: float = 1.0,
+    proj_segment_len: int = 1560,
+    backend: str = "auto",
+    routing: str = "gini",
+    topk=None,
+    head_modes: Optional[Sequence[str]] = None,
+    linear_mode: str = "lowrank",
+) -> torch.Tensor:
+    """Run HSA over ``[B, L, H, D]`` queries, keys and values (``attention.py:153-259``).
+
+    ``k_coarse`` / ``v_coarse`` supply an already-compressed view of the same KV range (the
+    decoding loop's compressed cache); when omitted the compression runs here.
+    """
+    if (k_coarse is None) != (v_coarse is None):
+        raise ValueError("k_coarse and v_coarse must be provided together")
+    bsz, q_len, heads, head_dim = q.shape
+    kv_len = k.shape[1]
+    if q_len <= 0 or kv_len <= 0:
+        raise ValueError("q_len and kv_len must be positive")
+    if k_coarse is not None:
+        if k_coarse.shape[0] != bsz or tuple(k_coarse.shape[2:]) != (heads, head_dim):
+            raise ValueError(
+                f"expected k_coarse shaped [B, Lc, {heads}, {head_dim}], got {tuple(k_coarse.shape)}")
+        if v_coarse.shape != k_coarse.shape:
+            raise ValueError("v_coarse must have the same shape as k_coarse")
+    resolve_backend(backend)
+    cfg = dict(k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=k_proj_mat, v_proj_mat=v_proj_mat,
+               gate_lin=gate_lin, block_size=block_size, tau_min=tau_min, tau_max=tau_max,
+               proj_segment_len=proj_segment_len, routing=routing, topk=topk, head_modes=head_modes,
+               linear_mode=linear_mode)
+    needs_grad = torch.is_grad_enabled() and (
+        any(t is not None and t.requires_grad for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat))
+        or (gate_lin is not None and any(p.requires_grad for p in gate_lin.parameters())))
+    if needs_grad:
+        from ._autograd import hsa_attention_autograd
+        output = hsa_attention_autograd(q, k, v, **cfg)
+    else:
+        output = hsa_forward(q, k, v, **cfg)
+    if distill.distill_enabled() and torch.is_grad_enabled():
+        distill.record_against_dense(output, q, k, v)
+    return output
+
+
+class HSAAttention(nn.Module):
+    """Hybrid Sparse Attention over a KV window (``attention.py:262-380``).
+
+    Owns the low-rank projections ``k_proj_mat`` / ``v_proj_mat`` (``[ceil(seg/block), seg]`` bf16)
+    and the fusion gate ``gate_lin`` (``Linear(D, D)``), all zero until loaded or initialized, so
+    state dicts are interchangeable with the reference's.
+
+    ``block_size`` may be 64 (reference) or 128 (north-star configs). The extension keywords
+    ``routing``, ``topk``, ``head_modes`` and ``linear_mode`` are forwarded to :func:`hsa_attention`.
+    """
+
+    def __init__(self, num_heads: int, head_dim: int, block_size: int = 64, tau_min: float = 0.35,
+                 tau_max: float = 1.0, proj_segment_len: int = 1560, backend: str = "auto", *,
+                 routing: str = "gini", topk=None, head_modes: Optional[Sequence[str]] = None,
+                 linear_mode: str = "lowrank"):
+        super().__init__()
+        if block_size not in SUPPORTED_BLOCK_SIZES:
+            raise ValueError(f"the sparse-branch kernels are specialized for block_size in {SUPPORTED_BLOCK_SIZES}")
+        if proj_segment_len <= 0:
+            raise ValueError(f"proj_segment_len must be positive, got {proj_segment_len}")
+        if routing not in _ROUTING_MODES:
+            raise ValueError(f"routing must be one of {_ROUTING_MODES}")
+        if linear_mode not in _LINEAR_MODES:
+            raise ValueError(f"linear_mode must be one of {_LINEAR_MODES}")
+        if head_modes is not None and (len(head_modes) != num_heads or any(m not in _HEAD_MODES for m in head_modes)):
+            raise ValueError(f"head_modes must list one of {_HEAD_MODES} per head")
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.block_size = block_size
+        self.tau_min = tau_min
+        self.tau_max = tau_max
+        self.proj_segment_len = proj_segment_len
+        self.proj_rank = math.ceil(proj_segment_len / block_size)
+        self.backend = backend
+        self.routing = routing
+        self.topk = topk
+        self.head_modes = list(head_modes) if head_modes is not None else None
+        self.linear_mode = linear_mode
+        self.k_proj_mat = nn.Parameter(torch.zeros((self.proj_rank, proj_segment_len), dtype=torch.bfloat16))
+        self.v_proj_mat = nn.Parameter(torch.zeros((self.proj_rank, proj_segment_len), dtype=torch.bfloat16))
+        self.gate_lin = nn.Linear(head_dim, head_dim, bias=True)
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        """Return every HSA parameter to its zero placeholder (``attention.py:318-329``)."""
+        with torch.no_grad():
+            self.k_proj_mat.zero_()
+            self.v_proj_mat.zero_()
+            self.gate_lin.weight.zero_()
+            self.gate_lin.bias.zero_()
+
+    def coarse_cache_size(self, kv_cache_size: int) -> int:
+        """Compressed slots needed to mirror a token cache of ``kv_cache_size`` (``:331-335``)."""
+        if kv_cache_size <= 0:
+            return 0
+        return math.ceil(kv_cache_size / self.proj_segment_len) * self.proj_rank
+
+    def token_range_to_coarse(self, start_index: int, end_index: int) -> tuple[int, int]:
+        """Map a segment-aligned token range onto compressed-cache slots (``:337-347``)."""
+        if start_index % self.proj_segment_len != 0 or end_index % self.proj_segment_len != 0:
+            raise ValueError(
+                "coarse-cache access requires segment-aligned token indices, got "
+                f"start={start_index}, end={end_index}, proj_segment_len={self.proj_segment_len}")
+        return ((start_index // self.proj_segment_len) * self.proj_rank,
+                (end_index // self.proj_segment_len) * self.proj_rank)
+
+    def compress_kv_cache(self, k: torch.Tensor, v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Compress ``[B, L, H, D]`` keys and values for the compressed cache (``:349-361``)."""
+        if k.shape != v.shape:
+            raise ValueError(f"k and v must match, got {tuple(k.shape)} and {tuple(v.shape)}")
+        if k.ndim != 4:
+            raise ValueError(f"expected [B, L, H, D] tensors, got ndim={k.ndim}")
+        if torch.is_grad_enabled() and (self.k_proj_mat.requires_grad or k.requires_grad or v.requires_grad):
+            from ._autograd import compress_autograd
+            return (compress_autograd(k, self.k_proj_mat, self.proj_segment_len, self.block_size),
+                    compress_autograd(v, self.v_proj_mat, self.proj_segment_len, self.block_size))
+        return (_compress(k, self.k_proj_mat, segment_len=self.proj_segment_len, block_size=self.block_size,
+                          layout="blhd"),
+                _compress(v, self.v_proj_mat, segment_len=self.proj_segment_len, block_size=self.block_size,
+                          layout="blhd"))
+
+    def forward(self, q, k, v, k_coarse=None, v_coarse=None) -> torch.Tensor:
+        return hsa_attention(
+            q, k, v, k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=self.k_proj_mat,
+            v_proj_mat=self.v_proj_mat, gate_lin=self.gate_lin, block_size=self.block_size,
+            tau_min=self.tau_min, tau_max=self.tau_max, proj_segment_len=self.proj_segment_len,
+            backend=self.backend, routing=self.routing, topk=self.topk, head_modes=self.head_modes,
+            linear_mode=self.linear_mode)

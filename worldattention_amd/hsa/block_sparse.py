@@ -1,0 +1,161 @@
+"""Block-sparse attention on the GPU behind the reference's two sparse-branch entry points.
+
+* :func:`block_sparse_attention` — the Triton module's API
+  (``wan/modules/hsa/block_sparse_triton.py:371-382``): ``(q2k_index, q2k_num)`` for inference, or
+  ``block_map`` for the differentiable path (``:353-368``).
+* :func:`block_sparse_attention_reference` — the torch module's API
+  (``wan/modules/hsa/block_sparse_torch.py:16-64``).
+* :func:`map_to_index` — ``block_sparse_triton.py:44-57``.
+
+Both attention entry points run ``wa_bsa_fwd`` (bf16 MFMA, fp32 accumulation); the backward runs
+``wa_bsa_bwd``. Inputs are ``[B, H, N, D]`` padded to the block size, as in the reference.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _lib
+
+__all__ = ["block_sparse_attention", "block_sparse_attention_reference", "map_to_index", "bsa_forward",
+           "bsa_backward"]
+
+
+def map_to_index(block_map: torch.Tensor):
+    """Boolean ``[B, H, Nq, Nkv]`` mask -> ascending ``(index, num)``, index padded with -1."""
+    dev = _lib.require_gpu(block_map)
+    m = block_map.to(torch.bool).contiguous()
+    index = torch.empty(m.shape, dtype=torch.int32, device=dev)
+    num = torch.empty(m.shape[:-1], dtype=torch.int32, device=dev)
+    rows = m.numel() // max(m.shape[-1], 1)
+    _lib.call("wa_map_to_index", m.data_ptr(), rows, m.shape[-1], index.data_ptr(), num.data_ptr(),
+              _lib.stream_ptr(dev))
+    return index, num
+
+
+def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=None, heads=None,
+                out=None, out_dtype=None, want_lse=False, epilogue=_lib.WA_EPI_PLAIN, x=None, gate_w=None,
+                gate_b=None, gate_pre_bf16=False, gate_out_bf16=False, attn_round_bf16=False, lq=None,
+                lkv=None):
+    """Launch ``wa_bsa_fwd`` on bf16 q/k/v in ``layout`` ("bhld" = [B, H, L, D], "blhd" = [B, L, H, D]).
+
+    ``index=None`` attends densely to every key block. Returns ``(out, lse)``.
+    """
+    dev = _lib.require_gpu(q, k, v)
+    strides = _lib.bhld if layout == "bhld" else _lib.blhd
+    if layout == "bhld":
+        bsz, nheads, ltok, d = q.shape
+        lkv_tok = k.shape[2]
+    else:
+        bsz, ltok, nheads, d = q.shape
+        lkv_tok = k.shape[1]
+    lq = ltok if lq is None else lq
+    lkv = lkv_tok if lkv is None else lkv
+    if out is None:
+        shape = (bsz, nheads, ltok, d) if layout == "bhld" else (bsz, ltok, nheads, d)
+        out = torch.empty(shape, dtype=out_dtype or q.dtype, device=dev)
+    lse = torch.empty((bsz, nheads, lq), dtype=torch.float32, device=dev) if want_lse else None
+    qp, q_sb, q_st, q_sh = strides(q)
+    kp, k_sb, k_st, k_sh = strides(k)
+    vp, v_sb, v_st, v_sh = strides(v)
+    op, o_sb, o_st, o_sh = strides(out)
+    if x is not None:
+        xp, x_sb, x_st, x_sh = strides(x)
+        x_dt = _lib.dtype_code(x)
+    else:
+        xp, x_sb, x_st, x_sh, x_dt = None, 0, 0, 0, 0
+    width = index.shape[-1] if index is not None else 0
+    args = _lib.BsaFwdArgs(
+        qp, q_sb, q_st, q_sh, kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh,
+        op, o_sb, o_st, o_sh, _lib.dtype_code(out), _lib.ptr(lse),
+        _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
+        _lib.ptr(heads), 0 if heads is None else heads.numel(),
+        bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
+        xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
+        int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16))
+    _lib.call("wa_bsa_fwd", args, _lib.stream_ptr(dev))
+    return out, lse
+
+
+def _check_padded(q, k, index, num, block_size):
+    if q.dim() != 4 or k.dim() != 4:
+        raise ValueError("expected [B, H, N, D] tensors")
+    if q.shape[2] % block_size or k.shape[2] % block_size:
+        raise ValueError(f"token counts must be multiples of the block size {block_size}")
+    nq = q.shape[2] // block_size
+    if index.shape[:3] != (q.shape[0], q.shape[1], nq) or num.shape != (q.shape[0], q.shape[1], nq):
+        raise ValueError("q2k_index / q2k_num do not match the query blocks")
+
+
+def _prep(t):
+    return _lib.kernel_ready(t, torch.bfloat16)
+
+
+class _BlockSparseAttention(torch.autograd.Function):
+    """Differentiable block-sparse attention (reference ``block_sparse_triton.py:353-368``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, index, num, block_sizes, block_size):
+        qb, kb, vb = _prep(q), _prep(k), _prep(v)
+        out, lse = bsa_forward(qb, kb, vb, index=index, num=num, block_size=block_size,
+                               block_sizes=block_sizes, out_dtype=torch.bfloat16, want_lse=True)
+        ctx.save_for_backward(qb, kb, vb, out, lse, index, num, block_sizes)
+        ctx.block_size = block_size
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        return out.to(q.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        qb, kb, vb, out, lse, index, num, block_sizes = ctx.saved_tensors
+        dq, dk, dv = bsa_backward(qb, kb, vb, out, lse, grad_out, index=index, num=num,
+                                  block_size=ctx.block_size, block_sizes=block_sizes)
+        qd, kd, vd = ctx.dtypes
+        return dq.to(qd), dk.to(kd), dv.to(vd), None, None, None, None
+
+
+def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_sizes=None, layout="bhld",
+                 heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None):
+    """Gradients of :func:`bsa_forward` (``wa_bsa_bwd``)."""
+    from . import _bwd
+    return _bwd.bsa_backward(q, k, v, out, lse, grad_out, index=index, num=num, block_size=block_size,
+                             block_sizes=block_sizes, layout=layout, heads=heads, lq=lq, lkv=lkv,
+                             dq=dq, dk=dk, dv=dv)
+
+
+def block_sparse_attention(q, k, v, *, block_sizes, q2k_index=None, q2k_num=None, block_map=None):
+    """Block-sparse attention over ``[B, H, N, D]`` tensors padded to the block size.
+
+    Pass ``block_map`` for a differentiable call, or ``(q2k_index, q2k_num)`` for inference.
+    Returns ``[B, H, N, D]`` in ``q.dtype``.
+    """
+    _lib.require_gpu(q, k, v)
+    block_size = k.shape[2] // block_sizes.numel()
+    if block_map is not None:
+        index, num = map_to_index(block_map)
+        _check_padded(q, k, index, num, block_size)
+        return _BlockSparseAttention.apply(q, k, v, index, num, block_sizes.to(torch.int32).contiguous(),
+                                           block_size)
+    if q2k_index is None or q2k_num is None:
+        raise ValueError("provide either block_map or both q2k_index and q2k_num")
+    return block_sparse_attention_reference(q, k, v, q2k_index, q2k_num, block_sizes, block_size)
+
+
+def block_sparse_attention_reference(q, k, v, q2k_index, q2k_num, block_sizes, block_size: int):
+    """Attention over selected blocks for ``[B, H, N, D]`` inputs padded to ``block_size``.
+
+    Same contract as ``block_sparse_torch.py:16-64`` (first ``num`` slots, ids clamped, partial
+    block masked, empty rows 0, result in ``q.dtype``), computed by the HIP kernel (bf16 operands,
+    fp32 accumulation). Differentiable in q, k, v.
+    """
+    _lib.require_gpu(q, k, v)
+    index = q2k_index.to(torch.int32).contiguous()
+    num = q2k_num.to(torch.int32).contiguous()
+    _check_padded(q, k, index, num, block_size)
+    sizes = block_sizes.to(device=q.device, dtype=torch.int32).contiguous()
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _BlockSparseAttention.apply(q, k, v, index, num, sizes, block_size)
+    out, _ = bsa_forward(_prep(q), _prep(k), _prep(v), index=index, num=num, block_size=block_size,
+                         block_sizes=sizes, out_dtype=torch.bfloat16)
+    return out.to(q.dtype)
