@@ -105,7 +105,16 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * Epilogue (per element, gate g = sigmoid(q . gate_w[d] + gate_b[d]) or sigmoid(q) when gate_w
  * is NULL, optionally rounded to bf16 before/after the sigmoid):
  *   PLAIN: o = attn;  FUSE: o = attn + g * x;  GATED: o = g * attn
- * — the gated fusion of attention.py:246-254 done in registers. */
+ * — the gated fusion of attention.py:246-254 done in registers.
+ *
+ * Work is split into units of at most split_visits consecutive list entries (0 = default) per
+ * (row = b, head, query block); partial results go to `workspace` and a second kernel merges them
+ * in split order (results do not depend on scheduling). max_visits (0 = index_width) must bound
+ * every row's num: visits past max_visits are not computed. units (optional, device int32
+ * [n_units][2] = (row, split)) lists the units to launch, in launch order; it must contain every
+ * split of every row with num > 0 (rows are numbered (b * n_heads + head_slot) * Nq + i). Without
+ * it every (row, split < ceil(max_visits / split_visits)) is launched. */
+#define WA_BSA_DEFAULT_SPLIT 8
 typedef struct wa_bsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;
@@ -121,7 +130,13 @@ typedef struct wa_bsa_fwd_args {
   const void* x; int64_t x_sb, x_st, x_sh; int32_t x_dtype;
   const void* gate_w; const float* gate_b;
   int32_t gate_pre_bf16, gate_out_bf16, attn_round_bf16;
+  void* workspace;
+  const int32_t* units; int64_t n_units;
+  int64_t max_visits; int32_t split_visits;
 } wa_bsa_fwd_args;
+/* Workspace bytes for rows = B * n_heads * ceil(Lq / block_size) rows. */
+int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t split_visits, int64_t block_size,
+                                   int64_t D);
 int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */

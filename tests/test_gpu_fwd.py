@@ -263,3 +263,32 @@ def test_coarse_cache_equals_inline_compression_on_gpu():
         kc, vc = hsa.compress_kv_cache(k, v)
         cached = hsa(q, k, v, k_coarse=kc, v_coarse=vc)
     assert torch.allclose(inline, cached, atol=1e-5)
+
+
+@pytest.mark.parametrize("use_visits", [False, True])
+@pytest.mark.parametrize("split", [1, 3, 8])
+def test_bsa_head_subset_split_units_match_oracle(use_visits, split):
+    """A launch over a subset of heads (rows numbered by head slot) with lists cut into several
+    split units; index / num are laid out by global head, as the routing writes them."""
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(split)
+    bs, d, b, h, nq, nkv = 128, 128, 2, 4, 3, 11
+    lq, lkv = nq * bs - 50, nkv * bs - 70
+    q = torch.randn(b, lq, h, d).bfloat16()
+    k = torch.randn(b, lkv, h, d).bfloat16()
+    v = torch.randn(b, lkv, h, d).bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    ks = [0, 5, 0, 11]
+    num = torch.tensor(ks, dtype=torch.int32).view(1, h, 1).expand(b, h, nq).contiguous()
+    heads = torch.tensor([3, 1], dtype=torch.int32)
+    out = torch.zeros(b, lq, h, d, dtype=torch.float32, device=DEV)
+    bsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), index=index.to(DEV), num=num.to(DEV), block_size=bs,
+                layout="blhd", heads=heads.to(DEV), out=out, lq=lq, lkv=lkv, split=split,
+                visits=[ks[3], ks[1]] if use_visits else None)
+    qp = O.pad_to_len(q, nq * bs).transpose(1, 2)
+    kp, vp = (O.pad_to_len(t, nkv * bs).transpose(1, 2) for t in (k, v))
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    want = O.block_sparse_attention(qp.float(), kp.float(), vp.float(), index, num, sizes, bs).transpose(1, 2)[:, :lq]
+    for hh in (1, 3):
+        assert_close(out[:, :, hh], want[:, :, hh], what=f"head {hh} split {split}")
+    assert torch.count_nonzero(out[:, :, 0]) == 0 and torch.count_nonzero(out[:, :, 2]) == 0

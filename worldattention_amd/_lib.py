@@ -54,7 +54,11 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
     ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
     ("gate_w", c_void_p), ("gate_b", c_void_p),
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("attn_round_bf16", c_int32),
+    ("workspace", c_void_p), ("units", c_void_p), ("n_units", c_int64),
+    ("max_visits", c_int64), ("split_visits", c_int32),
 ])
+
+BSA_DEFAULT_SPLIT = 8
 
 CompressArgs = _struct("wa_compress_args", [
     ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
@@ -92,6 +96,7 @@ SIGNATURES = {
     "wa_route_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_route": (c_int, [POINTER(RouteArgs), c_void_p]),
     "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "wa_bsa_fwd_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_compress_kv": (c_int, [POINTER(CompressArgs), c_void_p]),
     "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),

@@ -315,13 +315,16 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
             route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t)
         if save is not None:
             save.update(route=route)
+        # top-k routing fixes every row's visit count on the host: launch exactly those units
+        vis_of = (lambda hl: [min(ks[h], nkv) for h in hl]) if routing == "topk" else (lambda hl: None)
         if plan.sparse_only:
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
-                        heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True)
+                        heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True,
+                        visits=vis_of(plan.sparse_only))
         if plan.both:
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
                         heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
-                        x=lin_tmp, attn_round_bf16=True, **gate.kwargs())
+                        x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), **gate.kwargs())
     return out if out.dtype == out_dtype else out.to(out_dtype)
 
 

@@ -35,13 +35,39 @@ def map_to_index(block_map: torch.Tensor):
     return index, num
 
 
+_UNIT_CACHE: dict = {}
+
+
+def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[torch.Tensor, int]:
+    """Device ``[n, 2]`` int32 list of (row, split) units when every row's visit count is known on
+    the host (top-k routing: ``num = min(k_h, Nkv)``), ordered head by head so that consecutive
+    units — which the kernel places on the same XCD — share key blocks. Cached per shape."""
+    key = (str(device), bsz, tuple(visits_per_slot), nq, split)
+    hit = _UNIT_CACHE.get(key)
+    if hit is None:
+        units = []
+        n_slots = len(visits_per_slot)
+        for b in range(bsz):
+            for hs, nv in enumerate(visits_per_slot):
+                ns = -(-int(nv) // split) if nv > 0 else 0
+                for qb in range(nq):
+                    row = (b * n_slots + hs) * nq + qb
+                    units.extend((row, sp) for sp in range(ns))
+        t = torch.tensor(units if units else [(0, 0)], dtype=torch.int32, device=device).view(-1, 2)
+        hit = (t, len(units))
+        _UNIT_CACHE[key] = hit
+    return hit
+
+
 def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=None, heads=None,
                 out=None, out_dtype=None, want_lse=False, epilogue=_lib.WA_EPI_PLAIN, x=None, gate_w=None,
                 gate_b=None, gate_pre_bf16=False, gate_out_bf16=False, attn_round_bf16=False, lq=None,
-                lkv=None):
+                lkv=None, visits=None, split=None):
     """Launch ``wa_bsa_fwd`` on bf16 q/k/v in ``layout`` ("bhld" = [B, H, L, D], "blhd" = [B, L, H, D]).
 
-    ``index=None`` attends densely to every key block. Returns ``(out, lse)``.
+    ``index=None`` attends densely to every key block. ``visits`` (optional) gives each launched
+    head's exact visit count ``min(num, width)`` when the host knows it (top-k routing): the launch
+    then covers exactly the needed (row, split) units. Returns ``(out, lse)``.
     """
     dev = _lib.require_gpu(q, k, v)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -66,15 +92,30 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         x_dt = _lib.dtype_code(x)
     else:
         xp, x_sb, x_st, x_sh, x_dt = None, 0, 0, 0, 0
-    width = index.shape[-1] if index is not None else 0
+    nkv = -(-lkv // block_size)
+    nq = -(-lq // block_size)
+    width = index.shape[-1] if index is not None else nkv
+    n_slots = heads.numel() if heads is not None else nheads
+    split = int(split or _lib.BSA_DEFAULT_SPLIT)
+    units, n_units, max_visits = None, 0, width
+    if visits is not None:
+        vis = [max(0, min(int(n), width)) for n in visits]
+        if len(vis) != n_slots:
+            raise ValueError(f"visits lists {len(vis)} heads, launch has {n_slots}")
+        units, n_units = unit_table(bsz, vis, nq, split, dev)
+        max_visits = max(max(vis), 1)
+    rows = bsz * n_slots * nq
+    ws_bytes = _lib.lib().wa_bsa_fwd_workspace_bytes(rows, max_visits, split, block_size, d)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     args = _lib.BsaFwdArgs(
         qp, q_sb, q_st, q_sh, kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh,
         op, o_sb, o_st, o_sh, _lib.dtype_code(out), _lib.ptr(lse),
         _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
-        _lib.ptr(heads), 0 if heads is None else heads.numel(),
+        _lib.ptr(heads), n_slots if heads is not None else 0,
         bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
         xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
-        int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16))
+        int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16),
+        ws.data_ptr(), _lib.ptr(units), n_units, max_visits, split)
     _lib.call("wa_bsa_fwd", args, _lib.stream_ptr(dev))
     return out, lse
 
