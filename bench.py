@@ -103,9 +103,13 @@ def main():
     plan = WA.HeadPlan(q.shape[2], cfg["head_modes"], dev)
     out = torch.empty_like(q)
 
+    nkv = -(-k.shape[1] // cfg["block_size"])
+    visits = [min(cfg["topk"][h], nkv) for h in plan.sparse_only]
+
     def sparse_only():
         bsa_forward(q, k, v, index=route.index, num=route.num, block_size=cfg["block_size"], layout="blhd",
-                    heads=plan.t["sparse_only"], out=out, lq=q.shape[1], lkv=k.shape[1], attn_round_bf16=True)
+                    heads=plan.t["sparse_only"], out=out, lq=q.shape[1], lkv=k.shape[1], attn_round_bf16=True,
+                    visits=visits)
 
     for _ in range(3):
         sparse_only()

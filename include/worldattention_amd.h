@@ -114,7 +114,7 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * [n_units][2] = (row, split)) lists the units to launch, in launch order; it must contain every
  * split of every row with num > 0 (rows are numbered (b * n_heads + head_slot) * Nq + i). Without
  * it every (row, split < ceil(max_visits / split_visits)) is launched. */
-#define WA_BSA_DEFAULT_SPLIT 8
+#define WA_BSA_DEFAULT_SPLIT 16
 typedef struct wa_bsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;
@@ -157,7 +157,8 @@ int wa_compress_kv(const wa_compress_args* args, void* stream);
 
 /* Kernelized linear attention state (north star, no reference counterpart):
  * state[b,s,d,e] = sum_t v[t,d] * phi(k[t,e]) and zsum[b,s,e] = sum_t phi(k[t,e]) with
- * phi(x) = elu(x) + 1, for each listed head heads[s] (fp32 outputs, [B, n_heads, D, D] / [B, n_heads, D]). */
+ * phi(x) = elu(x) + 1, for each listed head heads[s] (fp32 outputs, [B, n_heads, D, D] / [B, n_heads, D]);
+ * D in {64, 128}, k/v bf16 or fp32. Chunk partials are summed in a fixed order (reproducible). */
 typedef struct wa_elu1_state_args {
   const void* k; int64_t k_sb, k_st, k_sh;
   const void* v; int64_t v_sb, v_st, v_sh;

@@ -160,10 +160,11 @@ def test_lowrank_linear_branch_matches_oracle():
     assert_close(got, O.linear_branch_lowrank(q, kc, vc), what="lowrank")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("d", [64, 128])
-def test_elu1_linear_branch_matches_oracle(d):
+def test_elu1_linear_branch_matches_oracle(d, dtype):
     torch.manual_seed(d)
-    q, k, v = (torch.randn(1, n, 4, d).bfloat16() for n in (700, 5000, 5000))
+    q, k, v = (torch.randn(1, n, 4, d).to(dtype) for n in (700, 5000, 5000))
     heads = torch.tensor([0, 2, 3], dtype=torch.int32, device=DEV)
     s, z = WA.elu1_state(k.to(DEV), v.to(DEV), heads)
     out = torch.zeros(1, 700, 4, d, dtype=torch.float32, device=DEV)

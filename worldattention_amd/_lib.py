@@ -58,7 +58,7 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
     ("max_visits", c_int64), ("split_visits", c_int32),
 ])
 
-BSA_DEFAULT_SPLIT = 8
+BSA_DEFAULT_SPLIT = 16
 
 CompressArgs = _struct("wa_compress_args", [
     ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
@@ -194,7 +194,7 @@ _HEAD_CACHE: dict = {}
 
 
 def head_list(heads, device: torch.device) -> torch.Tensor:
-    """Device int32 tensor of head ids, cached per (device, heads)."""
+    """Device int32 tensor of a small host int list (head ids, per-head budgets), cached per value."""
     key = (str(device), tuple(int(h) for h in heads))
     t = _HEAD_CACHE.get(key)
     if t is None:

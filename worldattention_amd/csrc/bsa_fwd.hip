@@ -16,7 +16,7 @@
 // the probabilities feed the PV product straight from the QK accumulator registers.
 //
 // LDS layouts (no padding; XOR swizzles on 16-byte chunks keep every read conflict-free):
-//   K[key][chunk ^ (key & 7)]        read with ds_read_b128 (8 lanes = 8 keys, one chunk)
+//   K[key][chunk ^ (key & 15)]      read with ds_read_b128 (16 lanes = 16 keys, one chunk; D = 128)
 //   V[key][chunk ^ 2*(key & 3)]      read with ds_read_b64_tr_b16 (16 lanes = 4 keys x 32 bytes)
 //
 // Reference semantics: wan/modules/hsa/block_sparse_triton.py:67-139 (online softmax, partial
@@ -74,42 +74,243 @@ __device__ __forceinline__ int block_real(const FwdParams& p, int j, int BS) {
   return max(real, 0);
 }
 
-// Streams one [BS, D] bf16 tile (rows j*BS .. of head h) into swizzled LDS. One wave instruction
-// moves 1 KiB = RPI rows; the XOR swizzle of a row only depends on the row's position within its
-// instruction, so every lane keeps one source offset for the whole tile. Rows at or past `real`
-// (the trailing partial block) re-read row 0 of the block: finite data that is masked (K) or
-// multiplied by a zero probability (V), and nothing outside the tensor is touched.
-template <int D, int BS, bool IS_V>
-__device__ __forceinline__ int dma_lane_chunk(int w, int lane) {
+// 16-byte chunk swizzles. gfx950 serves a 128-bit LDS read 16 lanes (256 bytes, all 64 banks)
+// per cycle, and the transpose read 16 lanes x 8 bytes (128 bytes) per cycle:
+//   K row r, D = 128 (256-byte rows): chunk ^ (r & 15) — 16 consecutive keys hit 16 distinct
+//     chunk slots of their rows, i.e. all 64 banks;
+//   K row r, D = 64 (128-byte rows, two per bank line): chunk ^ ((r >> 1) & 7);
+//   V row r: chunk ^ 2 (r & 3) — a transpose read's 16 lanes cover 4 rows x 32 bytes, which this
+//     spreads over 4 x 8 distinct banks.
+template <int D>
+__device__ __forceinline__ int k_swizzle(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+__device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
+
+// Streams one [64, D] bf16 step tile (64 consecutive key rows starting at `tile`) into swizzled
+// LDS. One wave instruction moves 1 KiB = RPI whole rows; lane L of instruction i writes row
+// r0(i) + L / CPR, slot L % CPR, and so reads the chunk that the swizzle stores in that slot.
+// Rows at or past `real` (the end of a trailing partial block) re-read the tile's row 0: finite
+// data that is masked (K) or multiplied by a zero probability (V); nothing outside the tensor is
+// read.
+template <int D, int NW, bool IS_V>
+__device__ __forceinline__ void dma_one(bf16_t* lds, const bf16_t* tile, int64_t st, int real, int w, int lane,
+                                        int i) {
   constexpr int CPR = D / 8;            // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;         // rows per wave instruction (4 or 8)
   const int rin = lane / CPR, pos = lane % CPR;
-  const int sw = IS_V ? 2 * (rin & 3) : (rin + (RPI == 4 ? 4 * (w & 1) : 0)) & 7;
-  return pos ^ sw;
+  const int r0 = (i * NW + w) * RPI;
+  const int row = r0 + rin;
+  const int chunk = pos ^ (IS_V ? v_swizzle(row) : k_swizzle<D>(row));
+  const int src = real >= 64 || row < real ? row : 0;
+  __builtin_amdgcn_global_load_lds((const void*)(tile + (int64_t)src * st + chunk * 8), WA_LDS(lds + r0 * D), 16,
+                                   0, 0);
 }
 
-template <int D, int BS>
-__device__ __forceinline__ void dma_tile(bf16_t* lds, const bf16_t* tile, int64_t st, uint32_t lane_off,
-                                         int chunk, int real, int w, int lane) {
-  constexpr int CPR = D / 8;
-  constexpr int RPI = 64 / CPR;
-  constexpr int NW = BS / 32;
-  constexpr int NI = BS / (RPI * NW);   // instructions per wave
-  if (real >= BS) {
+// The next step's tile stream, issued one instruction at a time from inside the current step's
+// MFMA loops so that a full memory queue stalls the wave between products rather than in a burst.
+template <int D, int NW>
+struct NextTile {
+  static constexpr int NI = 64 / ((64 / (D / 8)) * NW);  // instructions per wave per tensor
+  bf16_t* k_lds; bf16_t* v_lds;
+  const bf16_t* k_tile; const bf16_t* v_tile;
+  int64_t k_st, v_st;
+  int real;
+  bool valid;
+  __device__ __forceinline__ void k(int i, int w, int lane) const {
+    if (valid && i < NI) dma_one<D, NW, false>(k_lds, k_tile, k_st, real, w, lane, i);
+  }
+  __device__ __forceinline__ void v(int i, int w, int lane) const {
+    if (valid && i < NI) dma_one<D, NW, true>(v_lds, v_tile, v_st, real, w, lane, i);
+  }
+};
+
+// Writes one query column's result (lane = query qi, accumulator layout d = 32t + 8(r/4) + 4g +
+// r%4) with the fusion epilogue:
+//   PLAIN: o = attn;  FUSE: o = attn + g * x;  GATED: o = g * attn,
+// g = sigmoid(q . gate_w[d] + gate_b[d]) (or sigmoid(q) without gate_w): the gated fusion of
+// attention.py:246-254, in registers.
+template <int D>
+__device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&acc)[D / 32], float inv,
+                                             const bf16x8 (&qf)[D / 16], const bf16_t* qrow, int b, int h,
+                                             int qi, bool q_ok, int g, int l32) {
+  constexpr int DC = D / 16, DT = D / 32;
+  const bool need_gate = p.epilogue != WA_EPI_PLAIN;
+  f32x16 gacc[DT];
+  if (need_gate && p.gate_w) {
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int r0 = (i * NW + w) * RPI;
-      __builtin_amdgcn_global_load_lds((const void*)(tile + (int64_t)r0 * st + lane_off), WA_LDS(lds + r0 * D),
-                                       16, 0, 0);
+    for (int t = 0; t < DT; ++t) {
+      gacc[t] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const bf16x8 a = *(const bf16x8*)(p.gate_w + (t * 32 + l32) * D + c * 16 + g * 8);
+        gacc[t] = wa_mfma32(a, qf[c], gacc[t]);
+      }
     }
-  } else {
-    const int rin = lane / CPR;
+  }
+  if (!q_ok) return;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int r0 = (i * NW + w) * RPI;
-      const int row = r0 + rin;
-      const bf16_t* g = tile + (int64_t)(row < real ? row : 0) * st + chunk * 8;
-      __builtin_amdgcn_global_load_lds((const void*)g, WA_LDS(lds + r0 * D), 16, 0, 0);
+  for (int t = 0; t < DT; ++t) {
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = t * 32 + 8 * rq + 4 * g;
+      float val[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = acc[t][rq * 4 + i] * inv;
+        if (p.attn_round_bf16) a = wa_bf16_round(a);
+        val[i] = a;
+      }
+      if (need_gate) {
+        float gv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float pre = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f) : (float)qrow[d0 + i];
+          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
+          float gs = wa_sigmoid(pre);
+          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
+          gv[i] = gs;
+        }
+        if (p.epilogue == WA_EPI_FUSE) {
+          const int64_t xo = (int64_t)b * p.x_sb + (int64_t)qi * p.x_st + (int64_t)h * p.x_sh + d0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) val[i] = __fadd_rn(val[i], __fmul_rn(wa_load_f(p.x, xo + i, p.x_dtype), gv[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) val[i] = __fmul_rn(val[i], gv[i]);
+        }
+      }
+      const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + d0;
+      if (p.o_dtype == WA_BF16) {
+        bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
+        *(bf16x4*)((bf16_t*)p.o + oo) = ov;
+      } else {
+        f32x4 ov = {val[0], val[1], val[2], val[3]};
+        *(f32x4*)((float*)p.o + oo) = ov;
+      }
+    }
+  }
+}
+
+// Step cursor over the unit's visits: a visit of a BS = 128 block is two 64-key steps (the second
+// only when the block has more than 64 real keys), of a BS = 64 block one step. All fields are
+// wave-uniform.
+struct Cursor {
+  uint64_t todo;  // visits not yet started (bit = lane holding the visit)
+  int j, real;    // current block and its real key count
+  int half;       // current 64-key step within the block
+  bool valid;
+};
+
+template <int BS>
+__device__ __forceinline__ void cursor_next(Cursor& c, int my_j, int my_real) {
+  if (BS == 128 && c.valid && c.half == 0 && c.real > 64) {
+    c.half = 1;
+    return;
+  }
+  if (c.todo) {
+    const int v = __builtin_ctzll(c.todo);
+    c.todo &= c.todo - 1;
+    c.j = __builtin_amdgcn_readlane(my_j, v);
+    c.real = __builtin_amdgcn_readlane(my_real, v);
+    c.half = 0;
+    c.valid = true;
+  } else {
+    c.valid = false;
+  }
+}
+
+// One 64-key step of the online softmax on LDS buffer (kb, vb): S^T = K Q^T, lazily rescaled
+// exponentials, O^T += V^T P^T. `real` = real keys of this step (1..64). The next step's tile
+// stream (`nt`) is issued in slices between the products.
+template <int D, int NW>
+__device__ __forceinline__ void attend_step(const bf16_t* kb, const bf16_t* vb, const int (&k_rd)[D / 16],
+                                            const int (&v_rd)[2], const bf16x8 (&qf)[D / 16],
+                                            f32x16 (&oacc)[D / 32], float& m_i, float& l_i, int real, int g,
+                                            float scale_log2, const NextTile<D, NW>& nt, int w, int lane) {
+  constexpr int KT = 2, DC = D / 16, DT = D / 32, PC = 4;
+  constexpr int NI = NextTile<D, NW>::NI;
+  f32x16 sacc[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) sacc[kt] = f32x16{};
+  bf16x8 ka[KT], kn[KT];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) ka[kt] = *(const bf16x8*)(kb + k_rd[0] + kt * 32 * D);
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    if (c + 1 < DC) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) kn[kt] = *(const bf16x8*)(kb + k_rd[c + 1] + kt * 32 * D);
+    }
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) sacc[kt] = wa_mfma32(ka[kt], qf[c], sacc[kt]);
+    if (c % (DC / NI > 0 ? DC / NI : 1) == 0) nt.k(c / (DC / NI > 0 ? DC / NI : 1), w, lane);
+    if (c + 1 < DC) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) ka[kt] = kn[kt];
+    }
+  }
+  if (DC < NI) {
+#pragma unroll
+    for (int i = DC; i < NI; ++i) nt.k(i, w, lane);
+  }
+  if (real < 64) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (key >= real) sacc[kt][r] = -INFINITY;
+      }
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+  // Lazy rescale: keep the running max unless the step max exceeds it by more than 8 (so every
+  // exponential stays <= 2^8); the final normalization uses the same max, so results are exact.
+  if (__any(mx > m_i + 8.f)) {
+    const float m_new = mx > m_i + 8.f ? mx : m_i;
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+    l_i *= alpha;
+    m_i = m_new;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+  }
+  float rs = 0.f;
+  bf16x8 pb[PC];
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], scale_log2, -m_i));
+      rs += pv;
+      pb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)pv;
+    }
+  }
+  l_i += rs;
+#pragma unroll
+  for (int c = 0; c < PC; ++c) {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      bf16x8 a;
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const s16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            WA_LDS4(vb + v_rd[t & 1] + (16 * c + 8 * hf) * D + (t >> 1) * 64));
+        const bf16x4 vb4 = __builtin_bit_cast(bf16x4, vv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[4 * hf + e] = vb4[e];
+      }
+      oacc[t] = wa_mfma32(a, pb[c], oacc[t]);
+    }
+    if (NI >= PC) {
+#pragma unroll
+      for (int i = c * (NI / PC); i < (c + 1) * (NI / PC); ++i) nt.v(i, w, lane);
+    } else if (c < NI) {
+      nt.v(c, w, lane);
     }
   }
 }
@@ -117,15 +318,15 @@ __device__ __forceinline__ void dma_tile(bf16_t* lds, const bf16_t* tile, int64_
 template <int D, int BS>
 __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2)))
 bsa_unit_kernel(FwdParams p) {
-  constexpr int NW = BS / 32;
-  constexpr int KT = BS / 32;   // 32-key tiles per key block
-  constexpr int DC = D / 16;    // 16-wide chunks of the QK contraction
-  constexpr int DT = D / 32;    // 32-wide output tiles of O^T
-  constexpr int PC = BS / 16;   // 16-key chunks of the PV contraction
-  constexpr int CPR = D / 8;
-  constexpr int NI = D / 16;    // DMA instructions per wave per tile
-  __shared__ __attribute__((aligned(1024))) bf16_t k_lds[BS * D];
-  __shared__ __attribute__((aligned(1024))) bf16_t v_lds[BS * D];
+  constexpr int NW = BS / 32;   // waves; wave w owns query rows [32w, 32w + 32)
+  constexpr int DC = D / 16, DT = D / 32;
+  constexpr int TILE = 64 * D;  // elements of one K (or V) step tile
+  // Two step buffers, four distinct arrays so the compiler can tell the in-flight stream of one
+  // buffer from the reads of the other.
+  __shared__ __attribute__((aligned(1024))) bf16_t k0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t v0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t k1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t v1[TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -152,6 +353,7 @@ bsa_unit_kernel(FwdParams p) {
   const int s_begin = split * p.split;
   const int s_end = min(n, s_begin + p.split);
   if (s_begin >= s_end) return;  // unit beyond this row's list (an empty row is all zero)
+  const int ns = min((n + p.split - 1) / p.split, p.max_splits);
 
   const int qi = qb * BS + w * 32 + l32;
   const bool q_ok = qi < p.Lq;
@@ -159,159 +361,101 @@ bsa_unit_kernel(FwdParams p) {
   const bf16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
 
   // Q^T fragments (B operand): lane holds Q[qi, 16c + 8g .. +8).
+  const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
   bf16x8 qf[DC];
-  {
-    const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
-      qf[c] = q_ok ? t : bf16x8{};
-    }
+  for (int c = 0; c < DC; ++c) {
+    bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
+    qf[c] = q_ok ? t : bf16x8{};
   }
 
-  // This unit's list entries, one per lane (split <= 64), read once: the loop below fetches them
-  // with readlane and issues no memory reads besides the tile streams.
+  // This unit's list entries, one per lane (split <= 64), read once: the loop fetches them with
+  // readlane and issues no memory reads besides the tile streams.
   const int cnt = s_end - s_begin;
   int my_j = 0, my_real = 0;
   if (lane < cnt) {
     my_j = p.index ? min(max(p.index[irow * p.index_width + s_begin + lane], 0), p.Nkv - 1) : s_begin + lane;
     my_real = block_real(p, my_j, BS);
   }
-  uint64_t todo = __ballot(lane < cnt && my_real > 0);  // visits with at least one real key
+  Cursor cur{__ballot(lane < cnt && my_real > 0), 0, 0, 0, false};
+  cursor_next<BS>(cur, my_j, my_real);
 
-  const int k_chunk = dma_lane_chunk<D, BS, false>(w, lane);
-  const int v_chunk = dma_lane_chunk<D, BS, true>(w, lane);
-  const uint32_t k_off = (uint32_t)((lane / CPR) * p.k_st + k_chunk * 8);
-  const uint32_t v_off = (uint32_t)((lane / CPR) * p.v_st + v_chunk * 8);
-
-  int j = 0, real = 0;
-  if (todo) {
-    const int cur = __builtin_ctzll(todo);
-    todo &= todo - 1;
-    j = __builtin_amdgcn_readlane(my_j, cur);
-    real = __builtin_amdgcn_readlane(my_real, cur);
-    dma_tile<D, BS>(k_lds, kbase + (int64_t)j * BS * p.k_st, p.k_st, k_off, k_chunk, real, w, lane);
-    dma_tile<D, BS>(v_lds, vbase + (int64_t)j * BS * p.v_st, p.v_st, v_off, v_chunk, real, w, lane);
+  auto next_tile = [&](bf16_t* kl, bf16_t* vl, const Cursor& c) {
+    NextTile<D, NW> nt;
+    const int64_t r0 = (int64_t)c.j * BS + 64 * c.half;
+    nt.k_lds = kl; nt.v_lds = vl;
+    nt.k_tile = kbase + r0 * p.k_st; nt.v_tile = vbase + r0 * p.v_st;
+    nt.k_st = p.k_st; nt.v_st = p.v_st;
+    nt.real = c.real - 64 * c.half;
+    nt.valid = c.valid;
+    return nt;
+  };
+  if (cur.valid) {
+    const NextTile<D, NW> first = next_tile(k0, v0, cur);
+#pragma unroll
+    for (int i = 0; i < NextTile<D, NW>::NI; ++i) {
+      first.k(i, w, lane);
+      first.v(i, w, lane);
+    }
   }
+
+  // Per-lane LDS read offsets (elements). K (A operand of S^T = K Q^T): lane reads row kt*32 + l32,
+  // chunk 2c + g, stored in slot (2c + g) ^ k_swizzle(l32) (the swizzle of kt*32 + l32 equals
+  // that of l32).
+  int k_rd[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) k_rd[c] = l32 * D + ((2 * c + g) ^ k_swizzle<D>(l32)) * 8;
+  // V (A operand of O^T += V^T P^T via transpose reads): 16-lane group G, source lane j = 4r + q
+  // reads 4 elements of row 16c + 4(G/2) + 8hf + r at column 32t + 16(G%2) + 4q, whose chunk is
+  // swizzled by 2r: 8 (t / 2) + ((4 (t % 2) + 2 (G % 2) + q / 2) ^ 2r).
+  const int G = lane >> 4, tr_r = (lane & 15) >> 2, tr_q = lane & 3;
+  int v_rd[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    v_rd[t] = (4 * (G >> 1) + tr_r) * D + (((4 * t + 2 * (G & 1) + (tr_q >> 1)) ^ (2 * tr_r)) * 8) + 4 * (tr_q & 1);
 
   f32x16 oacc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
   float m_i = -INFINITY, l_i = 0.f;
 
-  // Per-lane LDS read bases. K (A operand of S^T = K Q^T): lane reads row kt*32 + l32, chunk
-  // 2c + g at position (2c + g) ^ (l32 & 7) = 8 (c / 4) + ((2 (c % 4) + g) ^ (l32 & 7)).
-  const bf16_t* k_rd[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) k_rd[c] = k_lds + l32 * D + ((2 * c + g) ^ (l32 & 7)) * 8;
-  // V (A operand of O^T += V^T P^T via transpose reads): 16-lane group G, source lane j = 4r + q
-  // reads 4 elements of row 16c + 4(G/2) + 8hf + r at column 32t + 16(G%2) + 4q, whose chunk is
-  // swizzled by 2r: 8 (t / 2) + ((4 (t % 2) + 2 (G % 2) + q / 2) ^ 2r).
-  const int G = lane >> 4, tr_r = (lane & 15) >> 2, tr_q = lane & 3;
-  const bf16_t* v_rd[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-    v_rd[t] = v_lds + (4 * (G >> 1) + tr_r) * D + (((4 * t + 2 * (G & 1) + (tr_q >> 1)) ^ (2 * tr_r)) * 8) + 4 * (tr_q & 1);
-
-  bool active = real > 0;
-  while (active) {
-    const int cur_real = real;
-    const bool has_next = todo != 0;
-    int j_next = 0, real_next = 0;
-    if (has_next) {
-      const int nxt = __builtin_ctzll(todo);
-      todo &= todo - 1;
-      j_next = __builtin_amdgcn_readlane(my_j, nxt);
-      real_next = __builtin_amdgcn_readlane(my_real, nxt);
+  // Two-stage pipeline, one barrier per step: at the top of a step this wave's stream into the
+  // current buffer has landed (vmcnt 0) and, after the barrier, every wave's has; every wave has
+  // also finished reading the other buffer (previous step), which the next stream then refills.
+  while (cur.valid) {
+    {
+      const int real = cur.real - 64 * cur.half;
+      Cursor nxt = cur;
+      cursor_next<BS>(nxt, my_j, my_real);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      attend_step<D, NW>(k0, v0, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k1, v1, nxt), w, lane);
+      cur = nxt;
     }
-
-    // ---- K tile ready (V of this tile may still stream) ----------------------------------
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NI) : "memory");
-
-    f32x16 sacc[KT];
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) sacc[kt] = f32x16{};
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const bf16x8 a = *(const bf16x8*)(k_rd[c & 3] + (c >> 2) * 64 + kt * 32 * D);
-        sacc[kt] = wa_mfma32(a, qf[c], sacc[kt]);
-      }
+    if (!cur.valid) break;
+    {
+      const int real = cur.real - 64 * cur.half;
+      Cursor nxt = cur;
+      cursor_next<BS>(nxt, my_j, my_real);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      attend_step<D, NW>(k1, v1, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k0, v0, nxt), w, lane);
+      cur = nxt;
     }
-    wa_lds_barrier();  // every wave is done with K: stream the next K tile
-    if (has_next)
-      dma_tile<D, BS>(k_lds, kbase + (int64_t)j_next * BS * p.k_st, p.k_st, k_off, k_chunk, real_next, w, lane);
-
-    // ---- online softmax in the log2 domain ------------------------------------------------
-    float mx = -INFINITY;
-    if (cur_real < BS) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= cur_real) sacc[kt][r] = -INFINITY;
-        }
-      }
-    }
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * p.scale_log2;
-    const float m_new = fmaxf(m_i, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-    float rs = 0.f;
-    bf16x8 pb[PC];
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], p.scale_log2, -m_new));
-        rs += pv;
-        pb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)pv;
-      }
-    }
-    l_i = fmaf(l_i, alpha, rs);
-    m_i = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-
-    // ---- V tile ready (the next K tile may still stream) -----------------------------------
-    if (has_next) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NI) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-#pragma unroll
-    for (int c = 0; c < PC; ++c) {
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        bf16x8 a;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const s16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              WA_LDS4(v_rd[t & 1] + (16 * c + 8 * hf) * D + (t >> 1) * 64));
-          const bf16x4 vb = __builtin_bit_cast(bf16x4, vv);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) a[4 * hf + e] = vb[e];
-        }
-        oacc[t] = wa_mfma32(a, pb[c], oacc[t]);
-      }
-    }
-    wa_lds_barrier();  // every wave is done with V: stream the next V tile
-    if (has_next)
-      dma_tile<D, BS>(v_lds, vbase + (int64_t)j_next * BS * p.v_st, p.v_st, v_off, v_chunk, real_next, w, lane);
-    real = real_next;
-    active = has_next;
   }
 
-  // ---- normalized partial + log2-sum-exp -------------------------------------------------
   const float lsum = l_i + __shfl_xor(l_i, 32, 64);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  if (ns == 1) {
+    // the row's only unit: final output straight from registers
+    if (p.lse && g == 0 && q_ok)
+      p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lsum > 0.f ? (m_i + __log2f(lsum)) * WA_LN2 : -INFINITY;
+    write_output<D>(p, oacc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
+    return;
+  }
+  // normalized partial + log2-sum-exp for the combine pass
   const int64_t slot = row * p.max_splits + split;
   float* po = p.part_o + slot * (int64_t)(BS * D);
   const int ql = w * 32 + l32;
-  if (g == 0) p.part_lse[slot * BS + ql] = lsum > 0.f ? m_i + log2f(lsum) : -INFINITY;
+  if (g == 0) p.part_lse[slot * BS + ql] = lsum > 0.f ? m_i + __log2f(lsum) : -INFINITY;
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
 #pragma unroll
@@ -324,10 +468,8 @@ bsa_unit_kernel(FwdParams p) {
   }
 }
 
-// Merges the partials of one row in split order, then the epilogue:
-//   PLAIN: o = attn;  FUSE: o = attn + g * x;  GATED: o = g * attn,
-// with g = sigmoid(q . gate_w[d] + gate_b[d]) (or sigmoid(q) without gate_w) — the gated fusion of
-// attention.py:246-254 — and the natural-log LSE when asked for.
+// Merges the partials of each row that has two or more units, in split order, and writes rows
+// with no visits at all; rows with exactly one unit were written by the unit kernel.
 template <int D, int BS>
 __global__ void __launch_bounds__(2 * BS) bsa_combine_kernel(FwdParams p) {
   constexpr int DC = D / 16, DT = D / 32;
@@ -339,11 +481,12 @@ __global__ void __launch_bounds__(2 * BS) bsa_combine_kernel(FwdParams p) {
   const int hs = (int)(bh % p.n_heads), b = (int)(bh / p.n_heads);
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
+  const int n = row_visits(p, ((int64_t)b * p.H + h) * p.Nq + qb);
+  const int ns = min(n > 0 ? (n + p.split - 1) / p.split : 0, p.max_splits);
+  if (ns == 1) return;
   const int qi = qb * BS + w * 32 + l32;
   const bool q_ok = qi < p.Lq;
   const int ql = w * 32 + l32;
-  const int n = row_visits(p, ((int64_t)b * p.H + h) * p.Nq + qb);
-  const int ns = min(n > 0 ? (n + p.split - 1) / p.split : 0, p.max_splits);
   const int64_t slot0 = row * p.max_splits;
 
   float M = -INFINITY;
@@ -373,75 +516,14 @@ __global__ void __launch_bounds__(2 * BS) bsa_combine_kernel(FwdParams p) {
   const float inv = Z > 0.f ? 1.f / Z : 0.f;
   if (p.lse && g == 0 && q_ok)
     p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = Z > 0.f ? (M + log2f(Z)) * WA_LN2 : -INFINITY;
-
   const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
-  const bool need_gate = p.epilogue != WA_EPI_PLAIN;
-  f32x16 gacc[DT];
-  if (need_gate && p.gate_w) {
-    bf16x8 qf[DC];
+  bf16x8 qf[DC];
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
-      qf[c] = q_ok ? t : bf16x8{};
-    }
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      gacc[t] = f32x16{};
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        const bf16x8 a = *(const bf16x8*)(p.gate_w + (t * 32 + l32) * D + c * 16 + g * 8);
-        gacc[t] = wa_mfma32(a, qf[c], gacc[t]);
-      }
-    }
+  for (int c = 0; c < DC; ++c) {
+    bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
+    qf[c] = q_ok ? t : bf16x8{};
   }
-  if (!q_ok) return;
-
-#pragma unroll
-  for (int t = 0; t < DT; ++t) {
-#pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int d0 = t * 32 + 8 * rq + 4 * g;
-      float val[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float a = acc[t][rq * 4 + i] * inv;
-        if (p.attn_round_bf16) a = wa_bf16_round(a);
-        val[i] = a;
-      }
-      if (need_gate) {
-        float gv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float pre;
-          if (p.gate_w) {
-            pre = gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f);
-          } else {
-            pre = (float)qrow[d0 + i];
-          }
-          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
-          float gs = wa_sigmoid(pre);
-          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
-          gv[i] = gs;
-        }
-        if (p.epilogue == WA_EPI_FUSE) {
-          const int64_t xo = (int64_t)b * p.x_sb + (int64_t)qi * p.x_st + (int64_t)h * p.x_sh + d0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) val[i] = __fadd_rn(val[i], __fmul_rn(wa_load_f(p.x, xo + i, p.x_dtype), gv[i]));
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) val[i] = __fmul_rn(val[i], gv[i]);
-        }
-      }
-      const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + d0;
-      if (p.o_dtype == WA_BF16) {
-        bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
-        *(bf16x4*)((bf16_t*)p.o + oo) = ov;
-      } else {
-        f32x4 ov = {val[0], val[1], val[2], val[3]};
-        *(f32x4*)((float*)p.o + oo) = ov;
-      }
-    }
-  }
+  write_output<D>(p, acc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
 }
 
 template <int D, int BS>
@@ -496,7 +578,8 @@ extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_fwd: bad head count");
   const int64_t rows = a->B * nh * nq;
   const int64_t split = a->split_visits > 0 ? a->split_visits : WA_BSA_DEFAULT_SPLIT;
-  WA_CHECK_ARG(split <= 64, "wa_bsa_fwd: split_visits %lld exceeds 64", (long long)split);
+  WA_CHECK_ARG(split <= 64 && (a->block_size == 64 || split <= 32),
+               "wa_bsa_fwd: split_visits %lld exceeds %d", (long long)split, a->block_size == 64 ? 64 : 32);
   const int64_t width = a->index ? a->index_width : nkv;
   const int64_t max_visits = a->max_visits > 0 ? (a->max_visits < width ? a->max_visits : width) : width;
   const int64_t max_splits = max_visits > 0 ? (max_visits + split - 1) / split : 1;

@@ -1,0 +1,417 @@
+// Kernelized linear attention with phi(x) = elu(x) + 1 (the north-star "linear-global" heads):
+//   state:   S^T[d, e] = sum_t v[t, d] phi(k[t, e]),   z[e] = sum_t phi(k[t, e])
+//   readout: o[q, d] = sum_e phi(q[q, e]) S^T[d, e] / (phi(q) . z)   (+ gated-fusion epilogue)
+// There is no reference counterpart: the reference's linear branch is the low-rank softmax branch
+// (wan/modules/hsa/attention.py:64-118), kept in linear.hip.
+//
+// gfx950 layout. Both products contract over a dimension that is contiguous in memory for one of
+// the operands only, so the state kernel stages row-major [token][channel] tiles in LDS and feeds
+// BOTH MFMA operands with transpose reads (ds_read_b64_tr_b16), while the next 64-token tile
+// streams into registers. The readout stages S^T once per workgroup in LDS as a bf16 hi + lo pair
+// (two MFMAs keep ~16 mantissa bits of the fp32 state).
+#include "common.h"
+
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+#define WA_LDS4(p) ((__attribute__((address_space(3))) s16x4*)(p))
+
+__device__ __forceinline__ float elu1f(float x) { return x > 0.f ? x + 1.f : __expf(x); }
+
+// Row swizzles of 16-byte chunks (see bsa_fwd.hip): transpose reads cover 4 rows x 32 bytes per
+// 16 lanes; 128-bit reads cover 16 rows x 16 bytes.
+__device__ __forceinline__ int tr_swizzle(int r) { return 2 * (r & 3); }
+template <int D>
+__device__ __forceinline__ int row_swizzle(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+
+// MFMA operand fragment of a row-major, tr-swizzled [rows][D] bf16 LDS tile for a contraction over
+// rows [16c, 16c + 16): lane (l32, g) receives rows 16c + 8g + e (e = 0..7) at column col0 + l32.
+// Transpose-read semantics (per 16-lane group): result lane i, element r comes from element i % 4
+// of source lane 4r + i / 4.
+template <int D>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16_t* buf, int c, int col0, int lane) {
+  const int G = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+  bf16x8 a;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int row = 16 * c + 8 * (G >> 1) + 4 * hf + r;
+    const int col = col0 + 16 * (G & 1) + 4 * q;
+    const int slot = (col >> 3) ^ tr_swizzle(row);
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(WA_LDS4(buf + row * D + slot * 8 + (col & 7)));
+    const bf16x4 b = __builtin_bit_cast(bf16x4, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[4 * hf + e] = b[e];
+  }
+  return a;
+}
+
+template <typename T>
+__device__ __forceinline__ void load_row8(const T* src, float (&f)[8]);
+template <>
+__device__ __forceinline__ void load_row8<bf16_t>(const bf16_t* src, float (&f)[8]) {
+  const bf16x8 v = *(const bf16x8*)src;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
+}
+template <>
+__device__ __forceinline__ void load_row8<float>(const float* src, float (&f)[8]) {
+  const f32x4 a = *(const f32x4*)src, b = *(const f32x4*)(src + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[e + 4] = b[e];
+  }
+}
+
+// =============================================================================================
+// state: one workgroup per (token chunk, head slot, batch) writes a partial S^T and z; a second
+// pass sums the chunk partials in a fixed order (bitwise reproducible).
+// =============================================================================================
+struct StateParams {
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  int H, L, n_heads, n_chunks, chunk_len, B;
+  const int32_t* heads;
+  float* part;  // [n_chunks][B][n_heads][D*D + D]
+  float* state; float* zsum;
+};
+
+template <int D, typename T>
+__global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
+  constexpr int TC = 64;                 // tokens per LDS tile
+  constexpr int CPR = D / 8;             // 8-element chunks per row
+  constexpr int UPT = TC * CPR / 256;    // chunks per thread per tensor (4 or 2)
+  constexpr int NT = D / 32;             // 32-wide tiles along d and e
+  constexpr int TPW = NT * NT / 4;       // output tiles per wave (4 or 1)
+  __shared__ __attribute__((aligned(1024))) bf16_t kb[2][TC * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t vb[2][TC * D];
+
+  const int chunk = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tbeg = chunk * p.chunk_len;
+  const int tend = min(p.L, tbeg + p.chunk_len);
+  const int c8 = tid % CPR, row0 = tid / CPR;  // this thread's chunk column and first row
+  const T* kbase = (const T*)p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + c8 * 8;
+  const T* vbase = (const T*)p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + c8 * 8;
+
+  // wave w owns output tiles (dt, et): D = 128 -> dt = w, et = 0..3; D = 64 -> (w / 2, w % 2)
+  f32x16 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = f32x16{};
+  float zacc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zacc[e] = 0.f;
+
+  // one register stage of the next 64-token tile (raw values); an LDS double buffer holds bf16
+  // phi(k) / v of the tile being multiplied
+  float kr[1][UPT][8], vr[1][UPT][8];
+#define WA_ELU1_LOAD(S, T0)                                                         \
+  _Pragma("unroll") for (int i = 0; i < UPT; ++i) {                                 \
+    const int t = (T0) + row0 + i * (256 / CPR);                                    \
+    if (t < tend) {                                                                 \
+      load_row8<T>(kbase + (int64_t)t * p.k_st, kr[S][i]);                          \
+      load_row8<T>(vbase + (int64_t)t * p.v_st, vr[S][i]);                          \
+    } else {                                                                        \
+      _Pragma("unroll") for (int e = 0; e < 8; ++e) kr[S][i][e] = vr[S][i][e] = 0.f; \
+    }                                                                               \
+  }
+#define WA_ELU1_STORE(S, BUF, T0)                                           \
+  _Pragma("unroll") for (int i = 0; i < UPT; ++i) {                         \
+    const int r = row0 + i * (256 / CPR);                                   \
+    const bool ok = (T0) + r < tend;                                        \
+    bf16x8 kk, vv;                                                          \
+    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                         \
+      const float ph = ok ? wa_bf16_round(elu1f(kr[S][i][e])) : 0.f;       \
+      zacc[e] += ph;                                                        \
+      kk[e] = (bf16_t)ph;                                                   \
+      vv[e] = (bf16_t)vr[S][i][e];                                          \
+    }                                                                       \
+    const int slot = c8 ^ tr_swizzle(r);                                    \
+    *(bf16x8*)(&kb[BUF][r * D + slot * 8]) = kk;                            \
+    *(bf16x8*)(&vb[BUF][r * D + slot * 8]) = vv;                            \
+  }
+#define WA_ELU1_MMA(BUF)                                                    \
+  _Pragma("unroll") for (int c = 0; c < TC / 16; ++c) {                     \
+    _Pragma("unroll") for (int i = 0; i < TPW; ++i) {                       \
+      const int dt = D == 128 ? w : (w >> 1);                               \
+      const int et = D == 128 ? i : (w & 1);                                \
+      const bf16x8 a = tr_frag<D>(vb[BUF], c, 32 * dt, lane);               \
+      const bf16x8 bb = tr_frag<D>(kb[BUF], c, 32 * et, lane);              \
+      acc[i] = wa_mfma32(a, bb, acc[i]);                                    \
+    }                                                                       \
+  }
+
+  // tile t0 + TC streams into registers while tile t0 is multiplied (LDS buffers alternate;
+  // unrolled by two so every index is static)
+  int t0 = tbeg;
+  if (t0 < tend) { WA_ELU1_LOAD(0, t0) }
+  while (t0 < tend) {
+    WA_ELU1_STORE(0, 0, t0)
+    if (t0 + TC < tend) { WA_ELU1_LOAD(0, t0 + TC) }
+    __syncthreads();  // LDS buffer 0 complete; every wave is past the tile before it
+    WA_ELU1_MMA(0)
+    t0 += TC;
+    if (t0 >= tend) break;
+    WA_ELU1_STORE(0, 1, t0)
+    if (t0 + TC < tend) { WA_ELU1_LOAD(0, t0 + TC) }
+    __syncthreads();
+    WA_ELU1_MMA(1)
+    t0 += TC;
+  }
+#undef WA_ELU1_STORE
+#undef WA_ELU1_MMA
+#undef WA_ELU1_LOAD
+
+  float* part = p.part + (((int64_t)chunk * p.B + b) * p.n_heads + hs) * (int64_t)(D * D + D);
+  // accumulator lane (e = 32 et + l32, g) holds d = 32 dt + 8 (r / 4) + 4 g + r % 4
+  const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int dt = D == 128 ? w : (w >> 1);
+    const int et = D == 128 ? i : (w & 1);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * dt + 8 * (r >> 2) + 4 * g + (r & 3);
+      part[d * D + 32 * et + l32] = acc[i][r];
+    }
+  }
+  // z: threads with the same chunk column c8 hold disjoint rows; reduce them in a fixed order
+  __syncthreads();
+  float* zbuf = (float*)kb;  // reuse the tile buffers: [256 threads][8]
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zbuf[tid * 8 + e] = zacc[e];
+  __syncthreads();
+  if (tid < D) {
+    const int cc = tid / 8, e = tid % 8;
+    float s = 0.f;
+    for (int r = 0; r < 256 / CPR; ++r) s += zbuf[(r * CPR + cc) * 8 + e];
+    part[D * D + tid] = s;
+  }
+}
+
+__global__ void __launch_bounds__(256) elu1_reduce_kernel(StateParams p, int D) {
+  const int64_t per = (int64_t)D * D + D;
+  const int64_t total = (int64_t)p.B * p.n_heads * per;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  int c = 0;
+  for (; c + 4 <= p.n_chunks; c += 4) {
+    a0 += p.part[(int64_t)c * total + i];
+    a1 += p.part[(int64_t)(c + 1) * total + i];
+    a2 += p.part[(int64_t)(c + 2) * total + i];
+    a3 += p.part[(int64_t)(c + 3) * total + i];
+  }
+  for (; c < p.n_chunks; ++c) a0 += p.part[(int64_t)c * total + i];
+  const float s = (a0 + a1) + (a2 + a3);
+  const int64_t bh = i / per, r = i % per;
+  if (r < (int64_t)D * D) p.state[bh * D * D + r] = s;
+  else p.zsum[bh * D + (r - (int64_t)D * D)] = s;
+}
+
+// =============================================================================================
+// readout: one workgroup per (128-query tile, head slot, batch); wave w owns 32 queries.
+// =============================================================================================
+struct ReadoutParams {
+  const void* q; int64_t q_sb, q_st, q_sh; int q_dtype;
+  const float* state; const float* zsum;
+  void* o; int64_t o_sb, o_st, o_sh; int o_dtype;
+  int H, L, n_heads;
+  const int32_t* heads;
+  int epilogue;
+  const bf16_t* gate_w; const float* gate_b;
+  int gate_pre_bf16, gate_out_bf16, lin_round_bf16;
+};
+
+template <int D>
+__global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
+  constexpr int DC = D / 16, DT = D / 32, CPR = D / 8;
+  __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_w[D * D];
+  __shared__ float s_z[D];
+  const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const float* S = p.state + ((int64_t)b * p.n_heads + hs) * D * D;
+  const bool use_w = p.epilogue == WA_EPI_GATED && p.gate_w;
+
+  // stage S^T as bf16 hi + lo (and the gate weights) in row-swizzled LDS; all loads are issued
+  // before any conversion so their latencies overlap
+  constexpr int SU = D * CPR / 256;  // 8-element units per thread (8 or 2)
+  f32x4 x0[SU], x1[SU];
+  bf16x8 wv[SU];
+#pragma unroll
+  for (int k = 0; k < SU; ++k) {
+    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    x0[k] = *(const f32x4*)(S + d * D + cc * 8);
+    x1[k] = *(const f32x4*)(S + d * D + cc * 8 + 4);
+    if (use_w) wv[k] = *(const bf16x8*)(p.gate_w + d * D + cc * 8);
+  }
+#pragma unroll
+  for (int k = 0; k < SU; ++k) {
+    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = (bf16_t)x0[k][e];
+      lo[e] = (bf16_t)(x0[k][e] - (float)hi[e]);
+      hi[e + 4] = (bf16_t)x1[k][e];
+      lo[e + 4] = (bf16_t)(x1[k][e] - (float)hi[e + 4]);
+    }
+    const int slot = cc ^ row_swizzle<D>(d);
+    *(bf16x8*)(s_hi + d * D + slot * 8) = hi;
+    *(bf16x8*)(s_lo + d * D + slot * 8) = lo;
+    if (use_w) *(bf16x8*)(s_w + d * D + slot * 8) = wv[k];
+  }
+  for (int e = tid; e < D; e += 256) s_z[e] = p.zsum[((int64_t)b * p.n_heads + hs) * D + e];
+  __syncthreads();
+
+  const int qi = tile * 128 + w * 32 + l32;
+  const bool q_ok = qi < p.L;
+  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
+  bf16x8 qf[DC], phf[DC];
+  float den = 0.f;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    float f[8];
+    if (p.q_dtype == WA_BF16) load_row8<bf16_t>((const bf16_t*)p.q + qoff + c * 16 + g * 8, f);
+    else load_row8<float>((const float*)p.q + qoff + c * 16 + g * 8, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!q_ok) f[e] = 0.f;
+      qf[c][e] = (bf16_t)f[e];
+      const float ph = wa_bf16_round(elu1f(f[e]));
+      phf[c][e] = (bf16_t)ph;
+      den = fmaf(ph, s_z[c * 16 + g * 8 + e], den);
+    }
+  }
+  den += __shfl_xor(den, 32, 64);
+
+  // O^T[d, q] = S^T[d, :] phi(Q)^T[:, q]; A fragment: row d = 32t + l32, chunk 2c + g
+  f32x16 oacc[DT], gacc[DT];
+  const int rs = row_swizzle<D>(l32);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    oacc[t] = f32x16{};
+    gacc[t] = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const int off = (32 * t + l32) * D + ((2 * c + g) ^ rs) * 8;
+      oacc[t] = wa_mfma32(*(const bf16x8*)(s_hi + off), phf[c], oacc[t]);
+      oacc[t] = wa_mfma32(*(const bf16x8*)(s_lo + off), phf[c], oacc[t]);
+      if (use_w) gacc[t] = wa_mfma32(*(const bf16x8*)(s_w + off), qf[c], gacc[t]);
+    }
+  }
+  if (!q_ok) return;
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  const bool need_gate = p.epilogue == WA_EPI_GATED;
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = t * 32 + 8 * rq + 4 * g;
+      float val[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = oacc[t][rq * 4 + i] * inv;
+        if (p.lin_round_bf16) a = wa_bf16_round(a);
+        if (need_gate) {
+          float pre = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f)
+                               : wa_load_f(p.q, qoff + d0 + i, p.q_dtype);
+          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
+          float gs = wa_sigmoid(pre);
+          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
+          a = __fmul_rn(a, gs);
+        }
+        val[i] = a;
+      }
+      const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + d0;
+      if (p.o_dtype == WA_BF16) {
+        bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
+        *(bf16x4*)((bf16_t*)p.o + oo) = ov;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ((float*)p.o)[oo + i] = val[i];
+      }
+    }
+  }
+}
+
+int state_chunks(int64_t B, int64_t nh, int64_t L) {
+  const int64_t target = 256;
+  const int64_t per_bh = (target + B * nh - 1) / (B * nh);
+  const int64_t max_chunks = (L + 63) / 64;
+  const int64_t c = per_bh < max_chunks ? per_bh : max_chunks;
+  return (int)(c < 1 ? 1 : c);
+}
+
+}  // namespace
+
+extern "C" int64_t wa_elu1_state_workspace_bytes(int64_t B, int64_t n_heads, int64_t L, int64_t D) {
+  const int64_t chunks = state_chunks(B, n_heads, L);
+  return ((chunks * B * n_heads * (D * D + D)) * 4 + 255) / 256 * 256;
+}
+
+extern "C" int wa_elu1_state(const wa_elu1_state_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->k && a->v && a->state && a->zsum && a->workspace, "wa_elu1_state: null argument");
+  WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_elu1_state: head dim %lld not in {64, 128}", (long long)a->D);
+  WA_CHECK_ARG(a->dtype == WA_F32 || a->dtype == WA_BF16, "wa_elu1_state: bad dtype");
+  WA_CHECK_ARG(a->L > 0 && a->H > 0 && a->B >= 0, "wa_elu1_state: bad sizes");
+  const int64_t vec = a->dtype == WA_BF16 ? 8 : 4;
+  WA_CHECK_ARG(wa_aligned16(a->k) && wa_aligned16(a->v) && a->k_sb % vec == 0 && a->k_st % vec == 0 &&
+                   a->k_sh % vec == 0 && a->v_sb % vec == 0 && a->v_st % vec == 0 && a->v_sh % vec == 0,
+               "wa_elu1_state: k/v must be 16-byte aligned with 16-byte aligned rows");
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  if (a->B == 0 || nh == 0) return WA_OK;
+  StateParams sp{};
+  sp.k = a->k; sp.k_sb = a->k_sb; sp.k_st = a->k_st; sp.k_sh = a->k_sh;
+  sp.v = a->v; sp.v_sb = a->v_sb; sp.v_st = a->v_st; sp.v_sh = a->v_sh;
+  sp.H = (int)a->H; sp.L = (int)a->L; sp.n_heads = (int)nh; sp.B = (int)a->B;
+  sp.n_chunks = state_chunks(a->B, nh, a->L);
+  sp.chunk_len = (int)(((a->L + sp.n_chunks - 1) / sp.n_chunks + 63) / 64 * 64);
+  sp.n_chunks = (int)((a->L + sp.chunk_len - 1) / sp.chunk_len);
+  sp.heads = a->heads; sp.part = (float*)a->workspace; sp.state = a->state; sp.zsum = a->zsum;
+  dim3 grid((unsigned)sp.n_chunks, (unsigned)nh, (unsigned)a->B);
+  hipStream_t s = (hipStream_t)stream;
+  if (a->D == 128) {
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_kernel<128, bf16_t>), grid, dim3(256), 0, s, sp);
+    else hipLaunchKernelGGL((elu1_state_kernel<128, float>), grid, dim3(256), 0, s, sp);
+  } else {
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_kernel<64, bf16_t>), grid, dim3(256), 0, s, sp);
+    else hipLaunchKernelGGL((elu1_state_kernel<64, float>), grid, dim3(256), 0, s, sp);
+  }
+  int rc = wa_launch_status("elu1_state");
+  if (rc != WA_OK) return rc;
+  const int64_t total = a->B * nh * (a->D * a->D + a->D);
+  hipLaunchKernelGGL(elu1_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp, (int)a->D);
+  return wa_launch_status("elu1_reduce");
+}
+
+extern "C" int wa_elu1_readout(const wa_elu1_readout_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->q && a->state && a->zsum && a->o, "wa_elu1_readout: null argument");
+  WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_elu1_readout: head dim %lld not in {64, 128}", (long long)a->D);
+  WA_CHECK_ARG(a->q_dtype == WA_F32 || a->q_dtype == WA_BF16, "wa_elu1_readout: bad q dtype");
+  WA_CHECK_ARG(a->o_dtype == WA_F32 || a->o_dtype == WA_BF16, "wa_elu1_readout: bad o dtype");
+  WA_CHECK_ARG(a->epilogue == WA_EPI_PLAIN || a->epilogue == WA_EPI_GATED, "wa_elu1_readout: epilogue must be PLAIN or GATED");
+  WA_CHECK_ARG(wa_aligned16(a->state), "wa_elu1_readout: state must be 16-byte aligned");
+  const int64_t vec = a->q_dtype == WA_BF16 ? 8 : 4;
+  WA_CHECK_ARG(wa_aligned16(a->q) && a->q_sb % vec == 0 && a->q_st % vec == 0 && a->q_sh % vec == 0,
+               "wa_elu1_readout: q must be 16-byte aligned with 16-byte aligned rows");
+  WA_CHECK_ARG((((uintptr_t)a->o) & 7u) == 0 && a->o_sb % 4 == 0 && a->o_st % 4 == 0 && a->o_sh % 4 == 0,
+               "wa_elu1_readout: output must be 8-byte aligned with strides multiple of 4");
+  if (a->gate_w) WA_CHECK_ARG(wa_aligned16(a->gate_w), "wa_elu1_readout: gate_w must be 16-byte aligned");
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  if (a->B == 0 || nh == 0 || a->L == 0) return WA_OK;
+  ReadoutParams rp{a->q, a->q_sb, a->q_st, a->q_sh, a->q_dtype, a->state, a->zsum, a->o, a->o_sb, a->o_st,
+                   a->o_sh, a->o_dtype, (int)a->H, (int)a->L, (int)nh, a->heads, a->epilogue,
+                   (const bf16_t*)a->gate_w, a->gate_b, a->gate_pre_bf16, a->gate_out_bf16, a->lin_round_bf16};
+  dim3 grid((unsigned)((a->L + 127) / 128), (unsigned)nh, (unsigned)a->B);
+  hipStream_t s = (hipStream_t)stream;
+  if (a->D == 128) hipLaunchKernelGGL(elu1_readout_kernel<128>, grid, dim3(256), 0, s, rp);
+  else hipLaunchKernelGGL(elu1_readout_kernel<64>, grid, dim3(256), 0, s, rp);
+  return wa_launch_status("elu1_readout");
+}

@@ -217,12 +217,26 @@ def elu1_readout(q, state, zsum, heads_t, out, *, epilogue=_lib.WA_EPI_PLAIN, ga
 class GateSpec:
     """Kernel-side view of the fusion gate (``attention.py:246-251``)."""
 
+    _cache: dict = {}
+
+    @classmethod
+    def _converted(cls, t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        # kernel-side copies of the gate parameters, refreshed when the parameter changes
+        key = (t.data_ptr(), t.dtype, dtype)
+        hit = cls._cache.get(key)
+        if hit is None or hit[0] != t._version:
+            hit = (t._version, t.detach().to(dtype).contiguous())
+            if len(cls._cache) > 64:
+                cls._cache.clear()
+            cls._cache[key] = hit
+        return hit[1]
+
     def __init__(self, gate_lin: Optional[nn.Module], comp_dtype: torch.dtype):
         if gate_lin is not None:
             w = gate_lin.weight
-            self.w = w.detach().to(torch.bfloat16).contiguous()
+            self.w = self._converted(w, torch.bfloat16)
             b = getattr(gate_lin, "bias", None)
-            self.b = b.detach().float().contiguous() if b is not None else None
+            self.b = self._converted(b, torch.float32) if b is not None else None
             self.pre_bf16 = w.dtype == torch.bfloat16
             self.out_bf16 = w.dtype == torch.bfloat16 or comp_dtype == torch.bfloat16
         else:

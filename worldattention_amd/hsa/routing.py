@@ -128,7 +128,8 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
         bsz, nheads, nq, d = qp.shape
         nkv = kp.shape[2]
     index = torch.empty((bsz, nheads, nq, nkv), dtype=torch.int32, device=dev)
-    num = torch.zeros((bsz, nheads, nq), dtype=torch.int32, device=dev)
+    # rows of heads outside `heads` are not written by the kernel: give them num = 0
+    num = (torch.zeros if heads is not None else torch.empty)((bsz, nheads, nq), dtype=torch.int32, device=dev)
     thresholds = torch.zeros((nheads,), dtype=torch.float32, device=dev)
     mask = torch.zeros((bsz, nheads, nq, nkv), dtype=torch.bool, device=dev) if return_mask else None
     probs_out = (torch.empty((bsz, nheads, nq, nkv), dtype=torch.float32, device=dev)
@@ -139,7 +140,7 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
         ws = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
     head_k_t = None
     if head_k is not None:
-        head_k_t = torch.as_tensor(head_k, dtype=torch.int32).to(dev)
+        head_k_t = _lib.head_list(head_k, dev)
     # the threshold is tau_min + G * (tau_max - tau_min) in fp32, with the span formed in double
     args = _lib.RouteArgs(_lib.ptr(probs), _lib.ptr(qp), _lib.ptr(kp), bsz, nheads, nq, nkv, d, mode,
                           float(tau_min), float(tau_max - tau_min), _lib.ptr(head_k_t), _lib.ptr(heads),
