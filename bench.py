@@ -137,7 +137,7 @@ def main():
         "sparse_useful_gflop": round(useful_flop / 1e9, 3),
         "sparse_tile_gflop": round(tile_flop / 1e9, 3),
         "pct_mfma_peak_sparse": round(100 * achieved / MFMA_BF16_PEAK_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "kernel": "bsa_fwd_kernel<128,128>", "achieved": round(achieved, 3),
+        "roofline": {"bound": "mfma", "kernel": "bsa_unit_kernel<128,128> + bsa_combine_kernel<128,128>", "achieved": round(achieved, 3),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": None},
     }
