@@ -139,6 +139,38 @@ int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t spl
                                    int64_t D);
 int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
 
+/* Backward of wa_bsa_fwd: dQ, dK, dV (fp32, BLHD) of the block-sparse attention output o.
+ * Replaces _bwd_preprocess/_bwd_kernel/_backward, wan/modules/hsa/block_sparse_triton.py:142-368
+ * (which requires Lq == Lkv), and the autograd of block_sparse_torch.py:16-64: any Lq / Lkv, a
+ * key block listed twice contributes twice, masked keys and empty rows contribute nothing.
+ * o: the forward's attention output (fp32 preferred; its row dot product with dout is delta),
+ * dout: gradient of o, lse: the forward's natural-log log-sum-exp [B, H, Lq]. index / num /
+ * block_sizes / heads as in wa_bsa_fwd. dq (optional), dk + dv (optional pair): with
+ * *_accumulate set the gradient is added to the existing contents. Routing is not
+ * differentiated. Work: a preprocess pass, the transposed (key block -> query blocks) lists,
+ * a dQ pass over each query block's list and a dK/dV pass over each key block's list; sums run
+ * in a fixed order (reproducible). */
+typedef struct wa_bsa_bwd_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  const void* o; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  const void* dout; int64_t d_sb, d_st, d_sh; int32_t dout_dtype;
+  const float* lse;
+  const int32_t* index; const int32_t* num; int64_t index_width;
+  const int32_t* block_sizes;
+  const int32_t* heads; int64_t n_heads;
+  int64_t B, H, Lq, Lkv, D, block_size;
+  float scale;
+  float* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_accumulate;
+  float* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
+  float* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
+  void* workspace;
+} wa_bsa_bwd_args;
+int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t Lkv, int64_t D,
+                                   int64_t block_size);
+int wa_bsa_bwd(const wa_bsa_bwd_args* args, void* stream);
+
 /* ------------------------------------------------------------------------------------------ */
 /* Linear branch                                                                               */
 /* ------------------------------------------------------------------------------------------ */
@@ -184,6 +216,60 @@ typedef struct wa_elu1_readout_args {
   int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
 } wa_elu1_readout_args;
 int wa_elu1_readout(const wa_elu1_readout_args* args, void* stream);
+
+/* Backward of the elu(x)+1 linear branch (wa_elu1_state + PLAIN wa_elu1_readout): given the
+ * forward's state / zsum and dout = dL/d(readout output), writes fp32 dq, dk, dv (BLHD; with
+ * *_accumulate set, added to the contents) for the listed heads. No reference counterpart (the
+ * north-star linear heads); the query-tile partial sums of dS and dz are reduced in a fixed order. */
+typedef struct wa_elu1_bwd_args {
+  const void* q; int64_t q_sb, q_st, q_sh; int32_t q_dtype;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh; int32_t kv_dtype;
+  const void* dout; int64_t d_sb, d_st, d_sh; int32_t dout_dtype;
+  const float* state; const float* zsum;
+  float* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_accumulate;
+  float* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
+  float* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
+  const int32_t* heads; int64_t n_heads;
+  int64_t B, H, Lq, Lkv, D;
+  void* workspace;
+} wa_elu1_bwd_args;
+int64_t wa_elu1_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t D);
+int wa_elu1_bwd(const wa_elu1_bwd_args* args, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
+/* Gated fusion as separate kernels (training path)                                            */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Branch fusion of attention.py:246-254 with per-head modes (head_modes[h]: bit 0 = the head runs
+ * the sparse branch, bit 1 = the linear branch, 0 = not written):
+ *   gate = sigmoid(q . gate_w[d] + gate_b[d])  (sigmoid(q) when gate_w is NULL; bf16 rounding of
+ *          the pre-activation / gate per the flags, as the reference's dtype casts do),
+ *   out  = [sparse] + [gate * linear]   (sparse / linear fp32 BLHD, optionally rounded to bf16).
+ * wa_hsa_fuse_fwd writes out and, when `gate` is given, the gate values of linear heads.
+ * wa_hsa_fuse_bwd takes dout, lin and the saved gate and writes dlin = dout * gate, adds
+ * dgpre * gate_w (or dgpre) into dq, and with gate_w writes dgate_w [D][D] and dgate_b [D]
+ * (sums of per-tile partials, fixed order; workspace from wa_hsa_fuse_bwd_workspace_bytes). The
+ * sparse branch's gradient is dout itself. q is bf16 BLHD. */
+typedef struct wa_hsa_fuse_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const float* sparse; int64_t s_sb, s_st, s_sh;
+  const float* lin; int64_t l_sb, l_st, l_sh;
+  const int32_t* head_modes;
+  void* out; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  float* gate; int64_t g_sb, g_st, g_sh;
+  const void* gate_w; const float* gate_b;
+  int32_t gate_pre_bf16, gate_out_bf16, attn_round_bf16, lin_round_bf16;
+  const void* dout; int64_t d_sb, d_st, d_sh; int32_t dout_dtype;
+  float* dlin; int64_t dl_sb, dl_st, dl_sh;
+  float* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_accumulate;
+  float* dgate_w; float* dgate_b;
+  void* workspace;
+  int64_t B, H, L, D;
+} wa_hsa_fuse_args;
+int wa_hsa_fuse_fwd(const wa_hsa_fuse_args* args, void* stream);
+int64_t wa_hsa_fuse_bwd_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t D);
+int wa_hsa_fuse_bwd(const wa_hsa_fuse_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -228,6 +228,35 @@ def block_sparse_attention(q, k, v, q2k_index, q2k_num, block_sizes, block_size,
     return (out, lse) if return_lse else out
 
 
+def block_sparse_attention_gather(q, k, v, q2k_index, q2k_num, block_sizes, block_size):
+    """Same result as :func:`block_sparse_attention`, vectorized the way the reference's torch path
+    is (``block_sparse_torch.py:30-64``): every row's listed key blocks are gathered at once
+    (width = the longest list), slots past ``num`` and tokens past ``block_sizes[j]`` are masked,
+    rows with nothing valid give 0. Autograd through it is cheap at the benchmark shapes.
+
+    pinned by: equality with the per-row loop of :func:`block_sparse_attention` (duplicates,
+    clamped ids, partial blocks, empty rows) in tests/test_oracle_hsa.py.
+    """
+    bsz, heads, nq_tok, d = q.shape
+    nq, nkv = nq_tok // block_size, k.shape[2] // block_size
+    width = max(int(q2k_num.max()), 1)
+    ids = q2k_index[..., :width].long().clamp(0, max(nkv - 1, 0))               # [B, H, Nq, W]
+    comp = q.dtype if q.dtype in (torch.float32, torch.float64) else torch.float32
+    tok = (ids.unsqueeze(-1) * block_size + torch.arange(block_size)).flatten(-2)  # [B, H, Nq, W*Bs]
+    bi = torch.arange(bsz).view(bsz, 1, 1, 1)
+    hi = torch.arange(heads).view(1, heads, 1, 1)
+    keys = k.to(comp)[bi, hi, tok]                                                # [B, H, Nq, W*Bs, D]
+    vals = v.to(comp)[bi, hi, tok]
+    qb = q.to(comp).view(bsz, heads, nq, block_size, d)
+    logits = torch.matmul(qb, keys.transpose(-1, -2)) / math.sqrt(d)              # [B, H, Nq, Bs, W*Bs]
+    slot_ok = torch.arange(width).view(1, 1, 1, width) < q2k_num.long().unsqueeze(-1)
+    tok_ok = torch.arange(block_size).view(1, 1, 1, 1, block_size) < block_sizes.long()[ids].unsqueeze(-1)
+    ok = (slot_ok.unsqueeze(-1) & tok_ok).flatten(-2).unsqueeze(-2)               # [B, H, Nq, 1, W*Bs]
+    logits = logits.masked_fill(~ok, float("-inf"))
+    probs = torch.nan_to_num(torch.softmax(logits, dim=-1), nan=0.0)
+    return torch.matmul(probs, vals).reshape(bsz, heads, nq_tok, d).to(q.dtype)
+
+
 # ----------------------------------------------------------------------------------------------
 # Linear branch (attention.py:64-118) and the north-star elu(x)+1 branch
 # ----------------------------------------------------------------------------------------------
@@ -354,8 +383,8 @@ def hsa_attention(q, k, v, *, k_coarse=None, v_coarse=None, k_proj_mat=None, v_p
     else:
         raise ValueError(f"routing must be one of {ROUTING_MODES}")
     sizes = variable_block_sizes(kv_len, kv_pad_len, block_size)
-    sparse = block_sparse_attention(q_p.to(torch.bfloat16), k_p.to(torch.bfloat16), v_p.to(torch.bfloat16),
-                                    route.index, route.num, sizes, block_size)
+    sparse = block_sparse_attention_gather(q_p.to(torch.bfloat16), k_p.to(torch.bfloat16),
+                                           v_p.to(torch.bfloat16), route.index, route.num, sizes, block_size)
 
     comp = linear.dtype
     if gate_weight is not None:

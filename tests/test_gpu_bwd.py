@@ -1,0 +1,157 @@
+"""GPU parity of the backward pass (cfg 5 path) against autograd through the CPU oracle.
+
+Tolerance (north star): gradients within max-abs <= 2e-2 and mean-abs <= 2e-3 of the fp32 oracle's
+autograd, for inputs and upstream gradients of unit scale. Routing is not differentiated (as in the
+reference), so the GPU and oracle runs must route identically — checked first where it matters."""
+import pytest
+import torch
+
+from oracle import hsa as O
+from worldattention_amd import hsa as W
+from worldattention_amd import workloads
+from worldattention_amd.hsa import attention as WA
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def assert_close(got, want, max_abs=2e-2, mean_abs=2e-3, what=""):
+    assert got is not None and want is not None, f"{what}: missing (gpu {got is None}, oracle {want is None})"
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    assert torch.isfinite(got).all(), f"{what}: non-finite"
+    diff = (got - want).abs()
+    assert diff.max().item() <= max_abs, f"{what}: max-abs {diff.max().item():.3e} (ref max {want.abs().max():.2e})"
+    assert diff.mean().item() <= mean_abs, f"{what}: mean-abs {diff.mean().item():.3e}"
+
+
+@pytest.mark.parametrize("d,bs", [(64, 64), (128, 64), (64, 128), (128, 128)])
+def test_sparse_backward_matches_oracle_autograd(d, bs):
+    torch.manual_seed(d + bs)
+    b, h, nq, nkv = 2, 3, 4, 7
+    lkv = nkv * bs - bs // 4           # partial trailing key block
+    q = torch.randn(b, h, nq * bs, d).bfloat16()
+    k = torch.randn(b, h, nkv * bs, d).bfloat16()
+    v = torch.randn(b, h, nkv * bs, d).bfloat16()
+    k[:, :, lkv:] = 0
+    v[:, :, lkv:] = 0
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    num = torch.randint(0, nkv + 1, (b, h, nq), dtype=torch.int32)
+    num[0, 0, 0] = 0                   # empty row
+    index[1, 2, 1, :3] = torch.tensor([4, 4, 2])  # a duplicated block counts twice
+    num[1, 2, 1] = 3
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    do = torch.randn(b, h, nq * bs, d)
+
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    want = O.block_sparse_attention(qr, kr, vr, index, num, sizes, bs)
+    want.backward(do.double())
+
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    got = W.block_sparse_attention_reference(qg, kg, vg, index.to(DEV), num.to(DEV), sizes.to(DEV), bs)
+    got.float().backward(do.to(DEV))
+    assert_close(got, want, what="out")
+    for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
+        assert_close(g[:, :, :lkv] if name != "dq" else g, r[:, :, :lkv] if name != "dq" else r,
+                     what=f"{name} d={d} bs={bs}")
+
+
+def test_sparse_backward_rectangular_lq_ne_lkv():
+    """cfg-5-like rectangle (the Triton reference backward assumes Lq == Lkv)."""
+    torch.manual_seed(5)
+    b, h, d, bs = 1, 2, 128, 128
+    nq, nkv = 3, 20
+    q, k, v = torch.randn(b, h, nq * bs, d).bfloat16(), torch.randn(b, h, nkv * bs, d).bfloat16(), \
+        torch.randn(b, h, nkv * bs, d).bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    num = torch.full((b, h, nq), 6, dtype=torch.int32)
+    sizes = torch.full((nkv,), bs, dtype=torch.int32)
+    do = torch.randn(b, h, nq * bs, d)
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    O.block_sparse_attention(qr, kr, vr, index, num, sizes, bs).backward(do.double())
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    W.block_sparse_attention_reference(qg, kg, vg, index.to(DEV), num.to(DEV), sizes.to(DEV), bs).float().backward(do.to(DEV))
+    for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
+        assert_close(g, r, what=name)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_elu1_backward_matches_oracle_autograd(d):
+    from worldattention_amd.hsa._autograd import elu1_backward
+    torch.manual_seed(d)
+    b, lq, lkv, h = 1, 300, 2000, 3
+    q, k, v = (torch.randn(b, n, h, d) for n in (lq, lkv, lkv))
+    g = torch.randn(b, lq, h, d)
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    out = O.linear_branch_elu1(qr.transpose(1, 2), kr.transpose(1, 2), vr.transpose(1, 2), compute_dtype=torch.float64)
+    out.transpose(1, 2).backward(g.double())
+    heads = torch.tensor([0, 2], dtype=torch.int32, device=DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    s, z = WA.elu1_state(kd, vd, heads)
+    dq, dk, dv = (torch.zeros(t.shape, device=DEV) for t in (q, k, v))
+    elu1_backward(qd, kd, vd, g.to(DEV), s, z, heads, dq, dk, dv)
+    for hh in (0, 2):
+        assert_close(dq[:, :, hh], qr.grad[:, :, hh], what=f"dq h{hh}")
+        assert_close(dk[:, :, hh], kr.grad[:, :, hh], what=f"dk h{hh}")
+        assert_close(dv[:, :, hh], vr.grad[:, :, hh], what=f"dv h{hh}")
+    assert torch.count_nonzero(dq[:, :, 1]) == 0
+
+
+def _grads_both(cfg, gate_w, gate_b, do, proj=None):
+    """(GPU grads, oracle grads, GPU route, oracle route) of hsa_attention for one config."""
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    d = q.shape[-1]
+    kw = dict(block_size=cfg["block_size"], routing=cfg["routing"], topk=cfg.get("topk"),
+              head_modes=cfg.get("head_modes"), linear_mode=cfg["linear_mode"], proj_segment_len=cfg["proj_segment_len"])
+    if proj is None:
+        rank = -(-cfg["proj_segment_len"] // cfg["block_size"])
+        proj = O.init_projection(rank, cfg["proj_segment_len"], cfg["block_size"])
+    qr, kr, vr = (t.detach().float().clone().requires_grad_() for t in (q, k, v))
+    wr, br = gate_w.clone().requires_grad_(), gate_b.clone().requires_grad_()
+    out_r, parts = O.hsa_attention(qr, kr, vr, k_proj_mat=proj, v_proj_mat=proj, gate_weight=wr, gate_bias=br,
+                                   return_parts=True, **kw)
+    out_r.float().backward(do.float())
+    lin = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        lin.weight.copy_(gate_w)
+        lin.bias.copy_(gate_b)
+    qg, kg, vg = (t.detach().float().to(DEV).requires_grad_() for t in (q, k, v))
+    out_g = W.hsa_attention(qg, kg, vg, k_proj_mat=proj.to(DEV), v_proj_mat=proj.to(DEV), gate_lin=lin, **kw)
+    out_g.float().backward(do.to(DEV).float())
+    return ((out_g, qg.grad, kg.grad, vg.grad, lin.weight.grad, lin.bias.grad),
+            (out_r, qr.grad, kr.grad, vr.grad, wr.grad, br.grad), parts)
+
+
+def test_hsa_split_heads_topk_elu1_gradients_match_oracle():
+    torch.manual_seed(11)
+    cfg = workloads.cfg1()
+    cfg["q"], cfg["k"], cfg["v"] = (t * 8 for t in (cfg["q"], cfg["k"], cfg["v"]))  # unit-scale inputs
+    d = cfg["q"].shape[-1]
+    do = torch.randn(cfg["q"].shape)
+    got, want, _ = _grads_both(cfg, torch.randn(d, d) * 0.1, torch.full((d,), 0.3), do)
+    for name, g, r in zip(("out", "dq", "dk", "dv", "dW", "db"), got, want):
+        tol = (0.1, 1e-2) if name in ("dW", "db") else (2e-2, 2e-3)   # parameter grads sum over tokens
+        assert_close(g, r, *tol, what=name)
+
+
+def test_hsa_reference_mode_gradients_match_oracle():
+    """Reference semantics: every head runs both branches, Gini routing, low-rank softmax branch."""
+    torch.manual_seed(3)
+    b, lq, lkv, h, d = 1, 200, 640, 2, 64
+    cfg = dict(q=torch.randn(b, lq, h, d), k=torch.randn(b, lkv, h, d), v=torch.randn(b, lkv, h, d), block_size=64,
+               routing="gini", linear_mode="lowrank", proj_segment_len=128)
+    proj = (torch.rand(2, 128) / 64).bfloat16()
+    do = torch.randn(b, lq, h, d)
+    got, want, parts = _grads_both(cfg, torch.randn(d, d) * 0.1, torch.zeros(d), do, proj=proj)
+    for name, g, r in zip(("out", "dq", "dk", "dv", "dW", "db"), got, want):
+        tol = (0.1, 1e-2) if name in ("dW", "db") else (2e-2, 2e-3)
+        assert_close(g, r, *tol, what=name)
+
+
+def test_cfg5_wan_chunk_fwd_bwd_matches_oracle():
+    """cfg 5: Lq=4680, Lkv=32760, H=12, D=128, bf16, block 128, top-k 16 on 8 sparse heads + 4 elu1
+    heads; dO ~ N(0, 1). Compares dQ, dK, dV of both branches with the oracle's fp32 autograd."""
+    cfg = workloads.cfg5()
+    d = cfg["q"].shape[-1]
+    got, want, parts = _grads_both(cfg, torch.zeros(d, d), torch.zeros(d), cfg["do"])
+    for name, g, r in zip(("out", "dq", "dk", "dv"), got[:4], want[:4]):
+        assert_close(g, r, what=f"cfg5 {name}")

@@ -101,3 +101,21 @@ def test_distillation_registry():
     finally:
         distill.enable_distill(False)
     assert not distill.distill_enabled()
+
+
+def test_gate_kernel_copies_follow_the_parameter_object():
+    """The bf16 / fp32 copies handed to the fusion kernels live on the parameter itself: a new
+    module never sees another module's copy (even at a reused address), and an in-place update
+    refreshes the copy."""
+    from worldattention_amd.hsa.attention import GateSpec
+    a, b = torch.nn.Linear(8, 8), torch.nn.Linear(8, 8)
+    with torch.no_grad():
+        b.weight.copy_(a.weight * 3)
+    wa = GateSpec(a, torch.float32).w
+    wb = GateSpec(b, torch.float32).w
+    assert torch.equal(wa.float(), a.weight.detach().bfloat16().float())
+    assert torch.equal(wb.float(), b.weight.detach().bfloat16().float())
+    assert GateSpec(a, torch.float32).w is wa                      # unchanged parameter: reused
+    with torch.no_grad():
+        a.weight.add_(1.0)
+    assert torch.equal(GateSpec(a, torch.float32).w.float(), a.weight.detach().bfloat16().float())

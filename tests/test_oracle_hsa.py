@@ -306,3 +306,28 @@ def test_init_projection_rows_average_one_block():
     assert O.token_range_to_coarse(50, 150, 50, 1) == (1, 3)
     with pytest.raises(ValueError):
         O.token_range_to_coarse(0, 51, 50, 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_vectorized_sparse_equals_the_per_row_loop(dtype):
+    torch.manual_seed(21)
+    b, h, nq, nkv, bs, d = 2, 3, 4, 6, 16, 8
+    q, k, v = (torch.randn(b, h, n * bs, d).to(dtype) for n in (nq, nkv, nkv))
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    num = torch.randint(0, nkv + 1, (b, h, nq), dtype=torch.int32)
+    num[0, 1, 2] = 0
+    index[1, 0, 3, :3] = torch.tensor([2, 2, 9])     # duplicate and out-of-range (clamped) ids
+    num[1, 0, 3] = 3
+    sizes = torch.tensor([16, 16, 16, 16, 16, 5], dtype=torch.int32)
+    loop = O.block_sparse_attention(q, k, v, index, num, sizes, bs)
+    vec = O.block_sparse_attention_gather(q, k, v, index, num, sizes, bs)
+    assert vec.dtype == loop.dtype
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert torch.allclose(vec.float(), loop.float(), atol=tol, rtol=tol)
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    ql, kl, vl = (t.double().requires_grad_() for t in (q, k, v))
+    g = torch.randn(q.shape, dtype=torch.float64)
+    O.block_sparse_attention_gather(qr, kr, vr, index, num, sizes, bs).backward(g)
+    O.block_sparse_attention(ql, kl, vl, index, num, sizes, bs).backward(g)
+    for a, c in ((qr, ql), (kr, kl), (vr, vl)):
+        assert torch.allclose(a.grad, c.grad, atol=1e-10)

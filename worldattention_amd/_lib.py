@@ -88,6 +88,55 @@ Elu1ReadoutArgs = _struct("wa_elu1_readout_args", [
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
 ])
 
+BsaBwdArgs = _struct("wa_bsa_bwd_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("o", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("dout", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64), ("dout_dtype", c_int32),
+    ("lse", c_void_p),
+    ("index", c_void_p), ("num", c_void_p), ("index_width", c_int64),
+    ("block_sizes", c_void_p),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64), ("block_size", c_int64),
+    ("scale", c_float),
+    ("dq", c_void_p), ("dq_sb", c_int64), ("dq_st", c_int64), ("dq_sh", c_int64), ("dq_accumulate", c_int32),
+    ("dk", c_void_p), ("dk_sb", c_int64), ("dk_st", c_int64), ("dk_sh", c_int64), ("dk_accumulate", c_int32),
+    ("dv", c_void_p), ("dv_sb", c_int64), ("dv_st", c_int64), ("dv_sh", c_int64), ("dv_accumulate", c_int32),
+    ("workspace", c_void_p),
+])
+
+Elu1BwdArgs = _struct("wa_elu1_bwd_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64), ("q_dtype", c_int32),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64), ("kv_dtype", c_int32),
+    ("dout", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64), ("dout_dtype", c_int32),
+    ("state", c_void_p), ("zsum", c_void_p),
+    ("dq", c_void_p), ("dq_sb", c_int64), ("dq_st", c_int64), ("dq_sh", c_int64), ("dq_accumulate", c_int32),
+    ("dk", c_void_p), ("dk_sb", c_int64), ("dk_st", c_int64), ("dk_sh", c_int64), ("dk_accumulate", c_int32),
+    ("dv", c_void_p), ("dv_sb", c_int64), ("dv_st", c_int64), ("dv_sh", c_int64), ("dv_accumulate", c_int32),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64),
+    ("workspace", c_void_p),
+])
+
+HsaFuseArgs = _struct("wa_hsa_fuse_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("sparse", c_void_p), ("s_sb", c_int64), ("s_st", c_int64), ("s_sh", c_int64),
+    ("lin", c_void_p), ("l_sb", c_int64), ("l_st", c_int64), ("l_sh", c_int64),
+    ("head_modes", c_void_p),
+    ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("gate", c_void_p), ("g_sb", c_int64), ("g_st", c_int64), ("g_sh", c_int64),
+    ("gate_w", c_void_p), ("gate_b", c_void_p),
+    ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("attn_round_bf16", c_int32), ("lin_round_bf16", c_int32),
+    ("dout", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64), ("dout_dtype", c_int32),
+    ("dlin", c_void_p), ("dl_sb", c_int64), ("dl_st", c_int64), ("dl_sh", c_int64),
+    ("dq", c_void_p), ("dq_sb", c_int64), ("dq_st", c_int64), ("dq_sh", c_int64), ("dq_accumulate", c_int32),
+    ("dgate_w", c_void_p), ("dgate_b", c_void_p),
+    ("workspace", c_void_p),
+    ("B", c_int64), ("H", c_int64), ("L", c_int64), ("D", c_int64),
+])
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "wa_version": (c_int, []),
@@ -102,6 +151,13 @@ SIGNATURES = {
     "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_elu1_state": (c_int, [POINTER(Elu1StateArgs), c_void_p]),
     "wa_elu1_readout": (c_int, [POINTER(Elu1ReadoutArgs), c_void_p]),
+    "wa_bsa_bwd_workspace_bytes": (c_int64, [c_int64] * 6),
+    "wa_bsa_bwd": (c_int, [POINTER(BsaBwdArgs), c_void_p]),
+    "wa_elu1_bwd_workspace_bytes": (c_int64, [c_int64] * 4),
+    "wa_elu1_bwd": (c_int, [POINTER(Elu1BwdArgs), c_void_p]),
+    "wa_hsa_fuse_fwd": (c_int, [POINTER(HsaFuseArgs), c_void_p]),
+    "wa_hsa_fuse_bwd_workspace_bytes": (c_int64, [c_int64] * 4),
+    "wa_hsa_fuse_bwd": (c_int, [POINTER(HsaFuseArgs), c_void_p]),
 }
 
 

@@ -9,12 +9,12 @@
 // BOTH MFMA operands with transpose reads (ds_read_b64_tr_b16), while the next 64-token tile
 // streams into registers. The readout stages S^T once per workgroup in LDS as a bf16 hi + lo pair
 // (two MFMAs keep ~16 mantissa bits of the fp32 state).
-#include "common.h"
+#include "tile.h"
 
 namespace {
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-#define WA_LDS4(p) ((__attribute__((address_space(3))) s16x4*)(p))
+typedef wa_s16x4 s16x4;
+#define WA_LDS4(p) WA_LDS_S16X4(p)
 
 __device__ __forceinline__ float elu1f(float x) { return x > 0.f ? x + 1.f : __expf(x); }
 
@@ -341,6 +341,283 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   }
 }
 
+// =============================================================================================
+// backward. With n = phi(q) S, den = phi(q) . z, o = n / den and g = dL/do (per head, batch):
+//   dn = g / den,  dden = -(g . o) / den,  dphi(q) = S^T-contraction of dn + dden z,
+//   dS^T[d, e] = sum_q dn[q, d] phi(q)[q, e],  dz = sum_q dden[q] phi(q)[q, :],
+//   dphi(k)[t, e] = sum_d v[t, d] dS^T[d, e] + dz[e],  dv[t, d] = sum_e dS^T[d, e] phi(k)[t, e],
+//   and dx = dphi(x) * phi'(x) with phi'(x) = 1 (x > 0) or e^x.
+// =============================================================================================
+struct Elu1BwdParams {
+  const void* q; int64_t q_sb, q_st, q_sh; int q_dtype;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh; int kv_dtype;
+  const void* g; int64_t g_sb, g_st, g_sh; int g_dtype;
+  const float* state; const float* zsum;
+  float* dq; int64_t dq_sb, dq_st, dq_sh; int dq_acc;
+  float* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
+  float* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
+  const int32_t* heads; int n_heads, H, B, Lq, Lkv, n_qt;
+  float* part;    // [n_qt][B][n_heads][D*D + D]
+  float* dstate;  // [B][n_heads][D*D]
+  float* dz;      // [B][n_heads][D]
+};
+
+__device__ __forceinline__ float elu1_grad(float x) { return x > 0.f ? 1.f : __expf(x); }
+
+__device__ __forceinline__ void load4_any(const void* base, int64_t i, int dtype, float (&f)[4]) {
+  if (dtype == WA_BF16) {
+    const bf16x4 v = *(const bf16x4*)((const bf16_t*)base + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = (float)v[e];
+  } else {
+    const f32x4 v = *(const f32x4*)((const float*)base + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = v[e];
+  }
+}
+
+__device__ __forceinline__ void load8_any(const void* base, int64_t i, int dtype, float (&f)[8]) {
+  if (dtype == WA_BF16) load_row8<bf16_t>((const bf16_t*)base + i, f);
+  else load_row8<float>((const float*)base + i, f);
+}
+
+// Stages an fp32 [D][D] matrix as bf16 hi + lo dual-swizzled tiles (rows = first index).
+template <int D>
+__device__ __forceinline__ void stage_hilo(const float* S, bf16_t* hi_t, bf16_t* lo_t, int tid) {
+  constexpr int CPR = D / 8, SU = D * CPR / 256;
+  f32x4 x0[SU], x1[SU];
+#pragma unroll
+  for (int k = 0; k < SU; ++k) {
+    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    x0[k] = *(const f32x4*)(S + d * D + cc * 8);
+    x1[k] = *(const f32x4*)(S + d * D + cc * 8 + 4);
+  }
+#pragma unroll
+  for (int k = 0; k < SU; ++k) {
+    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = (bf16_t)x0[k][e];
+      lo[e] = (bf16_t)(x0[k][e] - (float)hi[e]);
+      hi[e + 4] = (bf16_t)x1[k][e];
+      lo[e + 4] = (bf16_t)(x1[k][e] - (float)hi[e + 4]);
+    }
+    tile_put8<D>(hi_t, d, cc, hi);
+    tile_put8<D>(lo_t, d, cc, lo);
+  }
+}
+
+// Query side: one workgroup per (128-query tile, head slot, batch), wave w = queries 32w..
+template <int D>
+__global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
+  constexpr int DC = D / 16, DT = D / 32;
+  __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t t_dn[128 * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t t_ph[128 * D];
+  __shared__ float s_z[D], s_dd[128];
+  const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int64_t bh = (int64_t)b * p.n_heads + hs;
+  stage_hilo<D>(p.state + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 256) s_z[e] = p.zsum[bh * D + e];
+  __syncthreads();
+
+  const int ql = w * 32 + l32, qi = tile * 128 + ql;
+  const bool q_ok = qi < p.Lq;
+  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
+  const int64_t goff = (int64_t)b * p.g_sb + (int64_t)(q_ok ? qi : 0) * p.g_st + (int64_t)h * p.g_sh;
+  bf16x8 phf[DC];
+  float den = 0.f;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    float f[8];
+    load8_any(p.q, qoff + c * 16 + g * 8, p.q_dtype, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float ph = q_ok ? wa_bf16_round(elu1f(f[e])) : 0.f;
+      phf[c][e] = (bf16_t)ph;
+      den = fmaf(ph, s_z[c * 16 + g * 8 + e], den);
+    }
+    tile_put8<D>(t_ph, ql, 2 * c + g, phf[c]);
+  }
+  den += __shfl_xor(den, 32, 64);
+  const float inv = q_ok && den > 0.f ? 1.f / den : 0.f;
+
+  // n^T = S^T phi(q)^T, then o, dden, dn (accumulator layout: lane q, d = 32t + 8(r/4) + 4g + r%4)
+  f32x16 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    acc[t] = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      acc[t] = wa_mfma32(tile_row8<D>(s_hi, 32 * t + l32, 2 * c + g), phf[c], acc[t]);
+      acc[t] = wa_mfma32(tile_row8<D>(s_lo, 32 * t + l32, 2 * c + g), phf[c], acc[t]);
+    }
+  }
+  float go = 0.f;
+  bf16x8 dnb[DC];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      float gv[4];
+      load4_any(p.g, goff + 32 * t + 8 * rq + 4 * g, p.g_dtype, gv);
+      bf16x4 dn4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gg = q_ok ? gv[i] : 0.f;
+        go = fmaf(gg, acc[t][rq * 4 + i] * inv, go);
+        const float dn = gg * inv;
+        dnb[2 * t + (rq >> 1)][(rq & 1) * 4 + i] = (bf16_t)dn;
+        dn4[i] = (bf16_t)dn;
+      }
+      // t_dn[q][d]: 4 consecutive channels of one 16-byte chunk
+      const int d0 = 32 * t + 8 * rq + 4 * g;
+      *(bf16x4*)(t_dn + ql * D + (((d0 >> 3) ^ dual_swizzle<D>(ql)) * 8) + (d0 & 7)) = dn4;
+    }
+  }
+  go += __shfl_xor(go, 32, 64);
+  const float dden = -go * inv;
+  if (g == 0) s_dd[ql] = q_ok ? dden : 0.f;
+
+  // dphi(q)^T[e, q] = sum_d S^T[d, e] dn[q, d] (+ dden z[e]); contraction in accumulator order
+#pragma unroll
+  for (int et = 0; et < DT; ++et) {
+    f32x16 da = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      da = wa_mfma32(tile_tr8<D>(s_hi, c, 32 * et, lane), dnb[c], da);
+      da = wa_mfma32(tile_tr8<D>(s_lo, c, 32 * et, lane), dnb[c], da);
+    }
+    if (q_ok) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int e0 = 32 * et + 8 * rq + 4 * g;
+        float qv[4];
+        load4_any(p.q, qoff + e0, p.q_dtype, qv);
+        float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)qi * p.dq_st + (int64_t)h * p.dq_sh + e0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float val = (da[rq * 4 + i] + dden * s_z[e0 + i]) * elu1_grad(qv[i]);
+          dst[i] = p.dq_acc ? dst[i] + val : val;
+        }
+      }
+    }
+  }
+  __syncthreads();  // t_dn, t_ph, s_dd complete
+
+  // partial dS^T[d, e] = sum_q dn[q, d] phi(q)[q, e] over this tile (both operands transposed)
+  float* part = p.part + (((int64_t)tile * p.B + b) * p.n_heads + hs) * (int64_t)(D * D + D);
+  constexpr int TPW = DT * DT / 4;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int dt = D == 128 ? w : (w >> 1);
+    const int et = D == 128 ? i : (w & 1);
+    f32x16 pa = f32x16{};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) pa = wa_mfma32(tile_tr8<D>(t_dn, c, 32 * dt, lane), tile_tr8<D>(t_ph, c, 32 * et, lane), pa);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * dt + 8 * (r >> 2) + 4 * g + (r & 3);
+      part[d * D + 32 * et + l32] = pa[r];
+    }
+  }
+  // dz partial: thread per channel e, fixed query order
+  for (int e = tid; e < D; e += 256) {
+    float sz = 0.f;
+    for (int qq = 0; qq < 128; ++qq)
+      sz = fmaf(s_dd[qq], (float)t_ph[qq * D + (((e >> 3) ^ dual_swizzle<D>(qq)) * 8) + (e & 7)], sz);
+    part[D * D + e] = sz;
+  }
+}
+
+// Key side: one workgroup per (128-token tile, head slot, batch), wave w = tokens 32w..
+template <int D>
+__global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
+  constexpr int DC = D / 16, DT = D / 32;
+  __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
+  __shared__ float s_z[D];
+  const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int64_t bh = (int64_t)b * p.n_heads + hs;
+  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
+  __syncthreads();
+
+  const int tl = tile * 128 + w * 32 + l32;  // this lane's token as an A-operand row
+  const bool t_ok = tl < p.Lkv;
+  const int64_t koff = (int64_t)b * p.k_sb + (int64_t)(t_ok ? tl : 0) * p.k_st + (int64_t)h * p.k_sh;
+  const int64_t voff = (int64_t)b * p.v_sb + (int64_t)(t_ok ? tl : 0) * p.v_st + (int64_t)h * p.v_sh;
+  bf16x8 vf[DC], pk[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    float fk[8], fv[8];
+    load8_any(p.k, koff + c * 16 + g * 8, p.kv_dtype, fk);
+    load8_any(p.v, voff + c * 16 + g * 8, p.kv_dtype, fv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pk[c][e] = (bf16_t)(t_ok ? elu1f(fk[e]) : 0.f);
+      vf[c][e] = (bf16_t)(t_ok ? fv[e] : 0.f);
+    }
+  }
+  const int tb = tile * 128 + w * 32;  // accumulator rows: tokens tb + 8(r/4) + 4g + r%4
+#pragma unroll
+  for (int jt = 0; jt < DT; ++jt) {
+    f32x16 dk = f32x16{}, dv = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      // dphi(k)[t, e] = sum_d v[t, d] dS^T[d, e]   (B: column e of dS^T, rows d natural order)
+      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_hi, c, 32 * jt, lane), dk);
+      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_lo, c, 32 * jt, lane), dk);
+      // dv[t, d] = sum_e phi(k)[t, e] dS^T[d, e]   (B: row d of dS^T)
+      dv = wa_mfma32(pk[c], tile_row8<D>(s_hi, 32 * jt + l32, 2 * c + g), dv);
+      dv = wa_mfma32(pk[c], tile_row8<D>(s_lo, 32 * jt + l32, 2 * c + g), dv);
+    }
+    const int col = 32 * jt + l32;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
+      if (t < p.Lkv) {
+        const int64_t ko = (int64_t)b * p.k_sb + (int64_t)t * p.k_st + (int64_t)h * p.k_sh + col;
+        const float kx = p.kv_dtype == WA_BF16 ? (float)((const bf16_t*)p.k)[ko] : ((const float*)p.k)[ko];
+        float* dkp = p.dk + (int64_t)b * p.dk_sb + (int64_t)t * p.dk_st + (int64_t)h * p.dk_sh + col;
+        float* dvp = p.dv + (int64_t)b * p.dv_sb + (int64_t)t * p.dv_st + (int64_t)h * p.dv_sh + col;
+        const float vk = (dk[r] + s_z[col]) * elu1_grad(kx);
+        *dkp = p.dk_acc ? *dkp + vk : vk;
+        *dvp = p.dv_acc ? *dvp + dv[r] : dv[r];
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) elu1_bwd_reduce_kernel(Elu1BwdParams p, int D) {
+  const int64_t per = (int64_t)D * D + D;
+  const int64_t total = (int64_t)p.B * p.n_heads * per;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  int c = 0;
+  for (; c + 4 <= p.n_qt; c += 4) {
+    a0 += p.part[(int64_t)c * total + i];
+    a1 += p.part[(int64_t)(c + 1) * total + i];
+    a2 += p.part[(int64_t)(c + 2) * total + i];
+    a3 += p.part[(int64_t)(c + 3) * total + i];
+  }
+  for (; c < p.n_qt; ++c) a0 += p.part[(int64_t)c * total + i];
+  const float s = (a0 + a1) + (a2 + a3);
+  const int64_t bh = i / per, r = i % per;
+  if (r < (int64_t)D * D) p.dstate[bh * D * D + r] = s;
+  else p.dz[bh * D + (r - (int64_t)D * D)] = s;
+}
+
 int state_chunks(int64_t B, int64_t nh, int64_t L) {
   const int64_t target = 256;
   const int64_t per_bh = (target + B * nh - 1) / (B * nh);
@@ -414,4 +691,55 @@ extern "C" int wa_elu1_readout(const wa_elu1_readout_args* a, void* stream) {
   if (a->D == 128) hipLaunchKernelGGL(elu1_readout_kernel<128>, grid, dim3(256), 0, s, rp);
   else hipLaunchKernelGGL(elu1_readout_kernel<64>, grid, dim3(256), 0, s, rp);
   return wa_launch_status("elu1_readout");
+}
+
+extern "C" int64_t wa_elu1_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t D) {
+  const int64_t nqt = (Lq + 127) / 128;
+  return ((nqt * B * n_heads * (D * D + D) + B * n_heads * (D * D + D)) * 4 + 255) / 256 * 256;
+}
+
+extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->q && a->k && a->v && a->dout && a->state && a->zsum && a->workspace,
+               "wa_elu1_bwd: null argument");
+  WA_CHECK_ARG(a->dq && a->dk && a->dv, "wa_elu1_bwd: dq, dk and dv are required");
+  WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_elu1_bwd: head dim %lld not in {64, 128}", (long long)a->D);
+  WA_CHECK_ARG((a->q_dtype == WA_F32 || a->q_dtype == WA_BF16) && (a->kv_dtype == WA_F32 || a->kv_dtype == WA_BF16) &&
+                   (a->dout_dtype == WA_F32 || a->dout_dtype == WA_BF16),
+               "wa_elu1_bwd: bad dtype");
+  WA_CHECK_ARG(a->Lq > 0 && a->Lkv > 0 && a->H > 0 && a->B >= 0, "wa_elu1_bwd: bad sizes");
+  const int64_t vq = a->q_dtype == WA_BF16 ? 8 : 4, vk = a->kv_dtype == WA_BF16 ? 8 : 4, vg = a->dout_dtype == WA_BF16 ? 8 : 4;
+  WA_CHECK_ARG(wa_aligned16(a->q) && wa_aligned16(a->k) && wa_aligned16(a->v) && wa_aligned16(a->dout) &&
+                   wa_aligned16(a->state) && wa_aligned16(a->workspace) && a->q_sb % vq == 0 && a->q_st % vq == 0 &&
+                   a->q_sh % vq == 0 && a->k_sb % vk == 0 && a->k_st % vk == 0 && a->k_sh % vk == 0 &&
+                   a->v_sb % vk == 0 && a->v_st % vk == 0 && a->v_sh % vk == 0 && a->d_sb % vg == 0 &&
+                   a->d_st % vg == 0 && a->d_sh % vg == 0,
+               "wa_elu1_bwd: tensors must be 16-byte aligned with 16-byte aligned rows");
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  if (a->B == 0 || nh == 0) return WA_OK;
+  Elu1BwdParams bp{};
+  bp.q = a->q; bp.q_sb = a->q_sb; bp.q_st = a->q_st; bp.q_sh = a->q_sh; bp.q_dtype = a->q_dtype;
+  bp.k = a->k; bp.k_sb = a->k_sb; bp.k_st = a->k_st; bp.k_sh = a->k_sh;
+  bp.v = a->v; bp.v_sb = a->v_sb; bp.v_st = a->v_st; bp.v_sh = a->v_sh; bp.kv_dtype = a->kv_dtype;
+  bp.g = a->dout; bp.g_sb = a->d_sb; bp.g_st = a->d_st; bp.g_sh = a->d_sh; bp.g_dtype = a->dout_dtype;
+  bp.state = a->state; bp.zsum = a->zsum;
+  bp.dq = a->dq; bp.dq_sb = a->dq_sb; bp.dq_st = a->dq_st; bp.dq_sh = a->dq_sh; bp.dq_acc = a->dq_accumulate;
+  bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
+  bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
+  bp.heads = a->heads; bp.n_heads = (int)nh; bp.H = (int)a->H; bp.B = (int)a->B; bp.Lq = (int)a->Lq;
+  bp.Lkv = (int)a->Lkv; bp.n_qt = (int)((a->Lq + 127) / 128);
+  bp.part = (float*)a->workspace;
+  bp.dstate = bp.part + (int64_t)bp.n_qt * a->B * nh * (a->D * a->D + a->D);
+  bp.dz = bp.dstate + a->B * nh * a->D * a->D;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 gq((unsigned)bp.n_qt, (unsigned)nh, (unsigned)a->B), gk((unsigned)((a->Lkv + 127) / 128), (unsigned)nh, (unsigned)a->B);
+  const int64_t total = a->B * nh * (a->D * a->D + a->D);
+  int rc;
+  if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_q_kernel<128>, gq, dim3(256), 0, s, bp);
+  else hipLaunchKernelGGL(elu1_bwd_q_kernel<64>, gq, dim3(256), 0, s, bp);
+  if ((rc = wa_launch_status("elu1_bwd_q"))) return rc;
+  hipLaunchKernelGGL(elu1_bwd_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, bp, (int)a->D);
+  if ((rc = wa_launch_status("elu1_bwd_reduce"))) return rc;
+  if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv_kernel<128>, gk, dim3(256), 0, s, bp);
+  else hipLaunchKernelGGL(elu1_bwd_kv_kernel<64>, gk, dim3(256), 0, s, bp);
+  return wa_launch_status("elu1_bwd_kv");
 }

@@ -1,0 +1,271 @@
+"""Differentiable HSA on the GPU (the training path of ``wan/modules/hsa/attention.py:153-259``).
+
+The reference differentiates its torch path with autograd (and the Triton kernels with
+``block_sparse_triton.py:353-368``). Here the forward keeps the two branch outputs and the gate
+apart (fp32), fuses them with ``wa_hsa_fuse_fwd``, and the backward runs
+``wa_hsa_fuse_bwd`` -> ``wa_bsa_bwd`` (sparse branch) -> ``wa_elu1_bwd`` or a dense ``wa_bsa_bwd``
+over the compressed keys (linear branch), all accumulating into fp32 gradient buffers. Routing is
+not differentiated, as in the reference (its ``argsort`` / thresholds carry no gradient).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from ._bwd import bsa_backward
+from .block_sparse import bsa_forward
+from .routing import _route, block_counts, pool_blhd
+
+__all__ = ["hsa_attention_autograd", "compress_autograd", "elu1_backward", "fuse_forward", "fuse_backward"]
+
+MODE_SPARSE, MODE_LINEAR = 1, 2
+
+
+def _blhd(t):
+    return _lib.blhd(t) if t is not None else (None, 0, 0, 0)
+
+
+def _fuse_args(q, sparse, lin, modes_t, gate, spec, *, out=None, dout=None, dlin=None, dq=None, dgw=None, dgb=None,
+               ws=None, attn_round, lin_round):
+    bsz, length, heads, d = q.shape
+    return _lib.HsaFuseArgs(
+        *_lib.blhd(q), *_blhd(sparse), *_blhd(lin), modes_t.data_ptr(),
+        *_blhd(out), _lib.dtype_code(out) if out is not None else 0,
+        *_blhd(gate), _lib.ptr(spec.w), _lib.ptr(spec.b),
+        int(spec.pre_bf16), int(spec.out_bf16), int(attn_round), int(lin_round),
+        *_blhd(dout), _lib.dtype_code(dout) if dout is not None else 0,
+        *_blhd(dlin), *_blhd(dq), 1,
+        _lib.ptr(dgw), _lib.ptr(dgb), _lib.ptr(ws),
+        bsz, heads, length, d)
+
+
+def fuse_forward(q, sparse, lin, modes_t, gate, spec, out, *, attn_round, lin_round):
+    """``out = [sparse] + [gate * lin]`` per head mode (``wa_hsa_fuse_fwd``); fills ``gate``."""
+    dev = _lib.require_gpu(q, out)
+    args = _fuse_args(q, sparse, lin, modes_t, gate, spec, out=out, attn_round=attn_round, lin_round=lin_round)
+    _lib.call("wa_hsa_fuse_fwd", args, _lib.stream_ptr(dev))
+
+
+def fuse_backward(q, lin, modes_t, gate, spec, dout, dlin, dq, *, lin_round):
+    """``dlin = dout * gate``; adds the gate path into ``dq``; returns ``(dW, db)`` or ``(None, None)``."""
+    dev = _lib.require_gpu(q, dout)
+    bsz, length, heads, d = q.shape
+    dgw = dgb = ws = None
+    if spec.w is not None:
+        dgw = torch.empty((d, d), dtype=torch.float32, device=dev)
+        dgb = torch.empty((d,), dtype=torch.float32, device=dev)
+        ws = torch.empty((_lib.lib().wa_hsa_fuse_bwd_workspace_bytes(bsz, heads, length, d),), dtype=torch.uint8,
+                         device=dev)
+    args = _fuse_args(q, None, lin, modes_t, gate, spec, dout=dout, dlin=dlin, dq=dq, dgw=dgw, dgb=dgb, ws=ws,
+                      attn_round=False, lin_round=lin_round)
+    _lib.call("wa_hsa_fuse_bwd", args, _lib.stream_ptr(dev))
+    return dgw, dgb
+
+
+def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv):
+    """Adds the elu(x)+1 branch's gradients into fp32 ``dq``, ``dk``, ``dv`` (``wa_elu1_bwd``)."""
+    dev = _lib.require_gpu(q, k, v, dout)
+    if k.dtype != v.dtype:
+        v = v.to(k.dtype)
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    bsz, lq, heads, d = q.shape
+    lkv = k.shape[1]
+    n = heads_t.numel()
+    ws = torch.empty((_lib.lib().wa_elu1_bwd_workspace_bytes(bsz, n, lq, d),), dtype=torch.uint8, device=dev)
+    args = _lib.Elu1BwdArgs(
+        *_lib.blhd(q), _lib.dtype_code(q), *_lib.blhd(k), *_lib.blhd(v), _lib.dtype_code(k),
+        *_lib.blhd(dout), _lib.dtype_code(dout), state.data_ptr(), zsum.data_ptr(),
+        *_lib.blhd(dq), 1, *_lib.blhd(dk), 1, *_lib.blhd(dv), 1,
+        heads_t.data_ptr(), n, bsz, heads, lq, lkv, d, ws.data_ptr())
+    _lib.call("wa_elu1_bwd", args, _lib.stream_ptr(dev))
+
+
+# ----------------------------------------------------------------------------------------------
+# low-rank compression (attention.py:64-110) under autograd
+# ----------------------------------------------------------------------------------------------
+def _compress_backward(grad, x, proj, segment_len, block_size):
+    """Gradients of ``out_seg = E[:r, :len] @ x_seg`` per segment: ``dx_seg = E^T dout_seg`` and
+    ``dE[:r, :len] = sum_{b, h} dout_seg x_seg^T`` (fp32 library GEMMs over [B, H] batches)."""
+    bsz, length, heads, d = x.shape
+    seg = segment_len if segment_len > 0 else length
+    dx = torch.zeros((bsz, length, heads, d), dtype=torch.float32, device=x.device)
+    dproj = torch.zeros(proj.shape, dtype=torch.float32, device=x.device)
+    row = 0
+    for start in range(0, length, seg):
+        n = min(seg, length - start)
+        r = min(proj.shape[0], math.ceil(n / block_size))
+        e = proj[:r, :n].float().contiguous()                                     # [r, n]
+        go = grad[:, row:row + r].float().permute(0, 2, 1, 3).contiguous()        # [B, H, r, D]
+        xs = x[:, start:start + n].float().permute(0, 2, 1, 3).contiguous()       # [B, H, n, D]
+        dx[:, start:start + n] = torch.matmul(e.t().contiguous(), go).permute(0, 2, 1, 3)
+        dproj[:r, :n] += torch.matmul(go.reshape(-1, r, d), xs.reshape(-1, n, d).transpose(1, 2).contiguous()).sum(0)
+        row += r
+    return dx, dproj
+
+
+class _Compress(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, proj, segment_len, block_size):
+        from .attention import _compress
+        ctx.save_for_backward(x, proj)
+        ctx.cfg = (segment_len, block_size)
+        return _compress(x, proj, segment_len=segment_len, block_size=block_size, layout="blhd")
+
+    @staticmethod
+    def backward(ctx, grad):
+        x, proj = ctx.saved_tensors
+        dx, dproj = _compress_backward(grad, x, proj, *ctx.cfg)
+        return dx.to(x.dtype), dproj.to(proj.dtype), None, None
+
+
+def compress_autograd(x, proj, segment_len, block_size):
+    """Differentiable ``compress_kv`` of a ``[B, L, H, D]`` tensor (``attention.py:64-110``)."""
+    return _Compress.apply(x, proj, segment_len, block_size)
+
+
+# ----------------------------------------------------------------------------------------------
+# hsa_attention under autograd
+# ----------------------------------------------------------------------------------------------
+class _HSA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b, cfg):
+        from .attention import GateSpec, HeadPlan, _compress, _per_head_k, elu1_readout, elu1_state
+
+        block_size, routing, topk, linear_mode = cfg["block_size"], cfg["routing"], cfg["topk"], cfg["linear_mode"]
+        bsz, q_len, heads, d = q.shape
+        kv_len = k.shape[1]
+        dev = _lib.require_gpu(q, k, v, k_coarse, v_coarse)
+        plan = HeadPlan(heads, cfg["head_modes"], dev)
+        if linear_mode == "lowrank":
+            comp = v_coarse.dtype if v_coarse is not None else v.dtype
+        else:
+            comp = v.dtype
+        if comp not in (torch.float32, torch.bfloat16):
+            comp = torch.float32
+
+        class _Gate:
+            pass
+        gate_lin = None
+        if gate_w is not None:
+            gate_lin = _Gate()
+            gate_lin.weight, gate_lin.bias = gate_w, gate_b
+        spec = GateSpec(gate_lin, comp)
+        lin_round = comp == torch.bfloat16
+        modes = [(MODE_SPARSE if h in plan.sparse else 0) | (MODE_LINEAR if h in plan.linear else 0)
+                 for h in range(heads)]
+        modes_t = _lib.head_list(modes, dev)
+
+        qb, kb, vb = _lib.kernel_ready(q), _lib.kernel_ready(k), _lib.kernel_ready(v)
+        f32 = dict(dtype=torch.float32, device=dev)
+        sparse = torch.empty((bsz, q_len, heads, d), **f32) if plan.sparse else None
+        lin = torch.empty((bsz, q_len, heads, d), **f32) if plan.linear else None
+        gate = torch.empty((bsz, q_len, heads, d), **f32) if plan.linear else None
+        saved = dict(plan=plan, spec=spec, modes_t=modes_t, lin_round=lin_round, comp=comp)
+        lse_s = lse_l = kc = vc = kcb = vcb = state = zsum = route = None
+
+        if plan.linear:
+            lt = plan.t["linear"]
+            if linear_mode == "elu1":
+                state, zsum = elu1_state(k, v, lt)
+                elu1_readout(q, state, zsum, lt, lin)
+            else:
+                if k_coarse is None:
+                    kc = _compress(k, k_proj_mat, segment_len=cfg["proj_segment_len"], block_size=block_size,
+                                   layout="blhd")
+                    vc = _compress(v, v_proj_mat, segment_len=cfg["proj_segment_len"], block_size=block_size,
+                                   layout="blhd")
+                else:
+                    kc, vc = k_coarse, v_coarse
+                kcb, vcb = _lib.kernel_ready(kc), _lib.kernel_ready(vc)
+                _, lse_l = bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
+                                       heads=lt, out=lin, lq=q_len, want_lse=True)
+        if plan.sparse:
+            _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+            st = plan.t["sparse"]
+            qp = pool_blhd(q, q_len, nq, block_size, heads=st)
+            kp = pool_blhd(k, kv_len, nkv, block_size, heads=st)
+            visits = None
+            if routing == "gini":
+                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=cfg["tau_min"],
+                                  tau_max=cfg["tau_max"], heads=st)
+            else:
+                ks = _per_head_k(topk, heads)
+                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st)
+                visits = [min(ks[h], nkv) for h in plan.sparse]
+            _, lse_s = bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size,
+                                   layout="blhd", heads=st, out=sparse, lq=q_len, lkv=kv_len, want_lse=True,
+                                   visits=visits)
+        out = torch.empty((bsz, q_len, heads, d), dtype=comp, device=dev)
+        fuse_forward(qb, sparse, lin, modes_t, gate, spec, out, attn_round=True, lin_round=lin_round)
+
+        ctx.cfg = cfg
+        ctx.extra = saved
+        ctx.has_coarse = k_coarse is not None
+        ctx.dtypes = tuple(t.dtype if t is not None else None
+                           for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b))
+        ctx.save_for_backward(q, k, v, qb, kb, vb, sparse, lin, gate, lse_s, lse_l, kc, vc, kcb, vcb, state, zsum,
+                              route.index if route is not None else None,
+                              route.num if route is not None else None, k_proj_mat, v_proj_mat)
+        return out if out.dtype == q.dtype else out.to(q.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        (q, k, v, qb, kb, vb, sparse, lin, gate, lse_s, lse_l, kc, vc, kcb, vcb, state, zsum, index, num,
+         k_proj_mat, v_proj_mat) = ctx.saved_tensors
+        cfg, ex = ctx.cfg, ctx.extra
+        plan, spec = ex["plan"], ex["spec"]
+        dev = q.device
+        bsz, q_len, heads, d = q.shape
+        kv_len = k.shape[1]
+        block_size = cfg["block_size"]
+        dout = dout if dout.stride(-1) == 1 and dout.dtype in (torch.float32, torch.bfloat16) else dout.float().contiguous()
+        f32 = dict(dtype=torch.float32, device=dev)
+        dq = torch.zeros((bsz, q_len, heads, d), **f32)
+        dk = torch.zeros((bsz, kv_len, heads, d), **f32)
+        dv = torch.zeros((bsz, kv_len, heads, d), **f32)
+        dgw = dgb = dkc = dvc = dEk = dEv = None
+        if plan.linear:
+            dlin = torch.empty((bsz, q_len, heads, d), **f32)
+            dgw, dgb = fuse_backward(qb, lin, ex["modes_t"], gate, spec, dout, dlin, dq, lin_round=ex["lin_round"])
+        if plan.sparse:
+            bsa_backward(qb, kb, vb, sparse, lse_s, dout, index=index, num=num, block_size=block_size,
+                         layout="blhd", heads=plan.t["sparse"], lq=q_len, lkv=kv_len, dq=dq, dk=dk, dv=dv,
+                         accumulate=True)
+        if plan.linear:
+            lt = plan.t["linear"]
+            if cfg["linear_mode"] == "elu1":
+                elu1_backward(q, k, v, dlin, state, zsum, lt, dq, dk, dv)
+            else:
+                lc = kcb.shape[1]
+                dkc = torch.zeros((bsz, lc, heads, d), **f32)
+                dvc = torch.zeros((bsz, lc, heads, d), **f32)
+                bsa_backward(qb, kcb, vcb, lin, lse_l, dlin, index=None, num=None, block_size=block_size,
+                             layout="blhd", heads=lt, lq=q_len, lkv=lc, dq=dq, dk=dkc, dv=dvc, accumulate=True)
+                if not ctx.has_coarse:
+                    dk_c, dEk = _compress_backward(dkc, k, k_proj_mat, cfg["proj_segment_len"], block_size)
+                    dv_c, dEv = _compress_backward(dvc, v, v_proj_mat, cfg["proj_segment_len"], block_size)
+                    dk += dk_c
+                    dv += dv_c
+        qd, kd, vd, kcd, vcd, ekd, evd, gwd, gbd = ctx.dtypes
+
+        def cast(t, dt):
+            return None if t is None or dt is None else t.to(dt)
+        return (cast(dq, qd), cast(dk, kd), cast(dv, vd),
+                cast(dkc, kcd) if ctx.has_coarse else None, cast(dvc, vcd) if ctx.has_coarse else None,
+                cast(dEk, ekd), cast(dEv, evd), cast(dgw, gwd), cast(dgb, gbd), None)
+
+
+def hsa_attention_autograd(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
+                           tau_max, proj_segment_len, routing, topk, head_modes, linear_mode):
+    """Differentiable :func:`hsa_attention` (q, k, v, coarse caches, projections and gate)."""
+    if block_size not in (64, 128) or q.shape[-1] not in (64, 128):
+        raise ValueError("block_size and head_dim must each be 64 or 128 for the gfx950 kernels")
+    gate_w = gate_lin.weight if gate_lin is not None else None
+    gate_b = getattr(gate_lin, "bias", None) if gate_lin is not None else None
+    cfg = dict(block_size=block_size, tau_min=tau_min, tau_max=tau_max, proj_segment_len=proj_segment_len,
+               routing=routing, topk=topk, head_modes=head_modes, linear_mode=linear_mode)
+    return _HSA.apply(q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b, cfg)

@@ -217,19 +217,16 @@ def elu1_readout(q, state, zsum, heads_t, out, *, epilogue=_lib.WA_EPI_PLAIN, ga
 class GateSpec:
     """Kernel-side view of the fusion gate (``attention.py:246-251``)."""
 
-    _cache: dict = {}
-
-    @classmethod
-    def _converted(cls, t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-        # kernel-side copies of the gate parameters, refreshed when the parameter changes
-        key = (t.data_ptr(), t.dtype, dtype)
-        hit = cls._cache.get(key)
-        if hit is None or hit[0] != t._version:
-            hit = (t._version, t.detach().to(dtype).contiguous())
-            if len(cls._cache) > 64:
-                cls._cache.clear()
-            cls._cache[key] = hit
-        return hit[1]
+    @staticmethod
+    def _converted(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """Kernel-side copy of a gate parameter, held on the parameter object itself (so it dies
+        with it) and refreshed when the parameter is modified in place (its version counter)."""
+        per_t = t.__dict__.setdefault("_wa_kernel_copies", {})
+        hit = per_t.get(dtype)
+        if hit is None or hit[0] != t._version or hit[1] != t.data_ptr():
+            hit = (t._version, t.data_ptr(), t.detach().to(dtype).contiguous())
+            per_t[dtype] = hit
+        return hit[2]
 
     def __init__(self, gate_lin: Optional[nn.Module], comp_dtype: torch.dtype):
         if gate_lin is not None:

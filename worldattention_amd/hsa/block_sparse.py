@@ -140,8 +140,9 @@ class _BlockSparseAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, index, num, block_sizes, block_size):
         qb, kb, vb = _prep(q), _prep(k), _prep(v)
+        # fp32 output: the backward's delta = rowsum(o * do) uses it unrounded
         out, lse = bsa_forward(qb, kb, vb, index=index, num=num, block_size=block_size,
-                               block_sizes=block_sizes, out_dtype=torch.bfloat16, want_lse=True)
+                               block_sizes=block_sizes, out_dtype=torch.float32, want_lse=True)
         ctx.save_for_backward(qb, kb, vb, out, lse, index, num, block_sizes)
         ctx.block_size = block_size
         ctx.dtypes = (q.dtype, k.dtype, v.dtype)
@@ -197,6 +198,7 @@ def block_sparse_attention_reference(q, k, v, q2k_index, q2k_num, block_sizes, b
     sizes = block_sizes.to(device=q.device, dtype=torch.int32).contiguous()
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
         return _BlockSparseAttention.apply(q, k, v, index, num, sizes, block_size)
+    out_dtype = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
     out, _ = bsa_forward(_prep(q), _prep(k), _prep(v), index=index, num=num, block_size=block_size,
-                         block_sizes=sizes, out_dtype=torch.bfloat16)
+                         block_sizes=sizes, out_dtype=out_dtype)
     return out.to(q.dtype)
