@@ -271,6 +271,85 @@ int wa_hsa_fuse_fwd(const wa_hsa_fuse_args* args, void* stream);
 int64_t wa_hsa_fuse_bwd_workspace_bytes(int64_t B, int64_t H, int64_t L, int64_t D);
 int wa_hsa_fuse_bwd(const wa_hsa_fuse_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* HKV tier: page summaries, page selection, temporal re-rotation, host-tier copies             */
+/* ------------------------------------------------------------------------------------------ */
+
+/* Segment means of a [B, T, C] tensor (C = H*D; element (b, t, c) at x + b*x_sb + t*x_st + c) into
+ * fp32 out[n_seg][C]:  out[s][c] = mean_b ( mean_{t in segment s} y[b][t][c] ).
+ * Segment s is [s*seg_tokens, min((s+1)*seg_tokens, T)), or [spans[2s], spans[2s+1]) when `spans`
+ * (device int32 [n_seg][2]) is given; max_seg_tokens bounds every segment's length.
+ * With `factors` (device complex64 as float pairs, [n_rows][n_temporal]), y is x with complex pair
+ * p < n_temporal of every head multiplied by factors[min(t / row_tokens, n_rows - 1)][p] in fp32
+ * and rounded to x's dtype (the reference de-ropes into the cache dtype, then pools in fp32);
+ * without `factors`, y = x. With `normalize`, each out row becomes row / max(|row|_2, 1e-12).
+ * Replaces page_key_index + derope_temporal (pipeline/hkv/retrieval.py:50-72, rope.py:70-82),
+ * query_index (retrieval.py:41-47) and prompt_index (retrieval.py:32-38, normalize = 1).
+ * Workspace: wa_hkv_summary_workspace_bytes(B, n_seg, C, max_seg_tokens). */
+typedef struct wa_hkv_summary_args {
+  const void* x; int64_t x_sb, x_st; int32_t x_dtype;
+  int64_t B, T, H, D;
+  int64_t seg_tokens; const int32_t* spans; int64_t n_seg; int64_t max_seg_tokens;
+  const float* factors; int64_t n_temporal, row_tokens, n_rows;
+  int32_t normalize;
+  float* out;
+  void* workspace;
+} wa_hkv_summary_args;
+int64_t wa_hkv_summary_workspace_bytes(int64_t B, int64_t n_seg, int64_t C, int64_t max_seg_tokens);
+int wa_hkv_page_summary(const wa_hkv_summary_args* args, void* stream);
+
+/* Page scoring and selection in one workgroup:
+ *   scores[p] = (index[p] . query) / scale   (no division when scale <= 0), p < n_pages <= 4096,
+ * then the k highest in descending order, the lower page index first among equal scores (NaN
+ * ranks highest), into sel (int32) and sel_scores. Pages with mask[p] != 0 (device uint8,
+ * optional) are never selected; slots beyond the unmasked count get sel = -1, score = -inf.
+ * Replaces score_pages + select_topk_pages (pipeline/hkv/retrieval.py:75-89, 105-126) and the
+ * stage-1 cosine ranking select_top_chunks (retrieval.py:92-102, scale = 0). */
+#define WA_HKV_MAX_PAGES 4096
+typedef struct wa_hkv_topk_args {
+  const float* index; int64_t index_stride;   /* [n_pages][dim] fp32 */
+  const float* query;                          /* [dim] fp32 */
+  int64_t n_pages, dim;
+  float scale;
+  const uint8_t* mask;
+  int64_t k;
+  float* scores;                               /* optional [n_pages] */
+  int32_t* sel; float* sel_scores;             /* [k] each */
+} wa_hkv_topk_args;
+int wa_hkv_score_topk(const wa_hkv_topk_args* args, void* stream);
+
+/* Temporal re-rotation of tokens [t0, t1) of a BLHD tensor: complex pair p < n_temporal of every
+ * head is multiplied by factors[row][p] (complex64 as float pairs, fp32 math) and rounded to the
+ * tensor's dtype, row = rows[t - t0] (device int32) when `rows` is given, else
+ * min((t - t0) / row_tokens, n_rows - 1). src == dst rotates in place (only the temporal band is
+ * read and written); otherwise every channel is copied to dst (same dtype). Replaces
+ * shift_temporal_rope (pipeline/hkv/rope.py:50-67, one factor per installed page at
+ * cache.py:229-238 with the moves of cache.py:273-286) and derope_temporal (rope.py:70-82). */
+typedef struct wa_rerope_args {
+  const void* src; int64_t s_sb, s_st, s_sh;
+  void* dst; int64_t d_sb, d_st, d_sh;
+  int32_t dtype;
+  int64_t B, t0, t1, H, D;
+  const float* factors; int64_t n_temporal, n_rows;
+  const int32_t* rows; int64_t row_tokens;
+} wa_rerope_args;
+int wa_rerope(const wa_rerope_args* args, void* stream);
+
+/* Host-tier copies: each is `rows` rows of `width` bytes at the given pitches, enqueued in order
+ * on `stream` (hipMemcpy2DAsync); `done` (hipEvent_t, optional) is recorded after the last one.
+ * The host side must be pinned (hipHostMalloc / torch pin_memory) and is checked.
+ * wa_hkv_gather_async: pinned host -> device, the page install of HKVCache.apply
+ *   (pipeline/hkv/cache.py:229-246, which copies page by page with synchronous .to(device));
+ * wa_hkv_store_async: device -> pinned host, the chunk store of HKVCache.store (cache.py:104-107,
+ *   pageable .to("cpu")). */
+typedef struct wa_hkv_copy {
+  const void* src; int64_t src_pitch;
+  void* dst; int64_t dst_pitch;
+  int64_t width, rows;
+} wa_hkv_copy;
+int wa_hkv_gather_async(const wa_hkv_copy* copies, int64_t n, void* stream, void* done);
+int wa_hkv_store_async(const wa_hkv_copy* copies, int64_t n, void* stream, void* done);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,7 @@ def declared_functions():
 def declared_structs():
     names = []
     for h in HEADERS:
-        names += re.findall(r"typedef struct (wa_\w+_args)\s*\{", open(h).read())
+        names += re.findall(r"typedef struct (wa_\w+)\s*\{", open(h).read())
     return names
 
 

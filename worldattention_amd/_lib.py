@@ -137,6 +137,43 @@ HsaFuseArgs = _struct("wa_hsa_fuse_args", [
     ("B", c_int64), ("H", c_int64), ("L", c_int64), ("D", c_int64),
 ])
 
+HkvSummaryArgs = _struct("wa_hkv_summary_args", [
+    ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_dtype", c_int32),
+    ("B", c_int64), ("T", c_int64), ("H", c_int64), ("D", c_int64),
+    ("seg_tokens", c_int64), ("spans", c_void_p), ("n_seg", c_int64), ("max_seg_tokens", c_int64),
+    ("factors", c_void_p), ("n_temporal", c_int64), ("row_tokens", c_int64), ("n_rows", c_int64),
+    ("normalize", c_int32),
+    ("out", c_void_p),
+    ("workspace", c_void_p),
+])
+
+HKV_MAX_PAGES = 4096
+
+HkvTopkArgs = _struct("wa_hkv_topk_args", [
+    ("index", c_void_p), ("index_stride", c_int64),
+    ("query", c_void_p),
+    ("n_pages", c_int64), ("dim", c_int64),
+    ("scale", c_float),
+    ("mask", c_void_p),
+    ("k", c_int64),
+    ("scores", c_void_p), ("sel", c_void_p), ("sel_scores", c_void_p),
+])
+
+RopeArgs = _struct("wa_rerope_args", [
+    ("src", c_void_p), ("s_sb", c_int64), ("s_st", c_int64), ("s_sh", c_int64),
+    ("dst", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("t0", c_int64), ("t1", c_int64), ("H", c_int64), ("D", c_int64),
+    ("factors", c_void_p), ("n_temporal", c_int64), ("n_rows", c_int64),
+    ("rows", c_void_p), ("row_tokens", c_int64),
+])
+
+HkvCopy = _struct("wa_hkv_copy", [
+    ("src", c_void_p), ("src_pitch", c_int64),
+    ("dst", c_void_p), ("dst_pitch", c_int64),
+    ("width", c_int64), ("rows", c_int64),
+])
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "wa_version": (c_int, []),
@@ -158,6 +195,12 @@ SIGNATURES = {
     "wa_hsa_fuse_fwd": (c_int, [POINTER(HsaFuseArgs), c_void_p]),
     "wa_hsa_fuse_bwd_workspace_bytes": (c_int64, [c_int64] * 4),
     "wa_hsa_fuse_bwd": (c_int, [POINTER(HsaFuseArgs), c_void_p]),
+    "wa_hkv_summary_workspace_bytes": (c_int64, [c_int64] * 4),
+    "wa_hkv_page_summary": (c_int, [POINTER(HkvSummaryArgs), c_void_p]),
+    "wa_hkv_score_topk": (c_int, [POINTER(HkvTopkArgs), c_void_p]),
+    "wa_rerope": (c_int, [POINTER(RopeArgs), c_void_p]),
+    "wa_hkv_gather_async": (c_int, [POINTER(HkvCopy), c_int64, c_void_p, c_void_p]),
+    "wa_hkv_store_async": (c_int, [POINTER(HkvCopy), c_int64, c_void_p, c_void_p]),
 }
 
 
