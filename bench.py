@@ -1,15 +1,21 @@
-"""Benchmark of the HSA forward at the Wan-1.3B chunk shape on one GPU.
+"""Benchmark of the HSA + HKV path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only cfg2,cfg3,cfg4,cfg5]
 
+Headline (``value``, ``ms_per_step``, ``roofline``, ``cpu_baseline``): cfg 2, the Wan-1.3B chunk.
 A step is one ``hsa_forward`` call (routing + sparse branch + elu(x)+1 linear branch + fusion) on
-synthetic seeded inputs already resident in HBM: B=1, H=12 (8 sparse heads with per-head top-k
-from {8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16.
+seeded synthetic inputs already resident in HBM: B=1, H=12 (8 sparse heads with per-head top-k from
+{8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16. ``value`` is the
+effective sparse TFLOP/s of the whole call (useful sparse FLOP / call time); ``roofline`` is the
+sparse kernel's own rate, timed with HIP events on the stream it runs on.
 
-Prints one JSON line: ``value`` is the effective sparse TFLOP/s (useful sparse FLOP of one call /
-time of the whole call); ``ms_per_step`` is the HSA forward ms per chunk-call; ``roofline`` is the
-sparse kernel's own rate measured with HIP events on the stream it runs on; ``cpu_baseline`` times
-the CPU oracle (the reference algorithm restated in torch, fp32 math) on a bounded sample.
+Also on the same line:
+* ``hkv`` (cfg 3): page-summary HBM GB/s over the 120-frame history, selection time, the pinned
+  host -> device page gather GB/s (8 one-frame pages of K+V per layer, side stream) against a plain
+  pinned copy of the same size class, the re-rope, the HSA forward over the 14-frame pool, and the
+  per-layer time with the next layer's gather overlapped with this layer's attention;
+* ``train`` (cfg 5): HSA forward + backward at the cfg 2 shape with top-k 16;
+* ``wan14b`` (cfg 4): 40 layers x 4 denoising steps of QKV projection + HSA + out projection.
 """
 from __future__ import annotations
 
@@ -38,42 +44,62 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-calls", type=int, default=12)
+    ap.add_argument("--only", default="cfg2,cfg3,cfg4,cfg5",
+                    help="comma list of the extra configs to run (cfg2, the headline, always runs)")
+    ap.add_argument("--hkv-layers", type=int, default=4)
     return ap.parse_args()
 
 
-def event_time_ms(fn, iters: int) -> float:
-    """Average duration of ``fn`` (launches on torch's current stream) over ``iters`` runs."""
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def stream_time_ms(fn, iters: int, stream=None) -> float:
+    """Average duration of ``fn`` over ``iters`` runs, timed with events on ``stream`` (default:
+    the current stream, where ``fn`` launches)."""
+    stream = stream or torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record()
+    start.record(stream)
     for _ in range(iters):
         fn()
-    end.record()
+    end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / iters
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path shards by "
-                                   "head across GPUs by design, but no multi-GPU run is part of it)"}))
-        sys.exit(2)
+def median_ms(fn, iters: int) -> float:
+    times = []
+    for _ in range(iters):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        times.append(s.elapsed_time(e))
+    return statistics.median(times)
 
-    from worldattention_amd import _lib, workloads
-    from worldattention_amd.hsa import attention as WA
-    from worldattention_amd.hsa.block_sparse import bsa_forward
 
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    cfg = workloads.cfg2(device=dev, seed=args.seed)
-    q, k, v = cfg["q"], cfg["k"], cfg["v"]
-    d = q.shape[-1]
+def gate_and_proj(d: int, dev):
     gate = torch.nn.Linear(d, d).to(dev)
     with torch.no_grad():
         gate.weight.zero_()
         gate.bias.zero_()
-    proj = torch.zeros(13, 1560, dtype=torch.bfloat16, device=dev)
+    return gate, torch.zeros(13, 1560, dtype=torch.bfloat16, device=dev)
+
+
+# ---------------------------------------------------------------------------------------------
+# cfg 2 — the headline
+# ---------------------------------------------------------------------------------------------
+def bench_cfg2(args, dev):
+    from worldattention_amd import workloads
+    from worldattention_amd.hsa import attention as WA
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+
+    cfg = workloads.cfg2(device=dev, seed=args.seed)
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    d = q.shape[-1]
+    gate, proj = gate_and_proj(d, dev)
     kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate,
               block_size=cfg["block_size"], tau_min=0.35, tau_max=1.0, proj_segment_len=cfg["proj_segment_len"],
               routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
@@ -89,7 +115,6 @@ def main():
     sparse_heads = [h for h, m in enumerate(cfg["head_modes"]) if m != "linear"]
     useful_flop, tile_flop = workloads.sparse_flops(route.num, route.index, q.shape[1], k.shape[1],
                                                     cfg["block_size"], d, heads=sparse_heads)
-
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -99,10 +124,8 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    # dominant kernel: the sparse forward alone, same arguments as inside the step
     plan = WA.HeadPlan(q.shape[2], cfg["head_modes"], dev)
     out = torch.empty_like(q)
-
     nkv = -(-k.shape[1] // cfg["block_size"])
     visits = [min(cfg["topk"][h], nkv) for h in plan.sparse_only]
 
@@ -113,17 +136,339 @@ def main():
 
     for _ in range(3):
         sparse_only()
-    sparse_ms = event_time_ms(sparse_only, max(args.steps, 20))
+    sparse_ms = stream_time_ms(sparse_only, max(args.steps, 20))
     achieved = useful_flop / (sparse_ms * 1e-3) / 1e12
+    log(f"cfg2: {ms_per_step:.4f} ms/call, sparse kernel {sparse_ms:.4f} ms = {achieved:.1f} TFLOP/s")
+    return cfg, proj, dict(ms_per_step=ms_per_step, useful_flop=useful_flop, tile_flop=tile_flop,
+                           sparse_ms=sparse_ms, achieved=achieved)
 
+
+# ---------------------------------------------------------------------------------------------
+# cfg 3 — HKV retrieval, gather, re-rope and attention over the page pool
+# ---------------------------------------------------------------------------------------------
+def bench_cfg3(args, dev):
+    from worldattention_amd import hkv as W
+    from worldattention_amd import workloads
+    from worldattention_amd.hkv import _ops
+    from worldattention_amd.hkv.cache import _copy
+    from worldattention_amd.hsa import attention as WA
+
+    layers = args.hkv_layers
+    cfg = workloads.cfg3(dev, seed=args.seed, layers=layers)
+    ft, hf, nres, nret = cfg["frame_tokens"], cfg["host_frames"], cfg["resident_frames"], cfg["retrieved"]
+    hist = cfg["history_frames"]
+    heads, d = cfg["q"].shape[2], cfg["q"].shape[3]
+    nt = W.temporal_complex_dims(d)
+    main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    log(f"cfg3: workload ready ({layers} layers, {hist} frames, pinned host pool "
+        f"{sum(t.numel() * 2 for t in cfg['host_k'] + cfg['host_v']) / 2**30:.2f} GiB)")
+
+    # page summaries over the whole history (layer-0 keys, one page per frame)
+    keys0 = cfg["keys0"]
+    frames = torch.arange(hist)
+    factors = _ops.factor_table(cfg["freqs"][:, :nt], torch.zeros_like(frames), frames, keys0.device)
+    flat = keys0.view(1, keys0.shape[1], heads * d)
+
+    def summary_kernel():
+        return _ops.segment_means(flat, heads=heads, head_dim=d, seg_tokens=ft, factors=factors, row_tokens=ft)
+
+    summary_kernel()
+    sum_ms = stream_time_ms(summary_kernel, 20)
+    sum_bytes = keys0.numel() * keys0.element_size()
+    spans = [(f * ft, (f + 1) * ft) for f in range(hist)]
+    page_index = W.page_key_index(keys0, spans, frame_seq_length=ft, start_frame=0, temporal_freqs=cfg["freqs"])
+    api_ms = stream_time_ms(lambda: W.page_key_index(keys0, spans, frame_seq_length=ft, start_frame=0,
+                                                     temporal_freqs=cfg["freqs"]), 10)
+
+    # selection: query index + scores + top-8 among the host-tier pages
+    mask = torch.zeros(hist, dtype=torch.uint8, device=dev)
+    mask[hf:] = 1
+
+    def select():
+        qv = W.query_index(cfg["q_content"])
+        return W.select_pages(page_index, qv, nret, mask=mask)
+
+    sel, _ = select()
+    sel_ms = stream_time_ms(select, 50)
+    chosen = sorted(int(i) for i in sel.tolist())
+    recall = len(set(chosen) & set(cfg["truth"])) / nret
+
+    # gather plan: page i of the selection -> pool slot i, re-roped to frame (hist - nres - nret) + i
+    base = hist - nres - nret
+    pool_tokens = (nret + nres) * ft
+    rerope_f = _ops.factor_table(cfg["freqs"][:, :nt], torch.tensor([base + i for i in range(nret)]),
+                                 torch.tensor(chosen), dev)
+    rows = torch.arange(nret, dtype=torch.int32, device=dev).repeat_interleave(ft)
+
+    def layer_copies(layer):
+        cps = []
+        for name, host, pool in (("k", cfg["host_k"][layer], cfg["pool_k"][layer]),
+                                 ("v", cfg["host_v"][layer], cfg["pool_v"][layer])):
+            for i, f in enumerate(chosen):
+                cps.append(_copy(host[:, f * ft:(f + 1) * ft], pool[:, i * ft:(i + 1) * ft]))
+        return cps
+
+    plans = [layer_copies(layer) for layer in range(layers)]
+    gather_bytes = 2 * nret * ft * heads * d * 2
+
+    def gather(layer):
+        _ops.copy_pages(plans[layer], to_device=True, stream=side)
+
+    def rerope(layer):
+        with torch.cuda.stream(side):
+            _ops.rotate_temporal(cfg["pool_k"][layer], rerope_f, rows=rows, t0=0, t1=nret * ft)
+
+    side.wait_stream(main)
+    for layer in range(layers):
+        gather(layer)
+        rerope(layer)
+    torch.cuda.synchronize()
+    gather_ms = stream_time_ms(lambda: [gather(layer) for layer in range(layers)], 5, stream=side) / layers
+    rerope_ms = stream_time_ms(lambda: [rerope(layer) for layer in range(layers)], 10, stream=side) / layers
+    rerope_bytes = 2 * nret * ft * heads * (2 * nt) * 2
+
+    # plain pinned -> device copy of one layer's whole host K pool: the host-link reference rate
+    big = cfg["host_k"][0]
+    dst = torch.empty(big.shape, dtype=big.dtype, device=dev)
+    peak_copy = [_copy(big, dst)]
+    h2d_ms = stream_time_ms(lambda: _ops.copy_pages(peak_copy, to_device=True, stream=side), 3, stream=side)
+    h2d_gbs = big.numel() * 2 / (h2d_ms * 1e-3) / 1e9
+    del dst
+
+    # the reference's pattern: per-page synchronous copies from pageable host memory (cache.py:229-242)
+    pageable_k = cfg["host_k"][0][:, : (max(chosen) + 1) * ft].clone()
+    pageable_v = cfg["host_v"][0][:, : (max(chosen) + 1) * ft].clone()
+
+    def reference_style():
+        ks = [pageable_k[:, f * ft:(f + 1) * ft].to(dev) for f in chosen]
+        vs = [pageable_v[:, f * ft:(f + 1) * ft].to(dev) for f in chosen]
+        return torch.cat(ks, dim=1), torch.cat(vs, dim=1)
+
+    reference_style()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        reference_style()
+    torch.cuda.synchronize()
+    ref_ms = (time.perf_counter() - t0) * 1e3 / 3
+    del pageable_k, pageable_v
+
+    # HSA forward over the pool (8 retrieved + 6 resident frames = 21,840 tokens)
+    gate, proj = gate_and_proj(d, dev)
+    kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate, block_size=128,
+              tau_min=0.35, tau_max=1.0, proj_segment_len=ft, routing="topk", topk=cfg["topk"],
+              head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
+
+    def attend(layer):
+        with torch.no_grad():
+            return WA.hsa_forward(cfg["q"], cfg["pool_k"][layer], cfg["pool_v"][layer], **kw)
+
+    attend(0)
+    attn_ms = stream_time_ms(lambda: [attend(layer) for layer in range(layers)], 5) / layers
+
+    def serial():
+        for layer in range(layers):
+            side.wait_stream(main)
+            gather(layer)
+            rerope(layer)
+            main.wait_stream(side)
+            attend(layer)
+
+    def pipelined():
+        side.wait_stream(main)
+        events = []
+        for layer in range(layers):
+            gather(layer)
+            rerope(layer)
+            ev = torch.cuda.Event()
+            ev.record(side)
+            events.append(ev)
+        for layer in range(layers):
+            main.wait_event(events[layer])
+            attend(layer)
+
+    serial()
+    serial_ms = stream_time_ms(serial, 3) / layers
+    pipelined()
+    pipe_ms = stream_time_ms(pipelined, 3) / layers
+    res = {
+        "workload": f"cfg3: {hist}-frame history x {ft} tokens, H={heads} D={d} bf16, one-frame pages; frames "
+                    f"0..{hf - 1} in pinned host memory, {nres} resident; top-{nret} of the {hf} host pages "
+                    f"(resident pages masked), gathered into pool slots 0..{nret - 1} and re-roped to frames "
+                    f"{base}..{base + nret - 1}; HSA over {pool_tokens} pool tokens; {layers} layers",
+        "summary_gbs": round(sum_bytes / (sum_ms * 1e-3) / 1e9, 1),
+        "summary_kernel_ms": round(sum_ms, 4),
+        "summary_hbm_frac": round(sum_bytes / (sum_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "summary_api_ms": round(api_ms, 4),
+        "select_ms": round(sel_ms, 4),
+        "recall_vs_planted": recall,
+        "gather_bytes_per_layer": gather_bytes,
+        "gather_ms_per_layer": round(gather_ms, 4),
+        "gather_gbs": round(gather_bytes / (gather_ms * 1e-3) / 1e9, 2),
+        "pinned_h2d_copy_gbs": round(h2d_gbs, 2),
+        "gather_frac_of_pinned_copy": round(gather_bytes / (gather_ms * 1e-3) / 1e9 / h2d_gbs, 3),
+        "reference_style_pageable_gbs": round(gather_bytes / (ref_ms * 1e-3) / 1e9, 2),
+        "rerope_ms_per_layer": round(rerope_ms, 4),
+        "rerope_gbs": round(rerope_bytes / (rerope_ms * 1e-3) / 1e9, 1),
+        "hsa_fwd_ms_per_layer": round(attn_ms, 4),
+        "serial_ms_per_layer": round(serial_ms, 4),
+        "overlapped_ms_per_layer": round(pipe_ms, 4),
+    }
+    log(f"cfg3: summary {res['summary_gbs']} GB/s, gather {res['gather_gbs']} GB/s "
+        f"(pinned copy {res['pinned_h2d_copy_gbs']}), overlapped {pipe_ms:.3f} ms/layer vs serial {serial_ms:.3f}")
+    del cfg
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# cfg 5 — training step (forward + backward)
+# ---------------------------------------------------------------------------------------------
+def bench_cfg5(args, dev):
+    from worldattention_amd import hsa as W
+    from worldattention_amd import workloads
+    from worldattention_amd.hsa import attention as WA
+
+    cfg = workloads.cfg5(device=dev, seed=args.seed)
+    d = cfg["q"].shape[-1]
+    gate = torch.nn.Linear(d, d).to(dev)
+    with torch.no_grad():
+        gate.weight.normal_(0, 0.02)
+        gate.bias.zero_()
+    proj = torch.zeros(13, 1560, dtype=torch.bfloat16, device=dev)
+    q, k, v = (cfg[n].detach().requires_grad_() for n in ("q", "k", "v"))
+    kw = dict(k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate, block_size=128, routing="topk", topk=cfg["topk"],
+              head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
+
+    def fwd_bwd():
+        q.grad = k.grad = v.grad = None
+        gate.weight.grad = gate.bias.grad = None
+        W.hsa_attention(q, k, v, **kw).backward(cfg["do"])
+
+    def fwd():
+        return W.hsa_attention(q, k, v, **kw)
+
+    for _ in range(3):
+        fwd_bwd()
+    step_ms = median_ms(fwd_bwd, 20)
+    fwd_ms = median_ms(fwd, 20)
+    save = {}
+    with torch.no_grad():
+        g2, p2 = gate_and_proj(d, dev)
+        WA.hsa_forward(cfg["q"], cfg["k"], cfg["v"], save=save, k_coarse=None, v_coarse=None, k_proj_mat=p2,
+                       v_proj_mat=p2, gate_lin=g2, block_size=128, tau_min=0.35, tau_max=1.0, proj_segment_len=1560,
+                       routing="topk", topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode="elu1")
+    sparse = [h for h, m in enumerate(cfg["head_modes"]) if m != "linear"]
+    useful, _ = workloads.sparse_flops(save["route"].num, save["route"].index, q.shape[1], k.shape[1], 128, d,
+                                       heads=sparse)
+    res = {"workload": "cfg5: cfg2 shapes, top-16 on 8 sparse heads + 4 elu1 heads, bf16, dO ~ N(0,1); "
+                       "routing recomputed without grad; trained gate",
+           "fwd_bwd_ms": round(step_ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4),
+           "sparse_useful_gflop_fwd": round(useful / 1e9, 3),
+           "effective_sparse_tflops_fwd_bwd": round(3.5 * useful / (step_ms * 1e-3) / 1e12, 2)}
+    log(f"cfg5: fwd+bwd {step_ms:.3f} ms (fwd {fwd_ms:.3f})")
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# cfg 4 — Wan-14B attention stack
+# ---------------------------------------------------------------------------------------------
+def bench_cfg4(args, dev):
+    from worldattention_amd import workloads
+    from worldattention_amd.hsa import attention as WA
+
+    cfg = workloads.cfg4(dev, seed=args.seed)
+    heads, d, hist, chunk = cfg["heads"], cfg["d"], cfg["history"], cfg["chunk"]
+    layers = len(cfg["w_qkv"])
+    gate, proj = gate_and_proj(d, dev)
+    kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate, block_size=128,
+              tau_min=0.35, tau_max=1.0, proj_segment_len=1560, routing="topk", topk=cfg["topk"],
+              head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
+    hsa_events = []
+
+    def run(steps=4, time_hsa=False):
+        x = cfg["x"]
+        for _ in range(steps):
+            h = x
+            for layer in range(layers):
+                qkv = (h @ cfg["w_qkv"][layer]).view(1, chunk, 3, heads, d)
+                cfg["k_cache"][layer][:, hist:] = qkv[:, :, 1]
+                cfg["v_cache"][layer][:, hist:] = qkv[:, :, 2]
+                if time_hsa:
+                    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    s.record()
+                with torch.no_grad():
+                    o = WA.hsa_forward(qkv[:, :, 0], cfg["k_cache"][layer], cfg["v_cache"][layer], **kw)
+                if time_hsa:
+                    e.record()
+                    hsa_events.append((s, e))
+                h = h + o.reshape(1, chunk, heads * d) @ cfg["w_out"][layer]
+        return h
+
+    with torch.no_grad():
+        run(steps=1)
+        total_ms = median_ms(lambda: run(), 3)
+        hsa_events.clear()
+        run(time_hsa=True)
+        torch.cuda.synchronize()
+    hsa_ms = sum(s.elapsed_time(e) for s, e in hsa_events)
+    dim = heads * d
+    proj_flop = 4 * layers * (2 * chunk * dim * 3 * dim + 2 * chunk * dim * dim)
+    res = {"workload": f"cfg4: Wan-14B stack, {layers} layers x 4 steps, H={heads} D={d}, chunk {chunk} vs "
+                       f"{hist + chunk} KV tokens, 30 sparse (top-16) / 10 elu1 heads, bf16, seeded random weights "
+                       "(QKV/out projections via torch matmul; no RoPE in this stack)",
+           "ms_per_chunk_4_steps": round(total_ms, 3), "hsa_ms_4_steps": round(hsa_ms, 3),
+           "hsa_ms_per_layer_call": round(hsa_ms / (4 * layers), 4),
+           "projection_tflops": round(proj_flop / ((total_ms - hsa_ms) * 1e-3) / 1e12, 1)}
+    log(f"cfg4: {total_ms:.1f} ms for 4 steps x {layers} layers (HSA {hsa_ms:.1f} ms)")
+    del cfg
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+def cpu_baseline(args, cfg, proj, useful_flop):
+    from oracle import hsa as O
+    d = cfg["q"].shape[-1]
+    cpu = {k2: (t.cpu() if torch.is_tensor(t) else t) for k2, t in cfg.items()}
+    projc = proj.cpu()
+    zw, zb = torch.zeros(d, d), torch.zeros(d)
+    times = []
+    for i in range(args.cpu_sample_calls + 1):
+        t1 = time.perf_counter()
+        O.hsa_attention(cpu["q"], cpu["k"], cpu["v"], k_proj_mat=projc, v_proj_mat=projc, gate_weight=zw,
+                        gate_bias=zb, block_size=cfg["block_size"], routing="topk", topk=cfg["topk"],
+                        head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
+        if i:
+            times.append(time.perf_counter() - t1)
+    cpu_s = statistics.median(times)
+    log(f"cpu baseline: {cpu_s * 1e3:.1f} ms/call")
+    return {"value": round(useful_flop / cpu_s / 1e12, 4), "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{args.cpu_sample_calls} full cfg2 HSA forward calls of the CPU oracle (fp32 math), "
+                      f"median {cpu_s * 1e3:.1f} ms/call after 1 warm-up",
+            "ms_per_call": round(cpu_s * 1e3, 2)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path shards by "
+                                   "head across GPUs by design, but no multi-GPU run is part of it)"}))
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    extras = {s.strip() for s in args.only.split(",") if s.strip()}
+
+    cfg, proj, c2 = bench_cfg2(args, dev)
+    achieved = c2["achieved"]
     result = {
         "metric": METRIC,
-        "value": round(useful_flop / (ms_per_step * 1e-3) / 1e12, 3),
+        "value": round(c2["useful_flop"] / (c2["ms_per_step"] * 1e-3) / 1e12, 3),
         "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(c2["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -132,36 +477,25 @@ def main():
         "config": {"workload": "cfg2: Wan-1.3B chunk HSA forward, B=1 H=12 D=128 Lq=4680 Lkv=32760 block=128, "
                                "8 sparse heads top-k from {8,16,32} + 4 elu1 linear heads",
                    "topk": cfg["topk"], "head_modes": cfg["head_modes"], "seed": args.seed},
-        "hsa_fwd_ms_per_chunk": round(ms_per_step, 4),
-        "sparse_kernel_ms": round(sparse_ms, 4),
-        "sparse_useful_gflop": round(useful_flop / 1e9, 3),
-        "sparse_tile_gflop": round(tile_flop / 1e9, 3),
+        "hsa_fwd_ms_per_chunk": round(c2["ms_per_step"], 4),
+        "sparse_kernel_ms": round(c2["sparse_ms"], 4),
+        "sparse_useful_gflop": round(c2["useful_flop"] / 1e9, 3),
+        "sparse_tile_gflop": round(c2["tile_flop"] / 1e9, 3),
         "pct_mfma_peak_sparse": round(100 * achieved / MFMA_BF16_PEAK_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "kernel": "bsa_unit_kernel<128,128> + bsa_combine_kernel<128,128>", "achieved": round(achieved, 3),
-                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+        "roofline": {"bound": "mfma", "kernel": "bsa_unit_kernel<128,128> + bsa_combine_kernel<128,128>",
+                     "achieved": round(achieved, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
     }
-
     if not args.no_cpu_baseline:
-        from oracle import hsa as O
-        cpu = {k2: (t.cpu() if torch.is_tensor(t) else t) for k2, t in cfg.items()}
-        projc = proj.cpu()
-        zw, zb = torch.zeros(d, d), torch.zeros(d)
-        times = []
-        for i in range(args.cpu_sample_calls + 1):
-            t1 = time.perf_counter()
-            O.hsa_attention(cpu["q"], cpu["k"], cpu["v"], k_proj_mat=projc, v_proj_mat=projc, gate_weight=zw,
-                            gate_bias=zb, block_size=cfg["block_size"], routing="topk", topk=cfg["topk"],
-                            head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
-            if i:
-                times.append(time.perf_counter() - t1)
-        cpu_s = statistics.median(times)
-        result["cpu_baseline"] = {
-            "value": round(useful_flop / cpu_s / 1e12, 4), "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{args.cpu_sample_calls} full cfg2 HSA forward calls of the CPU oracle (fp32 math), "
-                      f"median {cpu_s * 1e3:.1f} ms/call after 1 warm-up",
-            "ms_per_call": round(cpu_s * 1e3, 2)}
+        result["cpu_baseline"] = cpu_baseline(args, cfg, proj, c2["useful_flop"])
+    del cfg
+    torch.cuda.empty_cache()
+    if "cfg3" in extras:
+        result["hkv"] = bench_cfg3(args, dev)
+    if "cfg5" in extras:
+        result["train"] = bench_cfg5(args, dev)
+    if "cfg4" in extras:
+        result["wan14b"] = bench_cfg4(args, dev)
     print(json.dumps(result), flush=True)
 
 

@@ -8,6 +8,13 @@
   offset per frame and head; Wan 3-D RoPE (temporal 22 / height 21 / width 21 complex pairs) is
   applied to Q and K at their frame positions. 8 sparse heads with budgets drawn from {8,16,32}
   and 4 linear heads, both chosen by the seed.
+* ``cfg3`` — HKV long-horizon retrieval at the Wan-1.3B shape: a 120-frame history (187,200
+  tokens, H=12, D=128, bf16) per layer, one-frame pages. Frames 0..113 of every layer sit in a
+  pinned host pool, frames 114..119 stay resident in the device pool; the query chunk (frames
+  120..122) mixes the key clusters of 8 seeded host frames, so retrieval has a ground truth.
+* ``cfg4`` — Wan-14B attention stack: H=40, D=128, model dim 5120, 40 layers with seeded
+  ``Linear(5120, 3*5120)`` QKV / ``Linear(5120, 5120)`` out weights, a 28,080-token synthetic KV
+  history per layer plus the chunk's own 4,680 tokens, 30 sparse (top-16) / 10 linear heads.
 * ``cfg5`` — cfg2 shapes with top-k 16 on every sparse head, plus dO ~ N(0,1), for fwd+bwd.
 
 The 3-D RoPE follows ``wan/modules/model.py:29-36`` and ``wan/modules/causal_model.py:34-62``.
@@ -126,3 +133,76 @@ def sparse_flops(num: torch.Tensor, index: torch.Tensor, q_len: int, kv_len: int
                 useful += int(q_real[i]) * int(kv_real[ids].sum())
                 tiles += n
     return 4.0 * d * useful, 4.0 * d * block_size * block_size * tiles
+
+
+def cfg3(device, seed: int = 0, layers: int = 4, history_frames: int = 120, resident_frames: int = 6,
+         retrieved: int = 8, q_frames: int = 3, heads: int = 12, d: int = 128) -> dict:
+    """HKV retrieval workload (see the module docstring). Returns device / pinned-host tensors:
+
+    host_k / host_v: per layer ``[1, host_frames * 1560, H, D]`` pinned bf16 (roped keys);
+    pool_k / pool_v: per layer device ``[1, (retrieved + resident) * 1560, H, D]`` with the resident
+        frames already in the last ``resident_frames`` slots;
+    keys0: device ``[1, history_frames * 1560, H, D]`` layer-0 keys (the page-summary input);
+    q: device roped queries ``[1, q_frames * 1560, H, D]``; q_content: pre-rope ``[1, Lq, H*D]``;
+    freqs: the complex128 RoPE table (device); truth: the host frames the query was built from.
+    """
+    g = torch.Generator(device=device).manual_seed(seed)
+    host_frames = history_frames - resident_frames
+    ft = FRAME_TOKENS
+    freqs = rope_freqs(1024, d).to(device)
+    offsets = torch.randn(history_frames, heads, d, generator=g, device=device) * 0.5
+    truth = sorted(torch.randperm(host_frames, generator=g, device=device)[:retrieved].tolist())
+    host_k, host_v, pool_k, pool_v = [], [], [], []
+    keys0 = None
+    slots = (retrieved + resident_frames) * ft
+    for layer in range(layers):
+        k = torch.randn(1, history_frames * ft, heads, d, generator=g, device=device)
+        k += offsets.repeat_interleave(ft, dim=0).unsqueeze(0)
+        k = apply_rope_3d(k, freqs, history_frames, FRAME_H, FRAME_W, 0).to(torch.bfloat16)
+        v = torch.randn(1, history_frames * ft, heads, d, generator=g, device=device).to(torch.bfloat16)
+        if layer == 0:
+            keys0 = k
+        hk = torch.empty((1, host_frames * ft, heads, d), dtype=torch.bfloat16, pin_memory=True)
+        hv = torch.empty_like(hk, pin_memory=True)
+        hk.copy_(k[:, : host_frames * ft])
+        hv.copy_(v[:, : host_frames * ft])
+        pk = torch.zeros((1, slots, heads, d), dtype=torch.bfloat16, device=device)
+        pv = torch.zeros_like(pk)
+        pk[:, retrieved * ft:] = k[:, host_frames * ft:]
+        pv[:, retrieved * ft:] = v[:, host_frames * ft:]
+        host_k.append(hk)
+        host_v.append(hv)
+        pool_k.append(pk)
+        pool_v.append(pv)
+        del k, v
+    lq = q_frames * ft
+    mix = offsets[truth].mean(dim=0) * 4.0
+    qc = torch.randn(1, lq, heads, d, generator=g, device=device) + mix.unsqueeze(0).unsqueeze(0)
+    q = apply_rope_3d(qc, freqs, q_frames, FRAME_H, FRAME_W, history_frames).to(torch.bfloat16)
+    gm = torch.Generator().manual_seed(seed + 1)
+    modes = head_split(gm, heads, 4)
+    return dict(host_k=host_k, host_v=host_v, pool_k=pool_k, pool_v=pool_v, keys0=keys0, q=q,
+                q_content=qc.reshape(1, lq, heads * d).to(torch.bfloat16), freqs=freqs, truth=truth,
+                history_frames=history_frames, host_frames=host_frames, resident_frames=resident_frames,
+                retrieved=retrieved, frame_tokens=ft, block_size=128, head_modes=modes,
+                topk=[16 if m == "sparse" else 0 for m in modes], linear_mode="elu1")
+
+
+def cfg4(device, seed: int = 0, layers: int = 40, heads: int = 40, d: int = 128, history: int = 28080,
+         chunk: int = 3 * FRAME_TOKENS) -> dict:
+    """Wan-14B stack workload (see the module docstring): weights and caches on ``device``."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    dim = heads * d
+    scale = 1.0 / math.sqrt(dim)
+    w_qkv = [(torch.randn(dim, 3 * dim, generator=g, device=device) * scale).to(torch.bfloat16) for _ in range(layers)]
+    w_out = [(torch.randn(dim, dim, generator=g, device=device) * scale).to(torch.bfloat16) for _ in range(layers)]
+    k_cache = [torch.randn(1, history + chunk, heads, d, generator=g, device=device).to(torch.bfloat16)
+               for _ in range(layers)]
+    v_cache = [torch.randn(1, history + chunk, heads, d, generator=g, device=device).to(torch.bfloat16)
+               for _ in range(layers)]
+    x = torch.randn(1, chunk, dim, generator=g, device=device).to(torch.bfloat16)
+    modes = ["sparse"] * 30 + ["linear"] * 10 if heads == 40 else head_split(torch.Generator().manual_seed(seed), heads,
+                                                                                heads // 4)
+    return dict(w_qkv=w_qkv, w_out=w_out, k_cache=k_cache, v_cache=v_cache, x=x, history=history, chunk=chunk,
+                heads=heads, d=d, block_size=128, head_modes=modes,
+                topk=[16 if m == "sparse" else 0 for m in modes], linear_mode="elu1")
