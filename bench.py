@@ -47,7 +47,21 @@ def parse():
     ap.add_argument("--only", default="cfg2,cfg3,cfg4,cfg5",
                     help="comma list of the extra configs to run (cfg2, the headline, always runs)")
     ap.add_argument("--hkv-layers", type=int, default=4)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (the reference kernel that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters of the traffic measurement)")
     return ap.parse_args()
+
+
+def copy_calibration(dev) -> None:
+    n = 1 << 29                               # 1 GiB of bf16
+    src = torch.randn(n, device=dev).to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 2, "copy_calibration_bytes_written": n * 2,
+                      "launches": 5}), flush=True)
 
 
 def log(msg: str) -> None:
@@ -457,6 +471,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
     extras = {s.strip() for s in args.only.split(",") if s.strip()}
 
     cfg, proj, c2 = bench_cfg2(args, dev)

@@ -67,6 +67,20 @@ __device__ __forceinline__ int row_visits(const FwdParams& p, int64_t irow) {
   return max(0, min(n, (int)p.index_width));
 }
 
+// Ascending bitonic sort of one int per lane across the 64-lane wave.
+__device__ __forceinline__ int wave_sort_ascending(int key, int lane) {
+#pragma unroll
+  for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const int other = __shfl_xor(key, j, 64);
+      const bool keep_min = ((lane & j) == 0) == ((lane & k) == 0);
+      key = keep_min ? min(key, other) : max(key, other);
+    }
+  }
+  return key;
+}
+
 __device__ __forceinline__ int block_real(const FwdParams& p, int j, int BS) {
   int real = BS;
   if (p.block_sizes) real = min(real, p.block_sizes[j]);
@@ -369,15 +383,22 @@ bsa_unit_kernel(FwdParams p) {
     qf[c] = q_ok ? t : bf16x8{};
   }
 
-  // This unit's list entries, one per lane (split <= 64), read once: the loop fetches them with
-  // readlane and issues no memory reads besides the tile streams.
-  const int cnt = s_end - s_begin;
-  int my_j = 0, my_real = 0;
-  if (lane < cnt) {
-    my_j = p.index ? min(max(p.index[irow * p.index_width + s_begin + lane], 0), p.Nkv - 1) : s_begin + lane;
-    my_real = block_real(p, my_j, BS);
-  }
-  Cursor cur{__ballot(lane < cnt && my_real > 0), 0, 0, 0, false};
+  // List entries one per lane, read once: the loop fetches them with readlane and issues no memory
+  // reads besides the tile streams. A row of at most 64 visits is loaded whole and sorted by block
+  // id, and this unit takes its slice of the sorted list: the units of a head (which run together
+  // on one XCD) then sweep the key range in step and share the K/V tiles they fetch in L2. The
+  // visit order only changes the summation order. Longer rows keep list order, one slice per unit.
+  const bool whole = n <= 64;
+  const int lo = whole ? 0 : s_begin;
+  const int take = whole ? n : s_end - s_begin;
+  int my_j = 0;
+  if (lane < take)
+    my_j = p.index ? min(max(p.index[irow * p.index_width + lo + lane], 0), p.Nkv - 1) : lo + lane;
+  if (whole) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
+  const int first = whole ? s_begin : 0, last = whole ? s_end : take;
+  const bool mine = lane >= first && lane < last;
+  const int my_real = mine ? block_real(p, my_j, BS) : 0;
+  Cursor cur{__ballot(mine && my_real > 0), 0, 0, 0, false};
   cursor_next<BS>(cur, my_j, my_real);
 
   auto next_tile = [&](bf16_t* kl, bf16_t* vl, const Cursor& c) {
