@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(256) summary_partial_kernel(SumParams p) {
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  constexpr int U = 4;  // tokens in flight per thread
+  constexpr int U = 8;  // tokens in flight per thread
   for (int t = ts; t < te; t += U) {
     float f[U][VEC];
 #pragma unroll
@@ -149,6 +149,8 @@ __global__ void __launch_bounds__(256) summary_partial_kernel(SumParams p) {
   for (int e = 0; e < VEC; ++e) out[e] = acc[e];
 }
 
+// Grid (n_seg, column groups of 256); with `normalize` a single column group covers the row so the
+// norm can be formed in the block.
 __global__ void __launch_bounds__(256) summary_reduce_kernel(SumParams p, float* out, int normalize) {
   __shared__ float red[4];
   const int seg = blockIdx.x;
@@ -156,7 +158,8 @@ __global__ void __launch_bounds__(256) summary_reduce_kernel(SumParams p, float*
   segment_bounds(p, seg, s0, s1);
   const float len = (float)(s1 - s0);
   float sq = 0.f;
-  for (int c = threadIdx.x; c < p.C; c += blockDim.x) {
+  const int c_begin = blockIdx.y * blockDim.x + threadIdx.x, c_step = blockDim.x * gridDim.y;
+  for (int c = c_begin; c < p.C; c += c_step) {
     float tot = 0.f;
     for (int b = 0; b < p.B; ++b) {
       const float* w = p.ws + ((int64_t)seg * p.B + b) * p.splits * (int64_t)p.C + c;
@@ -357,7 +360,8 @@ extern "C" int wa_hkv_page_summary(const wa_hkv_summary_args* a, void* stream) {
   }
   int rc = wa_launch_status("summary_partial_kernel");
   if (rc) return rc;
-  summary_reduce_kernel<<<(unsigned)a->n_seg, 256, 0, s>>>(p, a->out, a->normalize ? 1 : 0);
+  const unsigned red_groups = a->normalize ? 1u : (unsigned)std::min<int64_t>((C + 255) / 256, 65535);
+  summary_reduce_kernel<<<dim3((unsigned)a->n_seg, red_groups), 256, 0, s>>>(p, a->out, a->normalize ? 1 : 0);
   return wa_launch_status("summary_reduce_kernel");
 }
 

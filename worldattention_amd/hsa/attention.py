@@ -20,6 +20,7 @@ North-star extensions (keyword-only, defaults give the reference behaviour):
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Optional, Sequence
 
@@ -287,6 +288,63 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     lin_tmp = torch.empty_like(out) if plan.both else None
 
     # ---- linear branch -------------------------------------------------------------------
+    # With both branches present the linear branch runs on a side stream, concurrently with
+    # routing and the sparse branch on the caller's stream; the two write disjoint heads of `out`
+    # (or `lin_tmp`, joined before the fused sparse epilogue reads it).
+    main = torch.cuda.current_stream(dev)
+    side = _branch_stream(dev) if plan.linear and plan.sparse else None
+    if side is not None:
+        side.wait_stream(main)
+    with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+        _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat,
+                          proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save)
+
+    # ---- sparse branch -------------------------------------------------------------------
+    if plan.sparse:
+        _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+        sp_t = plan.t["sparse"]
+        qp = pool_blhd(q, q_len, nq, block_size, heads=sp_t)
+        kp = pool_blhd(k, kv_len, nkv, block_size, heads=sp_t)
+        if routing == "gini":
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t)
+        else:
+            ks = _per_head_k(topk, heads)
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t)
+        if save is not None:
+            save.update(route=route)
+        # top-k routing fixes every row's visit count on the host: launch exactly those units
+        vis_of = (lambda hl: [min(ks[h], nkv) for h in hl]) if routing == "topk" else (lambda hl: None)
+        if plan.sparse_only:
+            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
+                        heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True,
+                        visits=vis_of(plan.sparse_only))
+        if plan.both:
+            if side is not None:
+                main.wait_stream(side)
+            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
+                        heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
+                        x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), **gate.kwargs())
+    if side is not None:
+        main.wait_stream(side)
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+_BRANCH_STREAMS: dict = {}
+
+
+def _branch_stream(dev: torch.device) -> torch.cuda.Stream:
+    """The per-device side stream of the linear branch (default priority)."""
+    s = _BRANCH_STREAMS.get(dev)
+    if s is None:
+        s = torch.cuda.Stream(device=dev)
+        _BRANCH_STREAMS[dev] = s
+    return s
+
+
+def _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat, proj_segment_len,
+                      block_size, q_len, out, lin_tmp, gate, lin_round, save):
+    """Linear-branch heads of :func:`hsa_forward`: linear-only heads straight into ``out`` with the
+    gate applied, heads that also run the sparse branch into ``lin_tmp``."""
     if plan.linear:
         if linear_mode == "lowrank":
             if k_coarse is None:
@@ -312,31 +370,6 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
                 s_l, z_l = elu1_state(k, v, plan.t["linear_only"])
                 elu1_readout(q, s_l, z_l, plan.t["linear_only"], out, epilogue=_lib.WA_EPI_GATED,
                              lin_round_bf16=lin_round, **gate.kwargs())
-
-    # ---- sparse branch -------------------------------------------------------------------
-    if plan.sparse:
-        _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
-        sp_t = plan.t["sparse"]
-        qp = pool_blhd(q, q_len, nq, block_size, heads=sp_t)
-        kp = pool_blhd(k, kv_len, nkv, block_size, heads=sp_t)
-        if routing == "gini":
-            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t)
-        else:
-            ks = _per_head_k(topk, heads)
-            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t)
-        if save is not None:
-            save.update(route=route)
-        # top-k routing fixes every row's visit count on the host: launch exactly those units
-        vis_of = (lambda hl: [min(ks[h], nkv) for h in hl]) if routing == "topk" else (lambda hl: None)
-        if plan.sparse_only:
-            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
-                        heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True,
-                        visits=vis_of(plan.sparse_only))
-        if plan.both:
-            bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
-                        heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
-                        x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), **gate.kwargs())
-    return out if out.dtype == out_dtype else out.to(out_dtype)
 
 
 def hsa_attention(
