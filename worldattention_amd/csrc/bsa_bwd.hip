@@ -225,17 +225,22 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
       for (int tt = 0; tt < DT; ++tt) dqacc[tt] = wa_mfma32(dsb[c], tile_tr8<D>(kc, c, 32 * tt, lane), dqacc[tt]);
     }
   }
-  // accumulator lane (d = 32t + l32, g) holds rows q = 32w + 8(r/4) + 4g + r%4
+  // accumulator lane (d = 32t + l32, g) holds rows q = 32w + 8(r/4) + 4g + r%4. With accumulation
+  // every previous value of a tile is read before any store, so the reads overlap (a store may
+  // alias a later read, which would otherwise serialize each read-add-write round trip).
+  float* dq_col = p.dq + (int64_t)b * p.dq_sb + (int64_t)h * p.dq_sh + l32;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
+    float prev[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int q = qb * BS + w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-      if (q < p.Lq) {
-        float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)q * p.dq_st + (int64_t)h * p.dq_sh + 32 * tt + l32;
-        const float val = dqacc[tt][r] * p.scale;
-        *dst = p.dq_acc ? *dst + val : val;
-      }
+      prev[r] = p.dq_acc && q < p.Lq ? dq_col[(int64_t)q * p.dq_st + 32 * tt] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int q = qb * BS + w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+      if (q < p.Lq) dq_col[(int64_t)q * p.dq_st + 32 * tt] = prev[r] + dqacc[tt][r] * p.scale;
     }
   }
 }
@@ -352,21 +357,28 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
       }
     }
   }
-  // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4
+  // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4; previous values of a
+  // tile are all read before any store (see the dq epilogue)
+  float* dk_col = p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
+  float* dv_col = p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
+    float pk[16], pv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = j * BS + w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+      const bool in = row < p.Lkv;
+      pk[r] = p.dk_acc && in ? dk_col[(int64_t)row * p.dk_st + 32 * tt] : 0.f;
+      pv[r] = p.dv_acc && in ? dv_col[(int64_t)row * p.dv_st + 32 * tt] : 0.f;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
       const int row = j * BS + kk;
       if (row < p.Lkv) {
         const bool kval = kk < real;
-        float* dk = p.dk + (int64_t)b * p.dk_sb + (int64_t)row * p.dk_st + (int64_t)h * p.dk_sh + 32 * tt + l32;
-        float* dv = p.dv + (int64_t)b * p.dv_sb + (int64_t)row * p.dv_st + (int64_t)h * p.dv_sh + 32 * tt + l32;
-        const float vk = kval ? dkacc[tt][r] * p.scale : 0.f;
-        const float vv = kval ? dvacc[tt][r] : 0.f;
-        *dk = p.dk_acc ? *dk + vk : vk;
-        *dv = p.dv_acc ? *dv + vv : vv;
+        dk_col[(int64_t)row * p.dk_st + 32 * tt] = pk[r] + (kval ? dkacc[tt][r] * p.scale : 0.f);
+        dv_col[(int64_t)row * p.dv_st + 32 * tt] = pv[r] + (kval ? dvacc[tt][r] : 0.f);
       }
     }
   }

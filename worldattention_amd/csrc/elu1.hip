@@ -495,17 +495,22 @@ __global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
       da = wa_mfma32(tile_tr8<D>(s_lo, c, 32 * et, lane), dnb[c], da);
     }
     if (q_ok) {
+      // all reads (q and, when accumulating, the previous dq) before any store
+      float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)qi * p.dq_st + (int64_t)h * p.dq_sh;
+      float qv[4][4], prev[4][4];
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int e0 = 32 * et + 8 * rq + 4 * g;
-        float qv[4];
-        load4_any(p.q, qoff + e0, p.q_dtype, qv);
-        float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)qi * p.dq_st + (int64_t)h * p.dq_sh + e0;
+        load4_any(p.q, qoff + e0, p.q_dtype, qv[rq]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float val = (da[rq * 4 + i] + dden * s_z[e0 + i]) * elu1_grad(qv[i]);
-          dst[i] = p.dq_acc ? dst[i] + val : val;
-        }
+        for (int i = 0; i < 4; ++i) prev[rq][i] = p.dq_acc ? dst[e0 + i] : 0.f;
+      }
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int e0 = 32 * et + 8 * rq + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dst[e0 + i] = prev[rq][i] + (da[rq * 4 + i] + dden * s_z[e0 + i]) * elu1_grad(qv[rq][i]);
       }
     }
   }
@@ -582,17 +587,25 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
       dv = wa_mfma32(pk[c], tile_row8<D>(s_lo, 32 * jt + l32, 2 * c + g), dv);
     }
     const int col = 32 * jt + l32;
+    // all reads (k and, when accumulating, the previous dk / dv) before any store
+    float kx[16], pk[16], pv[16];
+    float* dk_col = p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + col;
+    float* dv_col = p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + col;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
+      const bool in = t < p.Lkv;
+      const int64_t ko = (int64_t)b * p.k_sb + (int64_t)(in ? t : 0) * p.k_st + (int64_t)h * p.k_sh + col;
+      kx[r] = p.kv_dtype == WA_BF16 ? (float)((const bf16_t*)p.k)[ko] : ((const float*)p.k)[ko];
+      pk[r] = p.dk_acc && in ? dk_col[(int64_t)t * p.dk_st] : 0.f;
+      pv[r] = p.dv_acc && in ? dv_col[(int64_t)t * p.dv_st] : 0.f;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
       if (t < p.Lkv) {
-        const int64_t ko = (int64_t)b * p.k_sb + (int64_t)t * p.k_st + (int64_t)h * p.k_sh + col;
-        const float kx = p.kv_dtype == WA_BF16 ? (float)((const bf16_t*)p.k)[ko] : ((const float*)p.k)[ko];
-        float* dkp = p.dk + (int64_t)b * p.dk_sb + (int64_t)t * p.dk_st + (int64_t)h * p.dk_sh + col;
-        float* dvp = p.dv + (int64_t)b * p.dv_sb + (int64_t)t * p.dv_st + (int64_t)h * p.dv_sh + col;
-        const float vk = (dk[r] + s_z[col]) * elu1_grad(kx);
-        *dkp = p.dk_acc ? *dkp + vk : vk;
-        *dvp = p.dv_acc ? *dvp + dv[r] : dv[r];
+        dk_col[(int64_t)t * p.dk_st] = pk[r] + (dk[r] + s_z[col]) * elu1_grad(kx[r]);
+        dv_col[(int64_t)t * p.dv_st] = pv[r] + dv[r];
       }
     }
   }

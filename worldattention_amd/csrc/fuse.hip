@@ -132,27 +132,50 @@ __global__ void __launch_bounds__(256) fuse_bwd_kernel(FuseParams p) {
     const bf16x8 v = *(const bf16x8*)(qrow + c * 16 + g * 8);
     tile_put8<D>(t_q, tl, 2 * c + g, ok ? v : bf16x8{});
   }
-  // dgpre in accumulator layout (lane = token, channels d = 32 tt + 8 (r / 4) + 4 g + r % 4)
+  // dgpre in accumulator layout (lane = token, channels d = 32 tt + 8 (r / 4) + 4 g + r % 4).
+  // Per channel tile all reads (lin, gate, dout, previous dq) are issued before any store, so
+  // they overlap instead of waiting behind stores that might alias them.
   bf16x8 dgb[DC];
+  const int64_t lrow = (int64_t)b * p.l_sb + (int64_t)t * p.l_st + (int64_t)h * p.l_sh;
+  const int64_t grow = (int64_t)b * p.g_sb + (int64_t)t * p.g_st + (int64_t)h * p.g_sh;
+  const int64_t drow = (int64_t)b * p.d_sb + (int64_t)t * p.d_st + (int64_t)h * p.d_sh;
+  const int64_t dlrow = (int64_t)b * p.dl_sb + (int64_t)t * p.dl_st + (int64_t)h * p.dl_sh;
+  float* dq_row = p.dq + (int64_t)b * p.dq_sb + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
+    f32x4 lv[4], gv[4];
+    float dy[4][4], prev[4][4];
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int d0 = 32 * tt + 8 * rq + 4 * g;
+      if (ok) {
+        lv[rq] = *(const f32x4*)(p.lin + lrow + d0);
+        gv[rq] = *(const f32x4*)(p.gate + grow + d0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dy[rq][i] = p.d_dtype == WA_BF16 ? (float)((const bf16_t*)p.dout)[drow + d0 + i]
+                                           : ((const float*)p.dout)[drow + d0 + i];
+          prev[rq][i] = !p.gate_w && p.dq_acc ? dq_row[d0 + i] : 0.f;
+        }
+      }
+    }
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
       const int d0 = 32 * tt + 8 * rq + 4 * g;
       float dg4[4] = {0.f, 0.f, 0.f, 0.f};
       if (ok) {
-        const int64_t di = (int64_t)b * p.d_sb + (int64_t)t * p.d_st + (int64_t)h * p.d_sh + d0;
-        const f32x4 lv = *(const f32x4*)(p.lin + (int64_t)b * p.l_sb + (int64_t)t * p.l_st + (int64_t)h * p.l_sh + d0);
-        const f32x4 gv = *(const f32x4*)(p.gate + (int64_t)b * p.g_sb + (int64_t)t * p.g_st + (int64_t)h * p.g_sh + d0);
         f32x4 dl;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float dy = p.d_dtype == WA_BF16 ? (float)((const bf16_t*)p.dout)[di + i] : ((const float*)p.dout)[di + i];
-          const float l = p.lin_round_bf16 ? wa_bf16_round(lv[i]) : lv[i];
-          dl[i] = dy * gv[i];
-          dg4[i] = dy * l * gv[i] * (1.f - gv[i]);
+          const float l = p.lin_round_bf16 ? wa_bf16_round(lv[rq][i]) : lv[rq][i];
+          dl[i] = dy[rq][i] * gv[rq][i];
+          dg4[i] = dy[rq][i] * l * gv[rq][i] * (1.f - gv[rq][i]);
         }
-        *(f32x4*)(p.dlin + (int64_t)b * p.dl_sb + (int64_t)t * p.dl_st + (int64_t)h * p.dl_sh + d0) = dl;
+        *(f32x4*)(p.dlin + dlrow + d0) = dl;
+        if (!p.gate_w) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dq_row[d0 + i] = prev[rq][i] + dg4[i];
+        }
       }
       bf16x4 d4;
 #pragma unroll
@@ -161,11 +184,6 @@ __global__ void __launch_bounds__(256) fuse_bwd_kernel(FuseParams p) {
         d4[i] = (bf16_t)dg4[i];
       }
       *(bf16x4*)(t_dg + tl * D + (((d0 >> 3) ^ dual_swizzle<D>(tl)) * 8) + (d0 & 7)) = d4;
-      if (!p.gate_w && ok) {
-        float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh + d0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = p.dq_acc ? dst[i] + dg4[i] : dg4[i];
-      }
     }
   }
   __syncthreads();
@@ -177,12 +195,18 @@ __global__ void __launch_bounds__(256) fuse_bwd_kernel(FuseParams p) {
 #pragma unroll
     for (int c = 0; c < DC; ++c) da = wa_mfma32(tile_tr8<D>(w_t, c, 32 * et, lane), dgb[c], da);
     if (ok) {
+      // previous values read before any store
+      float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh;
+      float prev[4][4];
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const int e0 = 32 * et + 8 * rq + 4 * g;
-        float* dst = p.dq + (int64_t)b * p.dq_sb + (int64_t)t * p.dq_st + (int64_t)h * p.dq_sh + e0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = p.dq_acc ? dst[i] + da[rq * 4 + i] : da[rq * 4 + i];
+        for (int i = 0; i < 4; ++i) prev[rq][i] = p.dq_acc ? dst[32 * et + 8 * rq + 4 * g + i] : 0.f;
+      }
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[32 * et + 8 * rq + 4 * g + i] = prev[rq][i] + da[rq * 4 + i];
       }
     }
   }
