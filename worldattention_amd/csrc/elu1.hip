@@ -191,6 +191,118 @@ __global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
   }
 }
 
+// bf16 K / V: raw [64 token][D] tiles stream global -> LDS by direct-to-LDS loads into a 4-stage
+// ring, so three tiles are in flight while one is processed (the register-staged kernel above
+// keeps one). Per tile: wait for it, issue the tile three ahead into the stage freed by the
+// previous one, apply phi in place (each thread owns a fixed 8-channel column, so it also sums z),
+// then the same MFMAs. Rows past the chunk re-read an in-bounds row and get phi = 0, so they add
+// nothing to S or z.
+template <int D>
+__global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
+  constexpr int TC = 64, STAGES = 4;
+  constexpr int CPR = D / 8;              // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;           // rows per wave DMA instruction
+  constexpr int NI = TC / (RPI * 4);      // DMA instructions per wave per tensor per tile
+  constexpr int UPT = TC * CPR / 256;     // chunks per thread in the phi pass
+  constexpr int NT = D / 32, TPW = NT * NT / 4;
+  __shared__ __attribute__((aligned(1024))) bf16_t kb[STAGES][TC * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t vb[STAGES][TC * D];
+
+  const int chunk = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tbeg = chunk * p.chunk_len;
+  const int tend = min(p.L, tbeg + p.chunk_len);
+  const int ntiles = tend > tbeg ? (tend - tbeg + TC - 1) / TC : 0;
+  const bf16_t* kbase = (const bf16_t*)p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
+  const bf16_t* vbase = (const bf16_t*)p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+
+  auto issue = [&](int it) {
+    const int t0 = tbeg + it * TC, st = it % STAGES;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int r0 = (i * 4 + w) * RPI;
+      const int row = r0 + lane / CPR;
+      const int src = t0 + row < tend ? t0 + row : t0;
+      const int cc = (lane % CPR) ^ tr_swizzle(row);
+      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)src * p.k_st + cc * 8),
+                                       WA_LDS_PTR(&kb[st][r0 * D]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)src * p.v_st + cc * 8),
+                                       WA_LDS_PTR(&vb[st][r0 * D]), 16, 0, 0);
+    }
+  };
+
+  f32x16 acc[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) acc[i] = f32x16{};
+  float zacc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zacc[e] = 0.f;
+  const int c8 = tid % CPR;  // this thread's channel chunk in the phi pass
+
+  for (int it = 0; it < min(ntiles, STAGES - 1); ++it) issue(it);
+  for (int it = 0; it < ntiles; ++it) {
+    const int ahead = min(STAGES - 2, ntiles - 1 - it);  // tiles after `it` already issued
+    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * NI) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);  // into the stage of tile it - 1
+    const int st = it % STAGES, t0 = tbeg + it * TC;
+    bf16_t* kt = kb[st];
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int r = tid / CPR + u * (256 / CPR);
+      const bool ok = t0 + r < tend;
+      bf16x8* cp = (bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8));
+      bf16x8 x = *cp;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float ph = ok ? wa_bf16_round(elu1f((float)x[e])) : 0.f;
+        zacc[e] += ph;
+        x[e] = (bf16_t)ph;
+      }
+      *cp = x;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < TC / 16; ++c) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i) {
+        const int dt = D == 128 ? w : (w >> 1);
+        const int et = D == 128 ? i : (w & 1);
+        const bf16x8 a = tr_frag<D>(vb[st], c, 32 * dt, lane);
+        const bf16x8 bb = tr_frag<D>(kb[st], c, 32 * et, lane);
+        acc[i] = wa_mfma32(a, bb, acc[i]);
+      }
+    }
+  }
+
+  float* part = p.part + (((int64_t)chunk * p.B + b) * p.n_heads + hs) * (int64_t)(D * D + D);
+  const int g = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int dt = D == 128 ? w : (w >> 1);
+    const int et = D == 128 ? i : (w & 1);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int d = 32 * dt + 8 * (r >> 2) + 4 * g + (r & 3);
+      part[d * D + 32 * et + l32] = acc[i][r];
+    }
+  }
+  __syncthreads();
+  float* zbuf = (float*)kb[0];  // [256 threads][8]
+#pragma unroll
+  for (int e = 0; e < 8; ++e) zbuf[tid * 8 + e] = zacc[e];
+  __syncthreads();
+  if (tid < D) {
+    const int cc = tid / 8, e = tid % 8;
+    float sum = 0.f;
+    for (int r = 0; r < 256 / CPR; ++r) sum += zbuf[(r * CPR + cc) * 8 + e];
+    part[D * D + tid] = sum;
+  }
+}
+
 __global__ void __launch_bounds__(256) elu1_reduce_kernel(StateParams p, int D) {
   const int64_t per = (int64_t)D * D + D;
   const int64_t total = (int64_t)p.B * p.n_heads * per;
@@ -668,10 +780,10 @@ extern "C" int wa_elu1_state(const wa_elu1_state_args* a, void* stream) {
   dim3 grid((unsigned)sp.n_chunks, (unsigned)nh, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
   if (a->D == 128) {
-    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_kernel<128, bf16_t>), grid, dim3(256), 0, s, sp);
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<128>), grid, dim3(256), 0, s, sp);
     else hipLaunchKernelGGL((elu1_state_kernel<128, float>), grid, dim3(256), 0, s, sp);
   } else {
-    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_kernel<64, bf16_t>), grid, dim3(256), 0, s, sp);
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<64>), grid, dim3(256), 0, s, sp);
     else hipLaunchKernelGGL((elu1_state_kernel<64, float>), grid, dim3(256), 0, s, sp);
   }
   int rc = wa_launch_status("elu1_state");

@@ -225,6 +225,148 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
   }
 }
 
+// Top-k routing, four rows (query blocks i0 .. i0 + 3 of one head) per workgroup, rows of at most
+// 512 blocks. Scores: thread t owns key j (= t, t + 256, ...) and forms its four rows' dot
+// products from one pass over the key's pooled vector (the rows share the head's pooled keys; the
+// pooled queries are broadcast from LDS). Then one wave per row: slot e*64 + lane lives in
+// register e of the lane, so the softmax reduces over the wave and the bitonic network runs in
+// registers (strides >= 64) and lane shuffles (strides < 64) without further barriers. The
+// softmax takes the max, fp32 exponentials and a double row sum, then p = e * (1 / sum).
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int KPL>
+__global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
+  constexpr int NP = 64 * KPL;
+  __shared__ __attribute__((aligned(16))) float q_sh[4][256];
+  __shared__ float s_sh[4][NP];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int i0 = blockIdx.x * 4, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;  // uniform per workgroup
+  const int N = p.Nkv, D = p.D;
+  const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
+
+  // 1. scores of the four rows
+  for (int u = tid; u < 4 * D; u += 256) {
+    const int r = u / D, d = u % D;
+    q_sh[r][d] = i0 + r < p.Nq ? p.qp[(row0 + i0 + r) * D + d] : 0.f;
+  }
+  __syncthreads();
+  const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * D;
+  for (int j = tid; j < N; j += 256) {
+    const float* kr = kbase + (int64_t)j * D;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if ((D & 31) == 0) {
+      for (int d0 = 0; d0 < D; d0 += 32) {
+        f32x4 kv[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) kv[c] = *(const f32x4*)(kr + d0 + 4 * c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const f32x4 qv = *(const f32x4*)(&q_sh[r][d0 + 4 * c]);
+            acc[r] = fmaf(qv[0], kv[c][0], acc[r]);
+            acc[r] = fmaf(qv[1], kv[c][1], acc[r]);
+            acc[r] = fmaf(qv[2], kv[c][2], acc[r]);
+            acc[r] = fmaf(qv[3], kv[c][3], acc[r]);
+          }
+        }
+      }
+    } else {
+      for (int d = 0; d < D; ++d) {
+        const float kd = kr[d];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_sh[r][j] = acc[r] * p.scale;
+  }
+  __syncthreads();
+  const int i = i0 + w;
+  if (i >= p.Nq) return;
+  const int64_t row = row0 + i;
+  float* ss = s_sh[w];
+
+  // 2. softmax over the row
+  float sc[KPL];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) {
+    const int j = e * 64 + lane;
+    sc[e] = j < N ? ss[j] : -INFINITY;
+    mx = fmaxf(mx, sc[e]);
+  }
+  mx = wa_wave_max(mx);
+  double se = 0.0;
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) {
+    const int j = e * 64 + lane;
+    sc[e] = j < N ? expf(sc[e] - mx) : 0.f;
+    se += (double)sc[e];
+  }
+  se = wa_wave_sum_d(se);
+  const float inv_sum = (float)(1.0 / se);
+
+  // 3. composite keys (probability order bits, inverted block id), padding 0; bitonic, descending
+  uint64_t key[KPL];
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) {
+    const int j = e * 64 + lane;
+    key[e] = j < N ? (((uint64_t)wa_float_key(sc[e] * inv_sum) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)j)) : 0ull;
+  }
+#pragma unroll
+  for (int size = 2; size <= NP; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= 64) {
+        const int es = stride >> 6;
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+          const int pe = e ^ es;
+          if (pe > e) {
+            const bool desc = ((e * 64 + lane) & size) == 0;
+            const uint64_t a = key[e], c = key[pe];
+            if ((a < c) == desc) {
+              key[e] = c;
+              key[pe] = a;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+          const uint64_t other = shfl_xor_u64(key[e], stride);
+          const bool lower = (lane & stride) == 0;
+          const bool desc = ((e * 64 + lane) & size) == 0;
+          const bool take_max = lower == desc;
+          key[e] = take_max ? (key[e] > other ? key[e] : other) : (key[e] < other ? key[e] : other);
+        }
+      }
+    }
+  }
+
+  // 4. permutation and count
+  int32_t* idx_row = p.index + row * N;
+  const int kk = p.head_k ? p.head_k[h] : N;
+  const int n = max(0, min(kk, N));
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) {
+    const int m = e * 64 + lane;
+    if (m < N) {
+      const int32_t id = (int32_t)(0xFFFFFFFFu - (uint32_t)key[e]);
+      idx_row[m] = id;
+      if (p.mask) p.mask[row * N + id] = m < n ? 1 : 0;
+    }
+  }
+  if (lane == 0) p.num[row] = n;
+}
+
 // Gini second pass: per-head threshold (mean of the head's row Ginis), then the count of sorted
 // slots whose exclusive prefix is below it. The prefix is the reference's: a sequential double
 // running sum rounded to fp32, minus the slot's own weight in fp32 (routing.py:95-113).
@@ -366,6 +508,14 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.ws_gini = a->workspace ? (float*)a->workspace + rows * a->Nkv : nullptr;
   dim3 grid((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
+  if (a->mode == WA_ROUTE_TOPK && !a->probs && !a->probs_out && a->Nkv <= 512) {
+    const dim3 wgrid((unsigned)((a->Nq + 3) / 4), (unsigned)nh, (unsigned)a->B);
+    if (a->Nkv <= 64) hipLaunchKernelGGL(route_wave_kernel<1>, wgrid, dim3(256), 0, s, rp);
+    else if (a->Nkv <= 128) hipLaunchKernelGGL(route_wave_kernel<2>, wgrid, dim3(256), 0, s, rp);
+    else if (a->Nkv <= 256) hipLaunchKernelGGL(route_wave_kernel<4>, wgrid, dim3(256), 0, s, rp);
+    else hipLaunchKernelGGL(route_wave_kernel<8>, wgrid, dim3(256), 0, s, rp);
+    return wa_launch_status("route_wave");
+  }
   hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);
   int rc = wa_launch_status("route");
   if (rc != WA_OK || a->mode != WA_ROUTE_GINI) return rc;
