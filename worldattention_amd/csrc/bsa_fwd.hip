@@ -49,6 +49,7 @@ struct FwdParams {
   const int32_t* units;  // [n_units][2] = (row, split) or NULL: unit u = (u / max_splits, u % max_splits)
   int n_units, max_splits, split;
   int64_t n_rows;
+  int k_slab_bytes, v_slab_bytes;  // bytes of one (batch, head) K / V slab: rows 0 .. Lkv-1
   float* part_o;         // [rows * max_splits][BS][D] normalized partial outputs
   float* part_lse;       // [rows * max_splits][BS] log2-sum-exp of the partials
 };
@@ -99,41 +100,39 @@ template <int D>
 __device__ __forceinline__ int k_swizzle(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 __device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
 
-// Streams one [64, D] bf16 step tile (64 consecutive key rows starting at `tile`) into swizzled
-// LDS. One wave instruction moves 1 KiB = RPI whole rows; lane L of instruction i writes row
-// r0(i) + L / CPR, slot L % CPR, and so reads the chunk that the swizzle stores in that slot.
-// Rows at or past `real` (the end of a trailing partial block) re-read the tile's row 0: finite
-// data that is masked (K) or multiplied by a zero probability (V); nothing outside the tensor is
-// read.
-template <int D, int NW, bool IS_V>
-__device__ __forceinline__ void dma_one(bf16_t* lds, const bf16_t* tile, int64_t st, int real, int w, int lane,
-                                        int i) {
-  constexpr int CPR = D / 8;            // 16-byte chunks per row
-  constexpr int RPI = 64 / CPR;         // rows per wave instruction (4 or 8)
-  const int rin = lane / CPR, pos = lane % CPR;
-  const int r0 = (i * NW + w) * RPI;
-  const int row = r0 + rin;
-  const int chunk = pos ^ (IS_V ? v_swizzle(row) : k_swizzle<D>(row));
-  const int src = real >= 64 || row < real ? row : 0;
-  __builtin_amdgcn_global_load_lds((const void*)(tile + (int64_t)src * st + chunk * 8), WA_LDS(lds + r0 * D), 16,
-                                   0, 0);
+// Raw buffer descriptor word 3 for the gfx9 family (32-bit data format; untyped loads ignore it
+// otherwise).
+#define WA_BUF_DWORD3 0x00020000
+
+// A K or V head slab (rows 0 .. Lkv-1 of one batch and head) as a buffer resource: byte offsets
+// past the slab read as zero instead of touching memory outside it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16_t* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, WA_BUF_DWORD3);
 }
 
-// The next step's tile stream, issued one instruction at a time from inside the current step's
-// MFMA loops so that a full memory queue stalls the wave between products rather than in a burst.
+// One [64, D] bf16 step tile (64 consecutive key rows) streamed into swizzled LDS with
+// direct-to-LDS buffer loads. Wave instruction i moves 1 KiB = RPI whole rows: lane L writes row
+// r0(i) + L / CPR, slot L % CPR, and so reads the chunk that the swizzle stores in that slot. The
+// per-lane byte offsets within a tile are loop-invariant; a tile is selected by the scalar offset
+// of its first row, so issuing a slice costs no vector arithmetic. Rows past a partial block's
+// end read either the following keys (finite, masked or multiplied by a zero probability) or,
+// past the slab, zeros.
 template <int D, int NW>
 struct NextTile {
-  static constexpr int NI = 64 / ((64 / (D / 8)) * NW);  // instructions per wave per tensor
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;               // rows per wave instruction (4 or 8)
+  static constexpr int NI = 64 / (RPI * NW);         // instructions per wave per tensor
+  __amdgpu_buffer_rsrc_t k_rs, v_rs;
   bf16_t* k_lds; bf16_t* v_lds;
-  const bf16_t* k_tile; const bf16_t* v_tile;
-  int64_t k_st, v_st;
-  int real;
-  bool valid;
-  __device__ __forceinline__ void k(int i, int w, int lane) const {
-    if (valid && i < NI) dma_one<D, NW, false>(k_lds, k_tile, k_st, real, w, lane, i);
+  int k_soff, v_soff;                                // byte offset of the tile's first row
+  int k_off[NI], v_off[NI];                          // this lane's byte offset per instruction
+  __device__ __forceinline__ void k(int i, int w, int) const {
+    if (i < NI)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, WA_LDS(k_lds + (i * NW + w) * RPI * D), 16, k_off[i], k_soff, 0, 0);
   }
-  __device__ __forceinline__ void v(int i, int w, int lane) const {
-    if (valid && i < NI) dma_one<D, NW, true>(v_lds, v_tile, v_st, real, w, lane, i);
+  __device__ __forceinline__ void v(int i, int w, int) const {
+    if (i < NI)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, WA_LDS(v_lds + (i * NW + w) * RPI * D), 16, v_off[i], v_soff, 0, 0);
   }
 };
 
@@ -161,8 +160,25 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
     }
   }
   if (!q_ok) return;
+  // Per 32-channel tile every global read (gate bias, q, the fused input x) is issued before the
+  // tile's stores: a store may alias a later read, which would otherwise cost one memory round
+  // trip per element.
+  const int64_t xo = (int64_t)b * p.x_sb + (int64_t)qi * p.x_st + (int64_t)h * p.x_sh;
+  const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
+    float pre[4][4], xv[4][4];
+    if (need_gate) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = t * 32 + 8 * rq + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pre[rq][i] = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f) : (float)qrow[d0 + i];
+          xv[rq][i] = p.epilogue == WA_EPI_FUSE ? wa_load_f(p.x, xo + d0 + i, p.x_dtype) : 0.f;
+        }
+      }
+    }
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
       const int d0 = t * 32 + 8 * rq + 4 * g;
@@ -171,34 +187,21 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
       for (int i = 0; i < 4; ++i) {
         float a = acc[t][rq * 4 + i] * inv;
         if (p.attn_round_bf16) a = wa_bf16_round(a);
+        if (need_gate) {
+          float pr = pre[rq][i];
+          if (p.gate_pre_bf16) pr = wa_bf16_round(pr);
+          float gs = wa_sigmoid(pr);
+          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
+          a = p.epilogue == WA_EPI_FUSE ? __fadd_rn(a, __fmul_rn(xv[rq][i], gs)) : __fmul_rn(a, gs);
+        }
         val[i] = a;
       }
-      if (need_gate) {
-        float gv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float pre = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f) : (float)qrow[d0 + i];
-          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
-          float gs = wa_sigmoid(pre);
-          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
-          gv[i] = gs;
-        }
-        if (p.epilogue == WA_EPI_FUSE) {
-          const int64_t xo = (int64_t)b * p.x_sb + (int64_t)qi * p.x_st + (int64_t)h * p.x_sh + d0;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) val[i] = __fadd_rn(val[i], __fmul_rn(wa_load_f(p.x, xo + i, p.x_dtype), gv[i]));
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) val[i] = __fmul_rn(val[i], gv[i]);
-        }
-      }
-      const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + d0;
       if (p.o_dtype == WA_BF16) {
         bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
-        *(bf16x4*)((bf16_t*)p.o + oo) = ov;
+        *(bf16x4*)((bf16_t*)p.o + oo + d0) = ov;
       } else {
         f32x4 ov = {val[0], val[1], val[2], val[3]};
-        *(f32x4*)((float*)p.o + oo) = ov;
+        *(f32x4*)((float*)p.o + oo + d0) = ov;
       }
     }
   }
@@ -401,20 +404,36 @@ bsa_unit_kernel(FwdParams p) {
   Cursor cur{__ballot(mine && my_real > 0), 0, 0, 0, false};
   cursor_next<BS>(cur, my_j, my_real);
 
+  // tile streams: slab resources and this lane's loop-invariant chunk offsets
+  using NT = NextTile<D, NW>;
+  const __amdgpu_buffer_rsrc_t k_rs = slab_rsrc(kbase, p.k_slab_bytes);
+  const __amdgpu_buffer_rsrc_t v_rs = slab_rsrc(vbase, p.v_slab_bytes);
+  int k_off[NT::NI], v_off[NT::NI];
+#pragma unroll
+  for (int i = 0; i < NT::NI; ++i) {
+    const int row = (i * NW + w) * NT::RPI + lane / NT::CPR, pos = lane % NT::CPR;
+    k_off[i] = (int)(row * p.k_st + (pos ^ k_swizzle<D>(row)) * 8) * 2;
+    v_off[i] = (int)(row * p.v_st + (pos ^ v_swizzle(row)) * 8) * 2;
+  }
+  // A finished list streams row 0 into the idle buffer (never read): the issue stays branch-free.
   auto next_tile = [&](bf16_t* kl, bf16_t* vl, const Cursor& c) {
-    NextTile<D, NW> nt;
-    const int64_t r0 = (int64_t)c.j * BS + 64 * c.half;
+    NT nt;
+    const int r0 = c.valid ? c.j * BS + 64 * c.half : 0;
+    nt.k_rs = k_rs; nt.v_rs = v_rs;
     nt.k_lds = kl; nt.v_lds = vl;
-    nt.k_tile = kbase + r0 * p.k_st; nt.v_tile = vbase + r0 * p.v_st;
-    nt.k_st = p.k_st; nt.v_st = p.v_st;
-    nt.real = c.real - 64 * c.half;
-    nt.valid = c.valid;
+    nt.k_soff = (int)(r0 * p.k_st) * 2;
+    nt.v_soff = (int)(r0 * p.v_st) * 2;
+#pragma unroll
+    for (int i = 0; i < NT::NI; ++i) {
+      nt.k_off[i] = k_off[i];
+      nt.v_off[i] = v_off[i];
+    }
     return nt;
   };
   if (cur.valid) {
-    const NextTile<D, NW> first = next_tile(k0, v0, cur);
+    const NT first = next_tile(k0, v0, cur);
 #pragma unroll
-    for (int i = 0; i < NextTile<D, NW>::NI; ++i) {
+    for (int i = 0; i < NT::NI; ++i) {
       first.k(i, w, lane);
       first.v(i, w, lane);
     }
@@ -463,6 +482,8 @@ bsa_unit_kernel(FwdParams p) {
     }
   }
 
+  // the last step streamed into the idle buffer: let it land before the workgroup's LDS is freed
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const float lsum = l_i + __shfl_xor(l_i, 32, 64);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
   if (ns == 1) {
@@ -631,6 +652,14 @@ extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
   fp.attn_round_bf16 = a->attn_round_bf16;
   fp.units = a->units; fp.n_units = (int)n_units; fp.max_splits = (int)max_splits; fp.split = (int)split;
   fp.n_rows = rows;
+  // the tile streams address one (batch, head) slab with 32-bit byte offsets
+  const int64_t k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2, v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
+  WA_CHECK_ARG(k_slab < ((int64_t)1 << 31) && v_slab < ((int64_t)1 << 31) &&
+                   ((int64_t)((a->Lkv + a->block_size - 1) / a->block_size) * a->block_size) * a->k_st * 2 < ((int64_t)1 << 31) &&
+                   ((int64_t)((a->Lkv + a->block_size - 1) / a->block_size) * a->block_size) * a->v_st * 2 < ((int64_t)1 << 31),
+               "wa_bsa_fwd: one K/V head slab must span less than 2 GiB");
+  fp.k_slab_bytes = (int)k_slab;
+  fp.v_slab_bytes = (int)v_slab;
   fp.part_o = (float*)a->workspace;
   fp.part_lse = fp.part_o + rows * max_splits * a->block_size * a->D;
   if (n_units == 0) fp.n_units = 0;

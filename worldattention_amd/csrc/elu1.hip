@@ -344,6 +344,7 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t s_w[D * D];
   __shared__ float s_z[D];
+  __shared__ float s_gb[D];
   const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
@@ -351,8 +352,17 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   const float* S = p.state + ((int64_t)b * p.n_heads + hs) * D * D;
   const bool use_w = p.epilogue == WA_EPI_GATED && p.gate_w;
 
-  // stage S^T as bf16 hi + lo (and the gate weights) in row-swizzled LDS; all loads are issued
-  // before any conversion so their latencies overlap
+  // Every global read of the workgroup is issued up front so the latencies overlap: this lane's
+  // query row, S^T (staged as bf16 hi + lo), the gate weights, z and the gate bias (both to LDS).
+  const int qi = tile * 128 + w * 32 + l32;
+  const bool q_ok = qi < p.L;
+  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
+  float qraw[DC][8];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    if (p.q_dtype == WA_BF16) load_row8<bf16_t>((const bf16_t*)p.q + qoff + c * 16 + g * 8, qraw[c]);
+    else load_row8<float>((const float*)p.q + qoff + c * 16 + g * 8, qraw[c]);
+  }
   constexpr int SU = D * CPR / 256;  // 8-element units per thread (8 or 2)
   f32x4 x0[SU], x1[SU];
   bf16x8 wv[SU];
@@ -379,19 +389,17 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
     *(bf16x8*)(s_lo + d * D + slot * 8) = lo;
     if (use_w) *(bf16x8*)(s_w + d * D + slot * 8) = wv[k];
   }
-  for (int e = tid; e < D; e += 256) s_z[e] = p.zsum[((int64_t)b * p.n_heads + hs) * D + e];
+  for (int e = tid; e < D; e += 256) {
+    s_z[e] = p.zsum[((int64_t)b * p.n_heads + hs) * D + e];
+    s_gb[e] = p.gate_b ? p.gate_b[e] : 0.f;
+  }
   __syncthreads();
 
-  const int qi = tile * 128 + w * 32 + l32;
-  const bool q_ok = qi < p.L;
-  const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
   bf16x8 qf[DC], phf[DC];
   float den = 0.f;
 #pragma unroll
   for (int c = 0; c < DC; ++c) {
-    float f[8];
-    if (p.q_dtype == WA_BF16) load_row8<bf16_t>((const bf16_t*)p.q + qoff + c * 16 + g * 8, f);
-    else load_row8<float>((const float*)p.q + qoff + c * 16 + g * 8, f);
+    float* f = qraw[c];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       if (!q_ok) f[e] = 0.f;
@@ -421,8 +429,20 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   if (!q_ok) return;
   const float inv = den > 0.f ? 1.f / den : 0.f;
   const bool need_gate = p.epilogue == WA_EPI_GATED;
+  const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
+    // every global read of the tile (gate bias or q) before its stores (see bsa_fwd.hip)
+    float pre[4][4];
+    if (need_gate) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d0 = t * 32 + 8 * rq + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pre[rq][i] = p.gate_w ? gacc[t][rq * 4 + i] + s_gb[d0 + i] : wa_load_f(p.q, qoff + d0 + i, p.q_dtype);
+      }
+    }
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
       const int d0 = t * 32 + 8 * rq + 4 * g;
@@ -432,22 +452,20 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
         float a = oacc[t][rq * 4 + i] * inv;
         if (p.lin_round_bf16) a = wa_bf16_round(a);
         if (need_gate) {
-          float pre = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f)
-                               : wa_load_f(p.q, qoff + d0 + i, p.q_dtype);
-          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
-          float gs = wa_sigmoid(pre);
+          float pr = pre[rq][i];
+          if (p.gate_pre_bf16) pr = wa_bf16_round(pr);
+          float gs = wa_sigmoid(pr);
           if (p.gate_out_bf16) gs = wa_bf16_round(gs);
           a = __fmul_rn(a, gs);
         }
         val[i] = a;
       }
-      const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + d0;
       if (p.o_dtype == WA_BF16) {
         bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
-        *(bf16x4*)((bf16_t*)p.o + oo) = ov;
+        *(bf16x4*)((bf16_t*)p.o + oo + d0) = ov;
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ((float*)p.o)[oo + i] = val[i];
+        for (int i = 0; i < 4; ++i) ((float*)p.o)[oo + d0 + i] = val[i];
       }
     }
   }
