@@ -64,6 +64,19 @@ def copy_calibration(dev) -> None:
                       "launches": 5}), flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the sparse pair from the committed counter summary (FETCH_SIZE and
+    WRITE_SIZE runs scaled by a plain-copy calibration), or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "bsa_fwd_cfg2_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -501,7 +514,7 @@ def main():
         "pct_mfma_peak_sparse": round(100 * achieved / MFMA_BF16_PEAK_TFLOPS, 2),
         "roofline": {"bound": "mfma", "kernel": "bsa_unit_kernel<128,128> + bsa_combine_kernel<128,128>",
                      "achieved": round(achieved, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None},
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, cfg, proj, c2["useful_flop"])
