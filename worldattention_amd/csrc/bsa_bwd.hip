@@ -90,29 +90,45 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// k2q: one workgroup per (batch, head slot); thread per key block scans the query rows in order.
+// k2q: one workgroup per (256 key blocks, head slot, batch). The head's row lists are staged in LDS
+// once (when they fit in K2Q_LDS_INTS), then thread j scans the query rows in order for block j
+// with broadcast reads.
 // ---------------------------------------------------------------------------------------------
+constexpr int K2Q_LDS_INTS = 12288;
+
 __global__ void __launch_bounds__(256) k2q_kernel(BwdParams p) {
-  const int hs = blockIdx.x, b = blockIdx.y;
+  __shared__ int32_t s_list[K2Q_LDS_INTS];
+  __shared__ int32_t s_num[1024];
+  const int hs = blockIdx.y, b = blockIdx.z;
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
-  for (int j = threadIdx.x; j < p.Nkv; j += 256) {
-    int32_t* out = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
-    int cnt = 0;
-    for (int i = 0; i < p.Nq; ++i) {
-      const int64_t irow = ((int64_t)b * p.H + h) * p.Nq + i;
-      const int n = row_visits(p, irow);
-      int m = 0;
-      if (p.index) {
-        const int32_t* lst = p.index + irow * p.index_width;
-        for (int s = 0; s < n; ++s) m += min(max(lst[s], 0), p.Nkv - 1) == j;
-      } else {
-        m = 1;
-      }
-      if (m > 0) out[cnt++] = i | (min(m, 32767) << 16);
-    }
-    p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j] = cnt;
+  const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
+  const int width = p.index ? (int)p.index_width : 0;
+  const bool staged = p.index && p.Nq <= 1024 && (int64_t)p.Nq * width <= K2Q_LDS_INTS;
+  if (staged) {
+    for (int i = threadIdx.x; i < p.Nq; i += 256) s_num[i] = row_visits(p, row0 + i);
+    for (int u = threadIdx.x; u < p.Nq * width; u += 256) s_list[u] = p.index[row0 * width + u];
   }
+  __syncthreads();
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= p.Nkv) return;
+  int32_t* out = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
+  int cnt = 0;
+  for (int i = 0; i < p.Nq; ++i) {
+    int m = 0;
+    if (!p.index) {
+      m = 1;
+    } else if (staged) {
+      const int n = s_num[i];
+      for (int s2 = 0; s2 < n; ++s2) m += min(max(s_list[i * width + s2], 0), p.Nkv - 1) == j;
+    } else {
+      const int n = row_visits(p, row0 + i);
+      const int32_t* lst = p.index + (row0 + i) * width;
+      for (int s2 = 0; s2 < n; ++s2) m += min(max(lst[s2], 0), p.Nkv - 1) == j;
+    }
+    if (m > 0) out[cnt++] = i | (min(m, 32767) << 16);
+  }
+  p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j] = cnt;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -391,7 +407,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
                      dim3(256), 0, s, bp);
   int rc = wa_launch_status("bsa_bwd_pre");
   if (rc) return rc;
-  hipLaunchKernelGGL(k2q_kernel, dim3(nh, bp.B), dim3(256), 0, s, bp);
+  hipLaunchKernelGGL(k2q_kernel, dim3((bp.Nkv + 255) / 256, nh, bp.B), dim3(256), 0, s, bp);
   if ((rc = wa_launch_status("bsa_bwd_k2q"))) return rc;
   if (bp.dq) {
     hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3(bp.Nq, nh, bp.B), dim3(2 * BS), 0, s, bp);

@@ -308,6 +308,9 @@ __device__ __forceinline__ void attend_step(const bf16_t* kb, const bf16_t* vb, 
     }
   }
   l_i += rs;
+  // V of this step: everything but the next step's K slices (the last NI loads) has landed, and
+  // after the barrier every wave's has.
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NI) : "memory");
 #pragma unroll
   for (int c = 0; c < PC; ++c) {
 #pragma unroll
@@ -431,12 +434,12 @@ bsa_unit_kernel(FwdParams p) {
     return nt;
   };
   if (cur.valid) {
+    // K slices before V slices: the step's waits count loads in issue order
     const NT first = next_tile(k0, v0, cur);
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) {
-      first.k(i, w, lane);
-      first.v(i, w, lane);
-    }
+    for (int i = 0; i < NT::NI; ++i) first.k(i, w, lane);
+#pragma unroll
+    for (int i = 0; i < NT::NI; ++i) first.v(i, w, lane);
   }
 
   // Per-lane LDS read offsets (elements). K (A operand of S^T = K Q^T): lane reads row kt*32 + l32,
@@ -459,15 +462,17 @@ bsa_unit_kernel(FwdParams p) {
   for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
   float m_i = -INFINITY, l_i = 0.f;
 
-  // Two-stage pipeline, one barrier per step: at the top of a step this wave's stream into the
-  // current buffer has landed (vmcnt 0) and, after the barrier, every wave's has; every wave has
-  // also finished reading the other buffer (previous step), which the next stream then refills.
+  // Two-stage pipeline with split waits: at the top of a step this step's K has landed (only its
+  // V slices, the last NI loads, may be in flight) and after the barrier every wave's has; every
+  // wave has also finished reading the other buffers (previous step), which the next step's
+  // streams then refill. V is waited for after the softmax (attend_step), which gives its
+  // stream, issued during the previous PV product, the QK product and softmax as extra lead.
   while (cur.valid) {
     {
       const int real = cur.real - 64 * cur.half;
       Cursor nxt = cur;
       cursor_next<BS>(nxt, my_j, my_real);
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
       attend_step<D, NW>(k0, v0, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k1, v1, nxt), w, lane);
       cur = nxt;
     }
@@ -476,7 +481,7 @@ bsa_unit_kernel(FwdParams p) {
       const int real = cur.real - 64 * cur.half;
       Cursor nxt = cur;
       cursor_next<BS>(nxt, my_j, my_real);
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
       attend_step<D, NW>(k1, v1, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k0, v0, nxt), w, lane);
       cur = nxt;
     }

@@ -231,22 +231,35 @@ __global__ void __launch_bounds__(256) fuse_bwd_kernel(FuseParams p) {
 }
 
 // dW, db: sum of the tile partials over (tile, batch, linear head) in a fixed order.
+// dW / db: sum of the per-(tile, batch, linear head) partials. A workgroup covers 32 elements with
+// 8 partial groups (group g sums the partials g, g + 8, ... of the fixed list order); the groups
+// are then added in a fixed order, so the result is bitwise reproducible.
 __global__ void __launch_bounds__(256) fuse_reduce_kernel(FuseParams p, int D) {
+  __shared__ float red[8][32];
   const int64_t per = (int64_t)D * D + D;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= per) return;
+  const int el = threadIdx.x & 31, grp = threadIdx.x >> 5;
+  const int64_t i = (int64_t)blockIdx.x * 32 + el;
+  const int n_src = p.n_tiles * p.B * p.H;
   float s0 = 0.f, s1 = 0.f;
-  for (int tile = 0; tile < p.n_tiles; ++tile)
-    for (int b = 0; b < p.B; ++b)
-      for (int h = 0; h < p.H; ++h) {
-        if (!(p.modes[h] & MODE_LINEAR)) continue;
-        const float v = p.part[(((int64_t)tile * p.B + b) * p.H + h) * per + i];
-        if (tile & 1) s1 += v;
-        else s0 += v;
-      }
-  const float s = s0 + s1;
-  if (i < (int64_t)D * D) p.dw[i] = s;
-  else p.db[i - (int64_t)D * D] = s;
+  if (i < per) {
+    int k = 0;
+    for (int src = grp; src < n_src; src += 8, ++k) {
+      const int h = src % p.H;
+      if (!(p.modes[h] & MODE_LINEAR)) continue;
+      const float v = p.part[(int64_t)src * per + i];   // src = (tile * B + b) * H + h
+      if (k & 1) s1 += v;
+      else s0 += v;
+    }
+  }
+  red[grp][el] = s0 + s1;
+  __syncthreads();
+  if (grp == 0 && i < per) {
+    float s = 0.f;
+#pragma unroll
+    for (int g2 = 0; g2 < 8; ++g2) s += red[g2][el];
+    if (i < (int64_t)D * D) p.dw[i] = s;
+    else p.db[i - (int64_t)D * D] = s;
+  }
 }
 
 void fill_common(FuseParams& fp, const wa_hsa_fuse_args* a) {
@@ -322,7 +335,7 @@ extern "C" int wa_hsa_fuse_bwd(const wa_hsa_fuse_args* a, void* stream) {
   if ((rc = wa_launch_status("hsa_fuse_bwd"))) return rc;
   if (a->gate_w) {
     const int64_t per = a->D * a->D + a->D;
-    hipLaunchKernelGGL(fuse_reduce_kernel, dim3((unsigned)((per + 255) / 256)), dim3(256), 0, s, fp, (int)a->D);
+    hipLaunchKernelGGL(fuse_reduce_kernel, dim3((unsigned)((per + 31) / 32)), dim3(256), 0, s, fp, (int)a->D);
     return wa_launch_status("hsa_fuse_reduce");
   }
   return WA_OK;

@@ -28,7 +28,7 @@ def _blhd(t):
 
 
 def _fuse_args(q, sparse, lin, modes_t, gate, spec, *, out=None, dout=None, dlin=None, dq=None, dgw=None, dgb=None,
-               ws=None, attn_round, lin_round):
+               ws=None, attn_round, lin_round, dq_accumulate=True):
     bsz, length, heads, d = q.shape
     return _lib.HsaFuseArgs(
         *_lib.blhd(q), *_blhd(sparse), *_blhd(lin), modes_t.data_ptr(),
@@ -36,7 +36,7 @@ def _fuse_args(q, sparse, lin, modes_t, gate, spec, *, out=None, dout=None, dlin
         *_blhd(gate), _lib.ptr(spec.w), _lib.ptr(spec.b),
         int(spec.pre_bf16), int(spec.out_bf16), int(attn_round), int(lin_round),
         *_blhd(dout), _lib.dtype_code(dout) if dout is not None else 0,
-        *_blhd(dlin), *_blhd(dq), 1,
+        *_blhd(dlin), *_blhd(dq), int(dq_accumulate),
         _lib.ptr(dgw), _lib.ptr(dgb), _lib.ptr(ws),
         bsz, heads, length, d)
 
@@ -48,8 +48,9 @@ def fuse_forward(q, sparse, lin, modes_t, gate, spec, out, *, attn_round, lin_ro
     _lib.call("wa_hsa_fuse_fwd", args, _lib.stream_ptr(dev))
 
 
-def fuse_backward(q, lin, modes_t, gate, spec, dout, dlin, dq, *, lin_round):
-    """``dlin = dout * gate``; adds the gate path into ``dq``; returns ``(dW, db)`` or ``(None, None)``."""
+def fuse_backward(q, lin, modes_t, gate, spec, dout, dlin, dq, *, lin_round, dq_accumulate=True):
+    """``dlin = dout * gate``; adds the gate path into ``dq`` (writes it with ``dq_accumulate=False``);
+    returns ``(dW, db)`` or ``(None, None)``."""
     dev = _lib.require_gpu(q, dout)
     bsz, length, heads, d = q.shape
     dgw = dgb = ws = None
@@ -59,13 +60,14 @@ def fuse_backward(q, lin, modes_t, gate, spec, dout, dlin, dq, *, lin_round):
         ws = torch.empty((_lib.lib().wa_hsa_fuse_bwd_workspace_bytes(bsz, heads, length, d),), dtype=torch.uint8,
                          device=dev)
     args = _fuse_args(q, None, lin, modes_t, gate, spec, dout=dout, dlin=dlin, dq=dq, dgw=dgw, dgb=dgb, ws=ws,
-                      attn_round=False, lin_round=lin_round)
+                      attn_round=False, lin_round=lin_round, dq_accumulate=dq_accumulate)
     _lib.call("wa_hsa_fuse_bwd", args, _lib.stream_ptr(dev))
     return dgw, dgb
 
 
-def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv):
-    """Adds the elu(x)+1 branch's gradients into fp32 ``dq``, ``dk``, ``dv`` (``wa_elu1_bwd``)."""
+def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumulate=True, kv_accumulate=True):
+    """Adds the elu(x)+1 branch's gradients into fp32 ``dq``, ``dk``, ``dv`` (``wa_elu1_bwd``); with
+    an ``*_accumulate`` flag off the gradient is written instead."""
     dev = _lib.require_gpu(q, k, v, dout)
     if k.dtype != v.dtype:
         v = v.to(k.dtype)
@@ -79,7 +81,7 @@ def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv):
     args = _lib.Elu1BwdArgs(
         *_lib.blhd(q), _lib.dtype_code(q), *_lib.blhd(k), *_lib.blhd(v), _lib.dtype_code(k),
         *_lib.blhd(dout), _lib.dtype_code(dout), state.data_ptr(), zsum.data_ptr(),
-        *_lib.blhd(dq), 1, *_lib.blhd(dk), 1, *_lib.blhd(dv), 1,
+        *_lib.blhd(dq), int(dq_accumulate), *_lib.blhd(dk), int(kv_accumulate), *_lib.blhd(dv), int(kv_accumulate),
         heads_t.data_ptr(), n, bsz, heads, lq, lkv, d, ws.data_ptr())
     _lib.call("wa_elu1_bwd", args, _lib.stream_ptr(dev))
 
@@ -224,21 +226,30 @@ class _HSA(torch.autograd.Function):
         block_size = cfg["block_size"]
         dout = dout if dout.stride(-1) == 1 and dout.dtype in (torch.float32, torch.bfloat16) else dout.float().contiguous()
         f32 = dict(dtype=torch.float32, device=dev)
-        dq = torch.zeros((bsz, q_len, heads, d), **f32)
-        dk = torch.zeros((bsz, kv_len, heads, d), **f32)
-        dv = torch.zeros((bsz, kv_len, heads, d), **f32)
+        # Split heads (each head in exactly one branch, elu1 linear heads): every gradient element
+        # has one first writer (gate for dq of linear heads, the sparse backward for its heads,
+        # elu1 for dk / dv of linear heads), which writes instead of adding, so the buffers need no
+        # zero fill. Otherwise they start at zero and every kernel accumulates.
+        fresh = (not plan.both and len(plan.sparse_only) + len(plan.linear_only) == heads
+                 and (not plan.linear or cfg["linear_mode"] == "elu1"))
+        alloc = torch.empty if fresh else torch.zeros
+        dq = alloc((bsz, q_len, heads, d), **f32)
+        dk = alloc((bsz, kv_len, heads, d), **f32)
+        dv = alloc((bsz, kv_len, heads, d), **f32)
         dgw = dgb = dkc = dvc = dEk = dEv = None
         if plan.linear:
             dlin = torch.empty((bsz, q_len, heads, d), **f32)
-            dgw, dgb = fuse_backward(qb, lin, ex["modes_t"], gate, spec, dout, dlin, dq, lin_round=ex["lin_round"])
+            dgw, dgb = fuse_backward(qb, lin, ex["modes_t"], gate, spec, dout, dlin, dq, lin_round=ex["lin_round"],
+                                     dq_accumulate=not fresh)
         if plan.sparse:
             bsa_backward(qb, kb, vb, sparse, lse_s, dout, index=index, num=num, block_size=block_size,
                          layout="blhd", heads=plan.t["sparse"], lq=q_len, lkv=kv_len, dq=dq, dk=dk, dv=dv,
-                         accumulate=True)
+                         accumulate=not fresh)
         if plan.linear:
             lt = plan.t["linear"]
             if cfg["linear_mode"] == "elu1":
-                elu1_backward(q, k, v, dlin, state, zsum, lt, dq, dk, dv)
+                elu1_backward(q, k, v, dlin, state, zsum, lt, dq, dk, dv, dq_accumulate=True,
+                              kv_accumulate=not fresh)
             else:
                 lc = kcb.shape[1]
                 dkc = torch.zeros((bsz, lc, heads, d), **f32)
