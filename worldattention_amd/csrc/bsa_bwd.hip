@@ -10,13 +10,17 @@
 //   dQ = scale dS K,  dK = scale dS^T Q,  dV = P^T dO
 //
 // Kernels:
-//   pre   — delta per query row and a compact bf16 copy of dO ([B, heads, Lq, D]) for the streams;
+//   pre   — per query row delta and the base-2 log-sum-exp (+inf for a row without one, so that
+//           its probabilities come out 0), and a compact bf16 copy of dO ([B, heads, Lq, D]);
 //   k2q   — per (batch, head, key block) the ascending list of query blocks that listed it, with
 //           multiplicity (the transposed routing of block_sparse_triton.py:364);
 //   dq    — one workgroup per query block walks its key list (64-key steps, K/V streamed to LDS);
 //   dkdv  — one workgroup per key block walks its query list (64-query steps, Q/dO streamed).
 // Lanes own one column of every 32x32 score tile, so row statistics are per lane and the
 // probabilities / score gradients feed the next product straight from the accumulators.
+#include <algorithm>
+#include <type_traits>
+
 #include "tile.h"
 
 namespace {
@@ -32,12 +36,14 @@ struct BwdParams {
   const int32_t* block_sizes;
   const int32_t* heads; int n_heads;
   int B, H, Lq, Lkv, Nq, Nkv;
+  int64_t q_slab, k_slab, v_slab;  // bytes of one (batch, head) Q / K / V slab: first row to last row's end
   float scale, scale_log2;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int dq_acc;
   float* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   float* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   // workspace
   float* delta;      // [B, n_heads, Lq]
+  float* lse2;       // [B, n_heads, Lq]: lse * log2(e), +inf where lse = -inf
   bf16_t* dob;       // [B, n_heads, Lq, D]
   int32_t* k2q;      // [B, n_heads, Nkv, Nq]: (query block) | (multiplicity << 16)
   int32_t* k2q_num;  // [B, n_heads, Nkv]
@@ -86,7 +92,12 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(BwdParams p) {
   }
 #pragma unroll
   for (int m = TPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-  if (qi < p.Lq && threadIdx.x % TPR == 0) p.delta[((int64_t)b * p.n_heads + hs) * p.Lq + qi] = s;
+  if (qi < p.Lq && threadIdx.x % TPR == 0) {
+    const int64_t r = ((int64_t)b * p.n_heads + hs) * p.Lq + qi;
+    const float l = p.lse[((int64_t)b * p.H + h) * p.Lq + qi];
+    p.delta[r] = s;
+    p.lse2[r] = l > -INFINITY ? l * WA_LOG2E : INFINITY;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -131,18 +142,57 @@ __global__ void __launch_bounds__(256) k2q_kernel(BwdParams p) {
   p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j] = cnt;
 }
 
+// The dq and dkdv passes keep one workgroup per CU (their accumulators and operand fragments
+// take 300-400 registers per lane), so they spend the CU's LDS on a 4-stage tile ring: the tiles of
+// steps t + 1 .. t + 2 stream in while step t is computed, and step t + 3 is issued into the stage
+// freed by step t - 1. Every step issues the same number of loads (an empty half-block streams
+// the slab's first rows), so the waits count them: at the top of step t only the loads of the (up to
+// two) later tiles may still be pending. Row lists (with each block's valid row count) are staged
+// in LDS once, so the loop issues no other memory reads while they fit.
+// Ring depth and staged list length: 128-row blocks (one workgroup per CU at D = 128) take four
+// stages, 64-row blocks (two or more workgroups per CU) two.
+template <int BS> constexpr int bwd_stages() { return BS == 128 ? 4 : 2; }
+template <int BS> constexpr int bwd_list_max() { return BS == 128 ? 4096 : 1024; }
+
+template <int N> using IC = std::integral_constant<int, N>;
+
+// Stage S of a ring kept as its own LDS array (four at most), so that every stage address is static.
+template <int S, class T>
+__device__ __forceinline__ T* stage_of(T* s0, T* s1, T* s2, T* s3) {
+  if constexpr (S == 0) return s0;
+  else if constexpr (S == 1) return s1;
+  else if constexpr (S == 2) return s2;
+  else return s3;
+}
+
+// Top of a step: this wave's loads of the current tile are done (at most `ahead` later tiles of
+// PER loads each still in flight) and so are its LDS reads of the previous step; the barrier
+// extends both to the workgroup, after which the previous step's stage may be refilled.
+template <int PER>
+__device__ __forceinline__ void ring_wait(int ahead) {
+  if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * PER) : "memory");
+  else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(PER) : "memory");
+  else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------------------------
 // dq: one workgroup (BS / 32 waves, wave w = query rows 32w..) per (batch, head slot, query
-// block); 64-key steps over the row's list, K and V streamed to a double-buffered LDS tile.
+// block); 64-key steps over the row's list, K and V streamed through the ring.
 // ---------------------------------------------------------------------------------------------
 template <int D, int BS>
 __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
   constexpr int NW = BS / 32, DC = D / 16, DT = D / 32;
-  constexpr int TILE = 64 * D;
-  __shared__ __attribute__((aligned(1024))) bf16_t k0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t v0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t k1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t v1[TILE];
+  constexpr int TILE = 64 * D, ST = bwd_stages<BS>(), LM = bwd_list_max<BS>();
+  using TS = TileStream<D, NW>;
+  constexpr int PER = 2 * TS::NI;                  // loads per wave per step: K and V
+  constexpr int HPV = BS / 64;                     // 64-key steps per visited block
+  constexpr int XS = ST == 4 ? 2 * TILE : 8;      // stages 2 and 3 exist only in 4-stage rings
+  // stage s: K tile at [0, TILE), V tile at [TILE, 2 TILE)
+  __shared__ __attribute__((aligned(1024))) bf16_t kv0[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t kv1[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t kv2[XS];
+  __shared__ __attribute__((aligned(1024))) bf16_t kv3[XS];
+  __shared__ int32_t s_lst[LM];  // visited block | (its valid key count << 16)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int qb = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
@@ -154,6 +204,12 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
   const bool q_ok = qi < p.Lq;
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
 
+  const int32_t* lst = p.index ? p.index + irow * p.index_width : nullptr;
+  auto visit = [&](int s2) {
+    const int j = lst ? min(max(lst[s2], 0), p.Nkv - 1) : s2;
+    return j | (kv_real(p, j, BS) << 16);
+  };
+  for (int i = tid; i < min(n, LM); i += 2 * BS) s_lst[i] = visit(i);
   bf16x8 qf[DC], dof[DC];
   {
     const bf16_t* qr = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
@@ -166,50 +222,49 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
       dof[c] = q_ok ? d : bf16x8{};
     }
   }
-  const float lse2 = q_ok ? p.lse[((int64_t)b * p.H + h) * p.Lq + qi] * WA_LOG2E : 0.f;
-  const float dl = q_ok ? p.delta[srow + qi] : 0.f;
-  // a row with no finite logsumexp (empty list) has zero gradients
-  const bool live = q_ok && lse2 > -INFINITY;
+  // a query past Lq or without a log-sum-exp gets lse2 = +inf: zero probabilities, zero gradient
+  float lse2 = q_ok ? p.lse2[srow + qi] : INFINITY;
+  float dl = q_ok ? p.delta[srow + qi] : 0.f;
+  // materialize the fragments before the ring's loads are issued: a use after the prologue would
+  // otherwise wait for every load in flight
+#pragma unroll
+  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]), "+v"(dof[c]));
+  asm volatile("" : "+v"(lse2), "+v"(dl));
+  __syncthreads();  // s_lst
 
   f32x16 dqacc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) dqacc[t] = f32x16{};
 
-  const bf16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
-  const bf16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
-  const int32_t* lst = p.index ? p.index + irow * p.index_width : nullptr;
-  // steps: visit s, half hf (BS = 128 blocks have two 64-key halves)
-  constexpr int HPV = BS / 64;
+  TS ks, vs;
+  ks.init(p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh, p.k_st, p.k_slab, w, lane);
+  vs.init(p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh, p.v_st, p.v_slab, w, lane);
   const int total = n * HPV;
-  auto step_info = [&](int t, int& j, int& real) {
-    const int s = t / HPV, hf = t % HPV;
-    j = lst ? min(max(lst[s], 0), p.Nkv - 1) : s;
-    real = kv_real(p, j, BS) - 64 * hf;
-    return (int64_t)j * BS + 64 * hf;
+  // step t = (visit t / HPV, half t % HPV): first key row and real key count (<= 0: empty half)
+  // (an empty half streams rows from key 0: never read, keeps the load count uniform)
+  auto step_at = [&](int t, int& real) -> int {
+    const int s2 = t / HPV, hf = t % HPV;
+    const int e = __builtin_amdgcn_readfirstlane(s2 < LM ? s_lst[s2] : visit(s2));
+    real = (e >> 16) - 64 * hf;
+    return real > 0 ? (e & 0xFFFF) * BS + 64 * hf : 0;
   };
-  if (total > 0) {
-    int j, real;
-    const int64_t r0 = step_info(0, j, real);
-    if (real > 0) {
-      tile_dma<D, NW>(k0, kbase + r0 * p.k_st, p.k_st, real, w, lane);
-      tile_dma<D, NW>(v0, vbase + r0 * p.v_st, p.v_st, real, w, lane);
-    }
-  }
-  for (int t = 0; t < total; ++t) {
-    int j, real;
-    step_info(t, j, real);
-    bf16_t* kc = (t & 1) ? k1 : k0;
-    bf16_t* vc = (t & 1) ? v1 : v0;
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (t + 1 < total) {
-      int jn, rn;
-      const int64_t r0 = step_info(t + 1, jn, rn);
-      if (rn > 0) {
-        tile_dma<D, NW>((t & 1) ? k0 : k1, kbase + r0 * p.k_st, p.k_st, rn, w, lane);
-        tile_dma<D, NW>((t & 1) ? v0 : v1, vbase + r0 * p.v_st, p.v_st, rn, w, lane);
-      }
-    }
-    if (real <= 0) continue;  // uniform: an empty half contributes nothing
+  auto issue = [&](auto S, int t) {
+    bf16_t* kv = stage_of<decltype(S)::value>(kv0, kv1, kv2, kv3);
+    int real;
+    const int r0 = step_at(t, real);
+    ks.issue(kv, r0, w);
+    vs.issue(kv + TILE, r0, w);
+  };
+  // step t computes on stage t % ST; the loop is unrolled by ST so that every stage is static
+  auto step = [&](auto S, int t) {
+    constexpr int SV = decltype(S)::value;
+    ring_wait<PER>(min(ST - 2, total - 1 - t));
+    if (t + ST - 1 < total) issue(IC<(SV + ST - 1) % ST>{}, t + ST - 1);  // the stage of step t - 1
+    int real;
+    step_at(t, real);
+    if (real <= 0) return;  // uniform: an empty half contributes nothing
+    const bf16_t* kc = stage_of<SV>(kv0, kv1, kv2, kv3);
+    const bf16_t* vc = kc + TILE;
     // S^T = K Q^T and dP^T = V dO^T (A from LDS, B from registers)
     f32x16 sacc[2], pacc[2];
 #pragma unroll
@@ -222,15 +277,24 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
         pacc[kt] = wa_mfma32(tile_row8<D>(vc, kt * 32 + l32, 2 * c + g), dof[c], pacc[kt]);
       }
     }
+    // keys past a partial block's end (their tile rows hold other keys) get zero probability
+    if (real < 64) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= real) sacc[kt][r] = -INFINITY;
+        }
+      }
+    }
     // dS^T = P^T (dP^T - delta), packed in accumulator order for the next product
     bf16x8 dsb[4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], p.scale_log2, -lse2));
-        if (key >= real || !live) pr = 0.f;
+        const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], p.scale_log2, -lse2));
         dsb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)(pr * (pacc[kt][r] - dl));
       }
     }
@@ -239,6 +303,20 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
       for (int tt = 0; tt < DT; ++tt) dqacc[tt] = wa_mfma32(dsb[c], tile_tr8<D>(kc, c, 32 * tt, lane), dqacc[tt]);
+    }
+  };
+  // prologue: tiles 0 .. ST - 2
+  if (total > 0) issue(IC<0>{}, 0);
+  if constexpr (ST == 4) {
+    if (total > 1) issue(IC<1>{}, 1);
+    if (total > 2) issue(IC<2>{}, 2);
+  }
+  for (int t = 0; t < total; t += ST) {
+    step(IC<0>{}, t);
+    if (t + 1 < total) step(IC<1>{}, t + 1);
+    if constexpr (ST == 4) {
+      if (t + 2 < total) step(IC<2>{}, t + 2);
+      if (t + 3 < total) step(IC<3>{}, t + 3);
     }
   }
   // accumulator lane (d = 32t + l32, g) holds rows q = 32w + 8(r/4) + 4g + r%4. With accumulation
@@ -263,18 +341,23 @@ __global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // dkdv: one workgroup (BS / 32 waves, wave w = keys 32w..) per (batch, head slot, key block);
-// 64-query steps over the query blocks that listed it, Q and dO streamed to LDS.
+// 64-query steps over the query blocks that listed it; Q, dO and the rows' log-sum-exp and delta
+// stream through the ring (the statistics as 4-byte direct-to-LDS loads, scaled at use).
 // ---------------------------------------------------------------------------------------------
 template <int D, int BS>
 __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
   constexpr int NW = BS / 32, DC = D / 16, DT = D / 32;
-  constexpr int TILE = 64 * D;
-  constexpr int QPB = BS / 64;  // 64-query steps per query block
-  __shared__ __attribute__((aligned(1024))) bf16_t q0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t d0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t q1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t d1[TILE];
-  __shared__ float st_lse[2][64], st_dl[2][64];
+  constexpr int TILE = 64 * D, ST = bwd_stages<BS>(), LM = bwd_list_max<BS>();
+  constexpr int QPB = BS / 64;                     // 64-query steps per query block
+  using TS = TileStream<D, NW>;
+  constexpr int PER = 2 * TS::NI + 2;              // Q and dO tiles, lse and delta rows
+  // stage s: Q tile at [0, TILE), dO tile at [TILE, 2 TILE), then 64 lse and 64 delta floats
+  constexpr int SS = 2 * TILE + 256, XS = ST == 4 ? SS : 8;
+  __shared__ __attribute__((aligned(1024))) bf16_t qd0[SS];
+  __shared__ __attribute__((aligned(1024))) bf16_t qd1[SS];
+  __shared__ __attribute__((aligned(1024))) bf16_t qd2[XS];
+  __shared__ __attribute__((aligned(1024))) bf16_t qd3[XS];
+  __shared__ int32_t s_lst[LM];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int j = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
@@ -286,6 +369,7 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
   const int32_t* lst = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
   const int nl = p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j];
+  for (int i = tid; i < min(nl, LM); i += 2 * BS) s_lst[i] = lst[i];
 
   // K^T and V^T fragments (B operands): lane holds row `key`, channels 16c + 8g .. +8
   bf16x8 kf[DC], vf[DC];
@@ -301,42 +385,51 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
       vf[c] = k_ok ? d : bf16x8{};
     }
   }
+#pragma unroll
+  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(kf[c]), "+v"(vf[c]));  // before the ring's loads
+  __syncthreads();  // s_lst
   f32x16 dkacc[DT], dvacc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) dkacc[t] = dvacc[t] = f32x16{};
 
-  const bf16_t* qbase = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
-  const bf16_t* dbase = p.dob + srow * D;
+  TS qs, ds;
+  qs.init(p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh, p.q_st, p.q_slab, w, lane);
+  ds.init(p.dob + srow * D, D, (int64_t)p.Lq * D * 2, w, lane);
   const int total = nl * QPB;
-  auto issue = [&](int t, bf16_t* ql, bf16_t* dl, int buf) {
-    const int e = lst[t / QPB];
-    const int i = e & 0xFFFF;
-    const int q0r = i * BS + 64 * (t % QPB);
-    const int rq = min(64, p.Lq - q0r);
-    if (rq > 0) {
-      tile_dma<D, NW>(ql, qbase + (int64_t)q0r * p.q_st, p.q_st, rq, w, lane);
-      tile_dma<D, NW>(dl, dbase + (int64_t)q0r * D, D, rq, w, lane);
-    }
-    for (int r = tid; r < 64; r += 2 * BS) {
-      const int qq = q0r + r;
-      const float lv = qq < p.Lq ? p.lse[((int64_t)b * p.H + h) * p.Lq + qq] * WA_LOG2E : -INFINITY;
-      st_lse[buf][r] = lv;
-      st_dl[buf][r] = qq < p.Lq ? p.delta[srow + qq] : 0.f;
-    }
+  // list entry: (query block) | (multiplicity << 16); lists longer than the LDS copy read the rest
+  // (the empty asm keeps the two reads apart: merged, they become one flat load that must wait
+  // for every direct-to-LDS load in flight)
+  auto entry = [&](int s2) {
+    if (s2 < LM) return __builtin_amdgcn_readfirstlane(s_lst[s2]);
+    int e = lst[s2];
+    asm volatile("" : "+v"(e));
+    return __builtin_amdgcn_readfirstlane(e);
   };
-  if (total > 0) issue(0, q0, d0, 0);
-  for (int t = 0; t < total; ++t) {
-    const int e = lst[t / QPB];
+  auto first_query = [&](int t) { return (entry(t / QPB) & 0xFFFF) * BS + 64 * (t % QPB); };
+  // every wave streams the statistics too (identical values), so all waves count the same loads
+  auto issue = [&](auto S, int t) {
+    bf16_t* qd = stage_of<decltype(S)::value>(qd0, qd1, qd2, qd3);
+    const int q0r = first_query(t);
+    const int src0 = q0r < p.Lq ? q0r : 0;  // a half past Lq streams query 0 (never used)
+    qs.issue(qd, src0, w);
+    ds.issue(qd + TILE, src0, w);
+    float* stats = (float*)(qd + 2 * TILE);
+    row_stats_dma(stats, p.lse2 + srow + src0, p.Lq - src0, lane);
+    row_stats_dma(stats + 64, p.delta + srow + src0, p.Lq - src0, lane);
+  };
+  // step t computes on stage t % ST; the loop is unrolled by ST so that every stage is static
+  auto step = [&](auto S, int t) {
+    constexpr int SV = decltype(S)::value;
+    ring_wait<PER>(min(ST - 2, total - 1 - t));
+    if (t + ST - 1 < total) issue(IC<(SV + ST - 1) % ST>{}, t + ST - 1);  // the stage of step t - 1
+    const int e = entry(t / QPB);
     const float mult = (float)(e >> 16);
     const int q0r = (e & 0xFFFF) * BS + 64 * (t % QPB);
-    const int buf = t & 1;
-    bf16_t* qc = buf ? q1 : q0;
-    bf16_t* dc = buf ? d1 : d0;
-    // the statistics of step t were written with plain LDS stores by other waves: the barrier
-    // below (after their lgkm wait) publishes them together with the streamed tiles
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (t + 1 < total) issue(t + 1, buf ? q0 : q1, buf ? d0 : d1, buf ^ 1);
-    if (q0r >= p.Lq) continue;
+    if (q0r >= p.Lq) return;
+    const bf16_t* qc = stage_of<SV>(qd0, qd1, qd2, qd3);
+    const bf16_t* dc = qc + TILE;
+    const float* st_lse2 = (const float*)(qc + 2 * TILE);
+    const float* st_dl = st_lse2 + 64;
     // S[q, key] = Q K^T and dP[q, key] = dO V^T per 32-query tile (A from LDS, B from registers)
     f32x16 sacc[2], pacc[2];
 #pragma unroll
@@ -349,18 +442,23 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
         pacc[qt] = wa_mfma32(tile_row8<D>(dc, qt * 32 + l32, 2 * c + g), vf[c], pacc[qt]);
       }
     }
-    // P and dS in accumulator order (lane = key, registers = queries), scaled by multiplicity
+    // P and dS in accumulator order (lane = key, registers = queries q = 32 qt + 8 rq + 4 g + i),
+    // scaled by multiplicity. Queries past Lq stream zero Q, dO and statistics rows: their dS and
+    // dO are 0, so they add nothing; keys past the block's end are dropped by the epilogue.
     bf16x8 pb[4], dsb[4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ql = qt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float lv = st_lse[buf][ql];
-        float pr = lv > -INFINITY ? __builtin_amdgcn_exp2f(fmaf(sacc[qt][r], p.scale_log2, -lv)) : 0.f;
-        if (!k_ok) pr = 0.f;
-        pb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(pr * mult);
-        dsb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(pr * mult * (pacc[qt][r] - st_dl[buf][ql]));
+      for (int rq = 0; rq < 4; ++rq) {
+        const f32x4 l4 = *(const f32x4*)(st_lse2 + qt * 32 + 8 * rq + 4 * g);
+        const f32x4 d4 = *(const f32x4*)(st_dl + qt * 32 + 8 * rq + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = rq * 4 + i;
+          const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[qt][r], p.scale_log2, -l4[i])) * mult;
+          pb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)pr;
+          dsb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(pr * (pacc[qt][r] - d4[i]));
+        }
       }
     }
     // dV[key, d] += P^T dO, dK[key, d] += dS^T Q: A from registers, B by transpose reads
@@ -371,6 +469,20 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
         dvacc[tt] = wa_mfma32(pb[c], tile_tr8<D>(dc, c, 32 * tt, lane), dvacc[tt]);
         dkacc[tt] = wa_mfma32(dsb[c], tile_tr8<D>(qc, c, 32 * tt, lane), dkacc[tt]);
       }
+    }
+  };
+  // prologue: tiles 0 .. ST - 2
+  if (total > 0) issue(IC<0>{}, 0);
+  if constexpr (ST == 4) {
+    if (total > 1) issue(IC<1>{}, 1);
+    if (total > 2) issue(IC<2>{}, 2);
+  }
+  for (int t = 0; t < total; t += ST) {
+    step(IC<0>{}, t);
+    if (t + 1 < total) step(IC<1>{}, t + 1);
+    if constexpr (ST == 4) {
+      if (t + 2 < total) step(IC<2>{}, t + 2);
+      if (t + 3 < total) step(IC<3>{}, t + 3);
     }
   }
   // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4; previous values of a
@@ -427,7 +539,7 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 extern "C" int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t Lkv, int64_t D,
                                               int64_t block_size) {
   const int64_t nq = (Lq + block_size - 1) / block_size, nkv = (Lkv + block_size - 1) / block_size;
-  return align256(B * n_heads * Lq * 4) + align256(B * n_heads * Lq * D * 2) +
+  return 2 * align256(B * n_heads * Lq * 4) + align256(B * n_heads * Lq * D * 2) +
          align256(B * n_heads * nkv * nq * 4) + align256(B * n_heads * nkv * 4);
 }
 
@@ -452,6 +564,12 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(nq <= 65535 && nkv <= 65535 && a->Lq < (1 << 30) && a->Lkv < (1 << 30), "wa_bsa_bwd: problem too large");
   const int64_t nh = a->heads ? a->n_heads : a->H;
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_bwd: bad head count");
+  // the tile streams address one (batch, head) slab with 32-bit byte offsets
+  const int64_t q_slab = ((a->Lq - 1) * a->q_st + a->D) * 2;
+  const int64_t k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2, v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
+  WA_CHECK_ARG(q_slab < ((int64_t)1 << 31) && k_slab < ((int64_t)1 << 31) && v_slab < ((int64_t)1 << 31) &&
+                   a->Lq * a->D * 2 < ((int64_t)1 << 31) && 64 * std::max({a->q_st, a->k_st, a->v_st}) < (1 << 30),
+               "wa_bsa_bwd: one Q/K/V head slab must span less than 2 GiB");
   if (a->B == 0 || nh == 0) return WA_OK;
 
   BwdParams bp{};
@@ -465,6 +583,7 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.block_sizes = a->block_sizes;
   bp.heads = a->heads; bp.n_heads = (int)nh;
   bp.B = (int)a->B; bp.H = (int)a->H; bp.Lq = (int)a->Lq; bp.Lkv = (int)a->Lkv; bp.Nq = (int)nq; bp.Nkv = (int)nkv;
+  bp.q_slab = q_slab; bp.k_slab = k_slab; bp.v_slab = v_slab;
   bp.scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
   bp.scale_log2 = bp.scale * WA_LOG2E;
   bp.dq = a->dq; bp.dq_sb = a->dq_sb; bp.dq_st = a->dq_st; bp.dq_sh = a->dq_sh; bp.dq_acc = a->dq_accumulate;
@@ -472,6 +591,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
   char* ws = (char*)a->workspace;
   bp.delta = (float*)ws;
+  ws += align256(a->B * nh * a->Lq * 4);
+  bp.lse2 = (float*)ws;
   ws += align256(a->B * nh * a->Lq * 4);
   bp.dob = (bf16_t*)ws;
   ws += align256(a->B * nh * a->Lq * a->D * 2);

@@ -100,10 +100,6 @@ template <int D>
 __device__ __forceinline__ int k_swizzle(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 __device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
 
-// Raw buffer descriptor word 3 for the gfx9 family (32-bit data format; untyped loads ignore it
-// otherwise).
-#define WA_BUF_DWORD3 0x00020000
-
 // A K or V head slab (rows 0 .. Lkv-1 of one batch and head) as a buffer resource: byte offsets
 // past the slab read as zero instead of touching memory outside it.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16_t* base, int bytes) {

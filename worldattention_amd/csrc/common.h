@@ -16,6 +16,10 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 #define WA_LOG2E 1.4426950408889634f
 #define WA_LN2 0.6931471805599453f
 
+// Raw buffer descriptor word 3 for the gfx9 family (32-bit data format; untyped loads ignore it
+// otherwise).
+#define WA_BUF_DWORD3 0x00020000
+
 // ---------------------------------------------------------------------------------------------
 // Host-side error reporting (wa_last_error): one thread-local message per calling thread.
 // ---------------------------------------------------------------------------------------------

@@ -22,29 +22,60 @@ __device__ __forceinline__ int dual_swizzle(int r) {
                   : (2 * ((r >> 1) & 1)) | (4 * ((r >> 2) & 1)) | ((r >> 3) & 1);
 }
 
-// One direct-to-LDS wave instruction of a step-tile stream: instruction i of wave w (NW waves)
-// writes rows r0 = (i NW + w) RPI .. +RPI (1 KiB), lane L row r0 + L / CPR, slot L % CPR, which
-// holds chunk slot ^ dual_swizzle(row). Rows at or past `real` re-read the tile's row 0 (in-bounds,
-// finite data that the caller masks).
-template <int D, int NW>
-__device__ __forceinline__ void tile_dma_one(bf16_t* lds, const bf16_t* tile, int64_t st, int real, int w,
-                                             int lane, int i) {
-  constexpr int CPR = D / 8;
-  constexpr int RPI = 64 / CPR;
-  const int rin = lane / CPR, pos = lane % CPR;
-  const int r0 = (i * NW + w) * RPI;
-  const int row = r0 + rin;
-  const int chunk = pos ^ dual_swizzle<D>(row);
-  const int src = row < real ? row : 0;
-  __builtin_amdgcn_global_load_lds((const void*)(tile + (int64_t)src * st + chunk * 8), WA_LDS_PTR(lds + r0 * D),
-                                   16, 0, 0);
+// Direct-to-LDS buffer loads written as inline assembly (16 or 4 bytes per lane; lane L writes LDS
+// at `lds` + 16 L or + 4 L). The compiler neither sees nor tracks these loads, so its own wait
+// insertion never stalls an LDS read behind them; every kernel that uses them orders them itself
+// with s_waitcnt vmcnt + s_barrier. (Through the builtins, the compiler makes some reads of one
+// ring stage wait for the loads in flight into the others.)
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
+  const unsigned m0 = (unsigned)(size_t)WA_LDS_PTR(lds);
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
+  const unsigned m0 = (unsigned)(size_t)WA_LDS_PTR(lds);
+  asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
 }
 
+// A step-tile stream over one slab (rows 0 .. R-1 with row stride `st` elements, `slab_bytes`
+// from the first row's start to the last row's end) by direct-to-LDS buffer loads. Instruction i
+// of wave w fills rows r0 = (i NW + w) RPI .. +RPI (1 KiB): lane L row r0 + L / CPR, slot L % CPR,
+// which holds chunk slot ^ dual_swizzle(row). Each tile gets a descriptor that starts at its
+// first row and ends at the slab's end, so the buffer range check (on the per-lane offset) turns
+// rows past the slab into zeros; the per-lane offsets are loop-invariant.
 template <int D, int NW>
-__device__ __forceinline__ void tile_dma(bf16_t* lds, const bf16_t* tile, int64_t st, int real, int w, int lane) {
-  constexpr int NI = 64 / ((64 / (D / 8)) * NW);
+struct TileStream {
+  static constexpr int CPR = D / 8;           // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;        // rows per wave instruction
+  static constexpr int NI = 64 / (RPI * NW);  // instructions per wave per tile
+  const char* base;
+  int64_t st_bytes, slab_bytes;
+  int off[NI];
+  __device__ __forceinline__ void init(const bf16_t* b, int64_t st, int64_t slab, int w, int lane) {
+    base = (const char*)b;
+    st_bytes = st * 2;
+    slab_bytes = slab;
 #pragma unroll
-  for (int i = 0; i < NI; ++i) tile_dma_one<D, NW>(lds, tile, st, real, w, lane, i);
+    for (int i = 0; i < NI; ++i) {
+      const int row = (i * NW + w) * RPI + lane / CPR, pos = lane % CPR;
+      off[i] = (int)(row * st_bytes) + (pos ^ dual_swizzle<D>(row)) * 16;
+    }
+  }
+  // rows row0 .. row0 + 63 (row0 < R, uniform) into `lds`
+  __device__ __forceinline__ void issue(bf16_t* lds, int row0, int w) const {
+    const int64_t o = (int64_t)row0 * st_bytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + o), (short)0, (int)(slab_bytes - o), WA_BUF_DWORD3);
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      lds_dma16(rs, lds + (i * NW + w) * RPI * D, off[i]);
+  }
+};
+
+// 64 consecutive fp32 values (lane L: element first + L; past `count` elements: zero) into `lds`
+// by one direct-to-LDS buffer load per wave.
+__device__ __forceinline__ void row_stats_dma(float* lds, const float* first, int count, int lane) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)first, (short)0, count * 4, WA_BUF_DWORD3);
+  lds_dma4(rs, lds, lane * 4);
 }
 
 // 128-bit fragment: row `row`, chunk `chunk` (8 bf16) of a swizzled tile.
