@@ -146,7 +146,9 @@ int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
  * o: the forward's attention output (fp32 preferred; its row dot product with dout is delta),
  * dout: gradient of o, lse: the forward's natural-log log-sum-exp [B, H, Lq]. index / num /
  * block_sizes / heads as in wa_bsa_fwd. dq (optional), dk + dv (optional pair): with
- * *_accumulate set the gradient is added to the existing contents. Routing is not
+ * *_accumulate set the gradient is added to the existing contents. dk / dv are fp32, or bf16
+ * (rounded to nearest even) when dkv_dtype = WA_BF16, which requires both accumulate flags off
+ * (a bf16 gradient is written once, in its final type). Routing is not
  * differentiated. Work: a preprocess pass, the transposed (key block -> query blocks) lists,
  * a dQ pass over each query block's list and a dK/dV pass over each key block's list; sums run
  * in a fixed order (reproducible). */
@@ -163,9 +165,10 @@ typedef struct wa_bsa_bwd_args {
   int64_t B, H, Lq, Lkv, D, block_size;
   float scale;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_accumulate;
-  float* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
-  float* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
+  void* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
+  void* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
   void* workspace;
+  int32_t dkv_dtype;  /* WA_F32 or WA_BF16 */
 } wa_bsa_bwd_args;
 int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t Lkv, int64_t D,
                                    int64_t block_size);
@@ -218,8 +221,9 @@ typedef struct wa_elu1_readout_args {
 int wa_elu1_readout(const wa_elu1_readout_args* args, void* stream);
 
 /* Backward of the elu(x)+1 linear branch (wa_elu1_state + PLAIN wa_elu1_readout): given the
- * forward's state / zsum and dout = dL/d(readout output), writes fp32 dq, dk, dv (BLHD; with
- * *_accumulate set, added to the contents) for the listed heads. No reference counterpart (the
+ * forward's state / zsum and dout = dL/d(readout output), writes fp32 dq and fp32 or bf16
+ * (dkv_dtype) dk, dv (BLHD; with *_accumulate set, added to the contents; bf16 only without) for
+ * the listed heads. No reference counterpart (the
  * north-star linear heads); the query-tile partial sums of dS and dz are reduced in a fixed order. */
 typedef struct wa_elu1_bwd_args {
   const void* q; int64_t q_sb, q_st, q_sh; int32_t q_dtype;
@@ -228,11 +232,12 @@ typedef struct wa_elu1_bwd_args {
   const void* dout; int64_t d_sb, d_st, d_sh; int32_t dout_dtype;
   const float* state; const float* zsum;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_accumulate;
-  float* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
-  float* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
+  void* dk; int64_t dk_sb, dk_st, dk_sh; int32_t dk_accumulate;
+  void* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
   const int32_t* heads; int64_t n_heads;
   int64_t B, H, Lq, Lkv, D;
   void* workspace;
+  int32_t dkv_dtype;  /* WA_F32 or WA_BF16 (then both kv accumulate flags must be off) */
 } wa_elu1_bwd_args;
 int64_t wa_elu1_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t D);
 int wa_elu1_bwd(const wa_elu1_bwd_args* args, void* stream);

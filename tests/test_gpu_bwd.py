@@ -155,3 +155,63 @@ def test_cfg5_wan_chunk_fwd_bwd_matches_oracle():
     got, want, parts = _grads_both(cfg, torch.zeros(d, d), torch.zeros(d), cfg["do"])
     for name, g, r in zip(("out", "dq", "dk", "dv"), got[:4], want[:4]):
         assert_close(g, r, what=f"cfg5 {name}")
+
+
+def test_bf16_dk_dv_are_the_fp32_gradients_rounded():
+    """dkv_dtype = WA_BF16: the sparse and elu1 backward kernels write dK / dV once in bf16; the
+    values are the fp32 path's, rounded to nearest even (bit-exact)."""
+    from worldattention_amd.hsa._autograd import elu1_backward
+    from worldattention_amd.hsa._bwd import bsa_backward
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(21)
+    b, h, d, bs, nq, nkv = 1, 2, 128, 128, 3, 9
+    lkv = nkv * bs - 40
+    q = torch.randn(b, nq * bs, h, d, device=DEV).bfloat16()
+    k = torch.randn(b, lkv, h, d, device=DEV).bfloat16()
+    v = torch.randn(b, lkv, h, d, device=DEV).bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int().to(DEV)
+    num = torch.tensor([[[4, 9, 2], [0, 5, 7]]], dtype=torch.int32, device=DEV)
+    out = torch.empty(b, nq * bs, h, d, device=DEV)
+    _, lse = bsa_forward(q, k, v, index=index, num=num, block_size=bs, layout="blhd", out=out, lkv=lkv,
+                           want_lse=True)
+    do = torch.randn(out.shape, device=DEV)
+    f32 = [torch.empty(t.shape, device=DEV) for t in (q, k, v)]
+    bsa_backward(q, k, v, out, lse, do, index=index, num=num, block_size=bs, layout="blhd", lkv=lkv,
+                 dq=f32[0], dk=f32[1], dv=f32[2])
+    dk16, dv16 = (torch.empty(t.shape, device=DEV, dtype=torch.bfloat16) for t in (k, v))
+    bsa_backward(q, k, v, out, lse, do, index=index, num=num, block_size=bs, layout="blhd", lkv=lkv,
+                 dq=torch.empty(q.shape, device=DEV), dk=dk16, dv=dv16)
+    assert torch.equal(dk16, f32[1].bfloat16()) and torch.equal(dv16, f32[2].bfloat16())
+
+    heads = torch.tensor([1], dtype=torch.int32, device=DEV)
+    s, z = WA.elu1_state(k, v, heads)
+    g = torch.randn(b, nq * bs, h, d, device=DEV)
+    grads = []
+    for dt in (torch.float32, torch.bfloat16):
+        dq = torch.zeros(q.shape, device=DEV)
+        dk, dv = (torch.zeros(t.shape, device=DEV, dtype=dt) for t in (k, v))
+        elu1_backward(q, k, v, g, s, z, heads, dq, dk, dv, kv_accumulate=False)
+        grads.append((dk, dv))
+    (dk32, dv32), (dk16, dv16) = grads
+    assert torch.equal(dk16[:, :, 1], dk32[:, :, 1].bfloat16()) and torch.equal(dv16[:, :, 1], dv32[:, :, 1].bfloat16())
+    with pytest.raises(Exception):
+        bsa_backward(q, k, v, out, lse, do, index=index, num=num, block_size=bs, layout="blhd", lkv=lkv,
+                     dq=torch.zeros(q.shape, device=DEV), dk=dk16, dv=dv16, accumulate=True)
+
+
+def test_hsa_bf16_inputs_get_bf16_gradients_within_tolerance():
+    """Split heads with bf16 q / k / v: dK and dV come back bf16 straight from the kernels."""
+    torch.manual_seed(12)
+    cfg = workloads.cfg1()
+    q, k, v = (t * 8 for t in (cfg["q"], cfg["k"], cfg["v"]))
+    kw = dict(block_size=cfg["block_size"], routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"],
+              linear_mode=cfg["linear_mode"], proj_segment_len=cfg["proj_segment_len"])
+    q16, k16, v16 = (t.bfloat16() for t in (q, k, v))
+    do = torch.randn(q.shape)
+    qr, kr, vr = (t.float().requires_grad_() for t in (q16, k16, v16))
+    O.hsa_attention(qr, kr, vr, **kw).float().backward(do)
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q16, k16, v16))
+    W.hsa_attention(qg, kg, vg, k_proj_mat=None, v_proj_mat=None, **kw).float().backward(do.to(DEV))
+    assert kg.grad.dtype == vg.grad.dtype == torch.bfloat16
+    for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
+        assert_close(g, r, 3e-2, 3e-3, what=f"bf16 {name}")

@@ -104,6 +104,7 @@ BsaBwdArgs = _struct("wa_bsa_bwd_args", [
     ("dk", c_void_p), ("dk_sb", c_int64), ("dk_st", c_int64), ("dk_sh", c_int64), ("dk_accumulate", c_int32),
     ("dv", c_void_p), ("dv_sb", c_int64), ("dv_st", c_int64), ("dv_sh", c_int64), ("dv_accumulate", c_int32),
     ("workspace", c_void_p),
+    ("dkv_dtype", c_int32),
 ])
 
 Elu1BwdArgs = _struct("wa_elu1_bwd_args", [
@@ -118,6 +119,7 @@ Elu1BwdArgs = _struct("wa_elu1_bwd_args", [
     ("heads", c_void_p), ("n_heads", c_int64),
     ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64),
     ("workspace", c_void_p),
+    ("dkv_dtype", c_int32),
 ])
 
 HsaFuseArgs = _struct("wa_hsa_fuse_args", [

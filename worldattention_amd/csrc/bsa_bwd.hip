@@ -39,8 +39,9 @@ struct BwdParams {
   int64_t q_slab, k_slab, v_slab;  // bytes of one (batch, head) Q / K / V slab: first row to last row's end
   float scale, scale_log2;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int dq_acc;
-  float* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
-  float* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
+  void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
+  void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
+  int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
   // workspace
   float* delta;      // [B, n_heads, Lq]
   float* lse2;       // [B, n_heads, Lq]: lse * log2(e), +inf where lse = -inf
@@ -485,10 +486,29 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
       if (t + 3 < total) step(IC<3>{}, t + 3);
     }
   }
-  // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4; previous values of a
-  // tile are all read before any store (see the dq epilogue)
-  float* dk_col = p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
-  float* dv_col = p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32;
+  // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4 (keys past the
+  // block's end are dropped)
+  const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
+  const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32;
+  if (p.dkv_bf16) {
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int row = j * BS + kk;
+        if (row < p.Lkv) {
+          const bool kval = kk < real;
+          ((bf16_t*)p.dk)[dk0 + (int64_t)row * p.dk_st + 32 * tt] = (bf16_t)(kval ? dkacc[tt][r] * p.scale : 0.f);
+          ((bf16_t*)p.dv)[dv0 + (int64_t)row * p.dv_st + 32 * tt] = (bf16_t)(kval ? dvacc[tt][r] : 0.f);
+        }
+      }
+    }
+    return;
+  }
+  // fp32: previous values of a tile are all read before any store (see the dq epilogue)
+  float* dk_col = (float*)p.dk + dk0;
+  float* dv_col = (float*)p.dv + dv0;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
     float pk[16], pv[16];
@@ -551,6 +571,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->Lq > 0 && a->Lkv > 0, "wa_bsa_bwd: bad sizes");
   WA_CHECK_ARG(a->q && a->k && a->v && a->o && a->dout && a->lse && a->workspace, "wa_bsa_bwd: null tensor");
   WA_CHECK_ARG(a->dq || (a->dk && a->dv), "wa_bsa_bwd: nothing to compute");
+  WA_CHECK_ARG(a->dkv_dtype == WA_F32 || (a->dkv_dtype == WA_BF16 && !a->dk_accumulate && !a->dv_accumulate),
+               "wa_bsa_bwd: dkv_dtype must be WA_F32, or WA_BF16 without accumulation");
   WA_CHECK_ARG(wa_aligned16(a->q) && wa_aligned16(a->k) && wa_aligned16(a->v) && wa_aligned16(a->workspace),
                "wa_bsa_bwd: q/k/v/workspace must be 16-byte aligned");
   WA_CHECK_ARG(a->q_sb % 8 == 0 && a->q_st % 8 == 0 && a->q_sh % 8 == 0 && a->k_sb % 8 == 0 && a->k_st % 8 == 0 &&
@@ -589,6 +611,7 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.dq = a->dq; bp.dq_sb = a->dq_sb; bp.dq_st = a->dq_st; bp.dq_sh = a->dq_sh; bp.dq_acc = a->dq_accumulate;
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
+  bp.dkv_bf16 = a->dkv_dtype == WA_BF16;
   char* ws = (char*)a->workspace;
   bp.delta = (float*)ws;
   ws += align256(a->B * nh * a->Lq * 4);

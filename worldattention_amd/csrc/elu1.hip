@@ -485,8 +485,9 @@ struct Elu1BwdParams {
   const void* g; int64_t g_sb, g_st, g_sh; int g_dtype;
   const float* state; const float* zsum;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int dq_acc;
-  float* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
-  float* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
+  void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
+  void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
+  int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
   const int32_t* heads; int n_heads, H, B, Lq, Lkv, n_qt;
   float* part;    // [n_qt][B][n_heads][D*D + D]
   float* dstate;  // [B][n_heads][D*D]
@@ -719,8 +720,10 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
     const int col = 32 * jt + l32;
     // all reads (k and, when accumulating, the previous dk / dv) before any store
     float kx[16], pk[16], pv[16];
-    float* dk_col = p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + col;
-    float* dv_col = p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + col;
+    const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + col;
+    const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + col;
+    float* dk_col = (float*)p.dk + dk0;
+    float* dv_col = (float*)p.dv + dv0;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -734,8 +737,14 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
     for (int r = 0; r < 16; ++r) {
       const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
       if (t < p.Lkv) {
-        dk_col[(int64_t)t * p.dk_st] = pk[r] + (dk[r] + s_z[col]) * elu1_grad(kx[r]);
-        dv_col[(int64_t)t * p.dv_st] = pv[r] + dv[r];
+        const float gk = pk[r] + (dk[r] + s_z[col]) * elu1_grad(kx[r]), gv = pv[r] + dv[r];
+        if (p.dkv_bf16) {
+          ((bf16_t*)p.dk)[dk0 + (int64_t)t * p.dk_st] = (bf16_t)gk;
+          ((bf16_t*)p.dv)[dv0 + (int64_t)t * p.dv_st] = (bf16_t)gv;
+        } else {
+          dk_col[(int64_t)t * p.dk_st] = gk;
+          dv_col[(int64_t)t * p.dv_st] = gv;
+        }
       }
     }
   }
@@ -845,6 +854,8 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   WA_CHECK_ARG(a && a->q && a->k && a->v && a->dout && a->state && a->zsum && a->workspace,
                "wa_elu1_bwd: null argument");
   WA_CHECK_ARG(a->dq && a->dk && a->dv, "wa_elu1_bwd: dq, dk and dv are required");
+  WA_CHECK_ARG(a->dkv_dtype == WA_F32 || (a->dkv_dtype == WA_BF16 && !a->dk_accumulate && !a->dv_accumulate),
+               "wa_elu1_bwd: dkv_dtype must be WA_F32, or WA_BF16 without accumulation");
   WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_elu1_bwd: head dim %lld not in {64, 128}", (long long)a->D);
   WA_CHECK_ARG((a->q_dtype == WA_F32 || a->q_dtype == WA_BF16) && (a->kv_dtype == WA_F32 || a->kv_dtype == WA_BF16) &&
                    (a->dout_dtype == WA_F32 || a->dout_dtype == WA_BF16),
@@ -868,6 +879,7 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   bp.dq = a->dq; bp.dq_sb = a->dq_sb; bp.dq_st = a->dq_st; bp.dq_sh = a->dq_sh; bp.dq_acc = a->dq_accumulate;
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
+  bp.dkv_bf16 = a->dkv_dtype == WA_BF16;
   bp.heads = a->heads; bp.n_heads = (int)nh; bp.H = (int)a->H; bp.B = (int)a->B; bp.Lq = (int)a->Lq;
   bp.Lkv = (int)a->Lkv; bp.n_qt = (int)((a->Lq + 127) / 128);
   bp.part = (float*)a->workspace;

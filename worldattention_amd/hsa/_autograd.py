@@ -67,7 +67,7 @@ def fuse_backward(q, lin, modes_t, gate, spec, dout, dlin, dq, *, lin_round, dq_
 
 def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumulate=True, kv_accumulate=True):
     """Adds the elu(x)+1 branch's gradients into fp32 ``dq``, ``dk``, ``dv`` (``wa_elu1_bwd``); with
-    an ``*_accumulate`` flag off the gradient is written instead."""
+    an ``*_accumulate`` flag off the gradient is written instead (then ``dk`` / ``dv`` may be bf16)."""
     dev = _lib.require_gpu(q, k, v, dout)
     if k.dtype != v.dtype:
         v = v.to(k.dtype)
@@ -82,7 +82,7 @@ def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumul
         *_lib.blhd(q), _lib.dtype_code(q), *_lib.blhd(k), *_lib.blhd(v), _lib.dtype_code(k),
         *_lib.blhd(dout), _lib.dtype_code(dout), state.data_ptr(), zsum.data_ptr(),
         *_lib.blhd(dq), int(dq_accumulate), *_lib.blhd(dk), int(kv_accumulate), *_lib.blhd(dv), int(kv_accumulate),
-        heads_t.data_ptr(), n, bsz, heads, lq, lkv, d, ws.data_ptr())
+        heads_t.data_ptr(), n, bsz, heads, lq, lkv, d, ws.data_ptr(), _lib.dtype_code(dk))
     _lib.call("wa_elu1_bwd", args, _lib.stream_ptr(dev))
 
 
@@ -234,8 +234,11 @@ class _HSA(torch.autograd.Function):
                  and (not plan.linear or cfg["linear_mode"] == "elu1"))
         alloc = torch.empty if fresh else torch.zeros
         dq = alloc((bsz, q_len, heads, d), **f32)
-        dk = alloc((bsz, kv_len, heads, d), **f32)
-        dv = alloc((bsz, kv_len, heads, d), **f32)
+        # written once in their final type when that is bf16 (no fp32 buffer, no cast pass)
+        kd, vd = ctx.dtypes[1], ctx.dtypes[2]
+        kv_dt = torch.bfloat16 if fresh and kd == vd == torch.bfloat16 else torch.float32
+        dk = alloc((bsz, kv_len, heads, d), dtype=kv_dt, device=dev)
+        dv = alloc((bsz, kv_len, heads, d), dtype=kv_dt, device=dev)
         dgw = dgb = dkc = dvc = dEk = dEv = None
         if plan.linear:
             dlin = torch.empty((bsz, q_len, heads, d), **f32)

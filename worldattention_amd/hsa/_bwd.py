@@ -14,11 +14,11 @@ __all__ = ["bsa_backward"]
 
 def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_sizes=None, layout="bhld",
                  heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None, accumulate=False):
-    """fp32 ``(dq, dk, dv)`` of :func:`bsa_forward` in ``layout``.
+    """``(dq, dk, dv)`` of :func:`bsa_forward` in ``layout`` (fp32; given ``dk`` / ``dv`` may be bf16).
 
     ``out`` is the forward's attention output (fp32 preferred, it sets ``delta``), ``lse`` its
     natural-log log-sum-exp ``[B, H, Lq]``. Given ``dq`` / ``dk`` / ``dv`` buffers are written, or
-    added to with ``accumulate``; only the heads in ``heads`` (device int32) are touched.
+    added to with ``accumulate`` (fp32 only); only the heads in ``heads`` (device int32) are touched.
     """
     dev = _lib.require_gpu(q, k, v, out, grad_out)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -36,6 +36,10 @@ def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_s
         dk = torch.zeros(k.shape, dtype=torch.float32, device=dev)
     if dv is None:
         dv = torch.zeros(v.shape, dtype=torch.float32, device=dev)
+    if dk.dtype != dv.dtype or dk.dtype not in (torch.float32, torch.bfloat16) or dq.dtype != torch.float32:
+        raise ValueError("dq must be fp32 and dk / dv both fp32 or both bf16")
+    if accumulate and dk.dtype != torch.float32:
+        raise ValueError("bf16 dk / dv are written, not accumulated")
     grad_out = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
     n_slots = heads.numel() if heads is not None else nheads
     ws = torch.empty((_lib.lib().wa_bsa_bwd_workspace_bytes(bsz, n_slots, lq, lkv, d, block_size),),
@@ -49,6 +53,6 @@ def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_s
         _lib.ptr(heads), n_slots if heads is not None else 0,
         bsz, nheads, lq, lkv, d, block_size, 0.0,
         *strides(dq), int(accumulate), *strides(dk), int(accumulate), *strides(dv), int(accumulate),
-        ws.data_ptr())
+        ws.data_ptr(), _lib.dtype_code(dk))
     _lib.call("wa_bsa_bwd", args, _lib.stream_ptr(dev))
     return dq, dk, dv
