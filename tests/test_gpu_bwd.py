@@ -74,6 +74,26 @@ def test_sparse_backward_rectangular_lq_ne_lkv():
         assert_close(g, r, what=name)
 
 
+def test_sparse_backward_many_query_blocks():
+    """More than 256 query blocks: the transposed lists come from the scanning kernel instead of the
+    counting one."""
+    torch.manual_seed(9)
+    b, h, d, bs = 1, 1, 64, 64
+    nq, nkv = 260, 64                  # about 12 query blocks per key block: unit-scale gradients
+    q = torch.randn(b, h, nq * bs, d).bfloat16()
+    k, v = torch.randn(b, h, nkv * bs, d).bfloat16(), torch.randn(b, h, nkv * bs, d).bfloat16()
+    index = torch.randint(0, nkv, (b, h, nq, 3), dtype=torch.int32)
+    num = torch.randint(0, 4, (b, h, nq), dtype=torch.int32)
+    sizes = torch.full((nkv,), bs, dtype=torch.int32)
+    do = torch.randn(b, h, nq * bs, d)
+    qr, kr, vr = (t.double().requires_grad_() for t in (q, k, v))
+    O.block_sparse_attention(qr, kr, vr, index, num, sizes, bs).backward(do.double())
+    qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    W.block_sparse_attention_reference(qg, kg, vg, index.to(DEV), num.to(DEV), sizes.to(DEV), bs).float().backward(do.to(DEV))
+    for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
+        assert_close(g, r, what=name)
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_elu1_backward_matches_oracle_autograd(d):
     from worldattention_amd.hsa._autograd import elu1_backward

@@ -102,6 +102,45 @@ __global__ void __launch_bounds__(256) bwd_pre_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// k2q by counting: one workgroup per (64 key blocks, head slot, batch). Every list entry of the
+// head that falls in the workgroup's key range adds 1 to cnt[key block][query block] in LDS; then
+// thread j walks row j in query order and writes the non-zero counts. For Nq <= K2Q_COUNT_NQ.
+// ---------------------------------------------------------------------------------------------
+constexpr int K2Q_COUNT_KB = 64;
+constexpr int K2Q_COUNT_NQ = 256;
+
+__global__ void __launch_bounds__(256) k2q_count_kernel(BwdParams p) {
+  __shared__ uint32_t cnt[K2Q_COUNT_KB * K2Q_COUNT_NQ];
+  __shared__ int32_t s_num[K2Q_COUNT_NQ];
+  const int hs = blockIdx.y, b = blockIdx.z, j0 = blockIdx.x * K2Q_COUNT_KB;
+  const int h = head_of(p, hs);
+  if (h < 0 || h >= p.H) return;
+  const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
+  const int width = (int)p.index_width, nq = p.Nq;
+  for (int u = threadIdx.x; u < K2Q_COUNT_KB * nq; u += 256) cnt[u] = 0;
+  for (int i = threadIdx.x; i < nq; i += 256) s_num[i] = row_visits(p, row0 + i);
+  __syncthreads();
+  for (int u = threadIdx.x; u < nq * width; u += 256) {
+    const int i = u / width, s2 = u - i * width;
+    if (s2 < s_num[i]) {
+      const int j = min(max(p.index[row0 * width + u], 0), p.Nkv - 1) - j0;
+      if (j >= 0 && j < K2Q_COUNT_KB) atomicAdd(&cnt[j * nq + i], 1u);
+    }
+  }
+  __syncthreads();
+  const int j = j0 + (int)threadIdx.x;
+  if (threadIdx.x >= K2Q_COUNT_KB || j >= p.Nkv) return;
+  int32_t* out = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
+  const uint32_t* c = cnt + threadIdx.x * nq;
+  int n = 0;
+  for (int i = 0; i < nq; ++i) {
+    const int m = (int)c[i];
+    if (m > 0) out[n++] = i | (min(m, 32767) << 16);
+  }
+  p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j] = n;
+}
+
+// ---------------------------------------------------------------------------------------------
 // k2q: one workgroup per (256 key blocks, head slot, batch). The head's row lists are staged in LDS
 // once (when they fit in K2Q_LDS_INTS), then thread j scans the query rows in order for block j
 // with broadcast reads.
@@ -539,7 +578,11 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
                      dim3(256), 0, s, bp);
   int rc = wa_launch_status("bsa_bwd_pre");
   if (rc) return rc;
-  hipLaunchKernelGGL(k2q_kernel, dim3((bp.Nkv + 255) / 256, nh, bp.B), dim3(256), 0, s, bp);
+  if (bp.index && bp.Nq <= K2Q_COUNT_NQ)
+    hipLaunchKernelGGL(k2q_count_kernel, dim3((bp.Nkv + K2Q_COUNT_KB - 1) / K2Q_COUNT_KB, nh, bp.B), dim3(256), 0, s,
+                       bp);
+  else
+    hipLaunchKernelGGL(k2q_kernel, dim3((bp.Nkv + 255) / 256, nh, bp.B), dim3(256), 0, s, bp);
   if ((rc = wa_launch_status("bsa_bwd_k2q"))) return rc;
   if (bp.dq) {
     hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3(bp.Nq, nh, bp.B), dim3(2 * BS), 0, s, bp);
