@@ -20,7 +20,7 @@ struct PoolParams {
 
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
-  extern __shared__ float red[];  // [rows_per_pass][D]
+  extern __shared__ float red[];  // [rows_per_pass][D + 4]
   const int blk = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
@@ -34,18 +34,33 @@ __global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
   if (slot < rpp) {
     const T* base = (const T*)p.x + (int64_t)b * p.sb + (int64_t)h * p.sh + (int64_t)blk * p.Bs * p.st + col;
-    for (int t = slot; t < real; t += rpp) {
-      const T* src = base + (int64_t)t * p.st;
+    // rows slot, slot + rpp, ...: groups of POOL_BATCH loads issued together, then summed in order
+    constexpr int POOL_BATCH = 8;
+    for (int t0 = slot; t0 < real; t0 += POOL_BATCH * rpp) {
+      T v[POOL_BATCH][VEC];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[i] += (float)src[i];
+      for (int k = 0; k < POOL_BATCH; ++k) {
+        const int t = t0 + k * rpp;
+        const T* src = base + (int64_t)(t < real ? t : 0) * p.st;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) v[k][i] = src[i];
+      }
+#pragma unroll
+      for (int k = 0; k < POOL_BATCH; ++k) {
+        if (t0 + k * rpp < real) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] += (float)v[k][i];
+        }
+      }
     }
+    // row stride D + 4 floats: the rows a wave stores land in different banks
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) red[slot * p.D + col + i] = acc[i];
+    for (int i = 0; i < VEC; ++i) red[slot * (p.D + 4) + col + i] = acc[i];
   }
   __syncthreads();
   for (int d = tid; d < p.D; d += 256) {
     float s = 0.f;
-    for (int r = 0; r < rpp; ++r) s += red[r * p.D + d];
+    for (int r = 0; r < rpp; ++r) s += red[r * (p.D + 4) + d];
     float m;
     const bool bf = p.emulate && p.dtype == WA_BF16;
     if (p.L % p.Bs == 0) {
@@ -453,21 +468,21 @@ extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
     const bool v8 = vec_ok && a->D % 8 == 0 && a->x_sb % 8 == 0 && a->x_st % 8 == 0 && a->x_sh % 8 == 0 && a->D / 8 <= 256;
     if (v8) {
       const int rpp = 256 / (int)(a->D / 8);
-      hipLaunchKernelGGL((pool_kernel<bf16_t, 8>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+      hipLaunchKernelGGL((pool_kernel<bf16_t, 8>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
     } else {
       WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned bf16 input needs D <= 256");
       const int rpp = 256 / (int)a->D;
-      hipLaunchKernelGGL((pool_kernel<bf16_t, 1>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+      hipLaunchKernelGGL((pool_kernel<bf16_t, 1>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
     }
   } else {
     const bool v4 = vec_ok && a->D % 4 == 0 && a->x_sb % 4 == 0 && a->x_st % 4 == 0 && a->x_sh % 4 == 0 && a->D / 4 <= 256;
     if (v4) {
       const int rpp = 256 / (int)(a->D / 4);
-      hipLaunchKernelGGL((pool_kernel<float, 4>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+      hipLaunchKernelGGL((pool_kernel<float, 4>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
     } else {
       WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned fp32 input needs D <= 256");
       const int rpp = 256 / (int)a->D;
-      hipLaunchKernelGGL((pool_kernel<float, 1>), grid, dim3(256), rpp * a->D * sizeof(float), s, pp);
+      hipLaunchKernelGGL((pool_kernel<float, 1>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
     }
   }
   return wa_launch_status("block_mean_pool");
