@@ -387,9 +387,11 @@ bsa_unit_kernel(FwdParams p) {
 
   // List entries one per lane, read once: the loop fetches them with readlane and issues no memory
   // reads besides the tile streams. A row of at most 64 visits is loaded whole and sorted by block
-  // id, and this unit takes its slice of the sorted list: the units of a head (which run together
-  // on one XCD) then sweep the key range in step and share the K/V tiles they fetch in L2. The
-  // visit order only changes the summation order. Longer rows keep list order, one slice per unit.
+  // id, and split s of the row's ns units takes the sorted positions s, s + ns, s + 2 ns, ...: every
+  // unit of a head (they run together on one XCD) then sweeps the whole key range in step with the
+  // others, so the units that list a block fetch it at about the same time and share it in L2.
+  // The visit order only changes the summation order. Longer rows keep list order, one contiguous
+  // slice per unit.
   const bool whole = n <= 64;
   const int lo = whole ? 0 : s_begin;
   const int take = whole ? n : s_end - s_begin;
@@ -397,8 +399,7 @@ bsa_unit_kernel(FwdParams p) {
   if (lane < take)
     my_j = p.index ? min(max(p.index[irow * p.index_width + lo + lane], 0), p.Nkv - 1) : lo + lane;
   if (whole) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
-  const int first = whole ? s_begin : 0, last = whole ? s_end : take;
-  const bool mine = lane >= first && lane < last;
+  const bool mine = whole ? lane < n && lane % ns == split : lane < take;
   const int my_real = mine ? block_real(p, my_j, BS) : 0;
   Cursor cur{__ballot(mine && my_real > 0), 0, 0, 0, false};
   cursor_next<BS>(cur, my_j, my_real);
