@@ -9,6 +9,8 @@
 // BOTH MFMA operands with transpose reads (ds_read_b64_tr_b16), while the next 64-token tile
 // streams into registers. The readout stages S^T once per workgroup in LDS as a bf16 hi + lo pair
 // (two MFMAs keep ~16 mantissa bits of the fp32 state).
+#include <algorithm>
+
 #include "tile.h"
 
 namespace {
@@ -488,6 +490,7 @@ struct Elu1BwdParams {
   void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
+  int64_t k_slab, v_slab;  // bytes of one (batch, head) K / V slab, first row to last row's end
   const int32_t* heads; int n_heads, H, B, Lq, Lkv, n_qt;
   float* part;    // [n_qt][B][n_heads][D*D + D]
   float* dstate;  // [B][n_heads][D*D]
@@ -705,7 +708,8 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
     }
   }
   const int tb = tile * 128 + w * 32;  // accumulator rows: tokens tb + 8(r/4) + 4g + r%4
-#pragma unroll
+  // one 32-channel column tile at a time (unrolled, the tiles' epilogues spill registers)
+#pragma unroll 1
   for (int jt = 0; jt < DT; ++jt) {
     f32x16 dk = f32x16{}, dv = f32x16{};
 #pragma unroll
@@ -719,7 +723,7 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
     }
     const int col = 32 * jt + l32;
     // all reads (k and, when accumulating, the previous dk / dv) before any store
-    float kx[16], pk[16], pv[16];
+    float kx[16], prk[16], prv[16];
     const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + col;
     const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + col;
     float* dk_col = (float*)p.dk + dk0;
@@ -730,14 +734,14 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
       const bool in = t < p.Lkv;
       const int64_t ko = (int64_t)b * p.k_sb + (int64_t)(in ? t : 0) * p.k_st + (int64_t)h * p.k_sh + col;
       kx[r] = p.kv_dtype == WA_BF16 ? (float)((const bf16_t*)p.k)[ko] : ((const float*)p.k)[ko];
-      pk[r] = p.dk_acc && in ? dk_col[(int64_t)t * p.dk_st] : 0.f;
-      pv[r] = p.dv_acc && in ? dv_col[(int64_t)t * p.dv_st] : 0.f;
+      prk[r] = p.dk_acc && in ? dk_col[(int64_t)t * p.dk_st] : 0.f;
+      prv[r] = p.dv_acc && in ? dv_col[(int64_t)t * p.dv_st] : 0.f;
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = tb + 8 * (r >> 2) + 4 * g + (r & 3);
       if (t < p.Lkv) {
-        const float gk = pk[r] + (dk[r] + s_z[col]) * elu1_grad(kx[r]), gv = pv[r] + dv[r];
+        const float gk = prk[r] + (dk[r] + s_z[col]) * elu1_grad(kx[r]), gv = prv[r] + dv[r];
         if (p.dkv_bf16) {
           ((bf16_t*)p.dk)[dk0 + (int64_t)t * p.dk_st] = (bf16_t)gk;
           ((bf16_t*)p.dv)[dv0 + (int64_t)t * p.dv_st] = (bf16_t)gv;
@@ -746,6 +750,114 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
           dv_col[(int64_t)t * p.dv_st] = gv;
         }
       }
+    }
+  }
+}
+
+// Key side, bf16 K / V in and bf16 dK / dV out (written once): the same products as
+// elu1_bwd_kv_kernel with every global access coalesced. The workgroup's K and V tiles (128 tokens)
+// stream into LDS by direct-to-LDS loads, chunk-swizzled by token (chunk ^ (token & 15)), and give
+// the A fragments; per 32-channel column tile the results go through an LDS staging tile, from
+// which each thread forms 8 consecutive channels of a token (the dK factor elu1'(k) read from the
+// K tile) and writes them with one 16-byte store.
+template <int D>
+__global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
+  constexpr int DC = D / 16, DT = D / 32, CPR = D / 8;
+  __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_k[128 * D];
+  __shared__ __attribute__((aligned(1024))) bf16_t s_v[128 * D];
+  // staging of one column tile, [2][128][32] floats: in s_v once the fragments are read (D = 128),
+  // else its own array
+  __shared__ __attribute__((aligned(1024))) float s_stage[D == 128 ? 4 : 2 * 128 * 32];
+  __shared__ float s_z[D];
+  const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, l32 = lane & 31;
+  const int64_t bh = (int64_t)b * p.n_heads + hs;
+  const int t0 = tile * 128;
+
+  // K / V tiles: wave instruction q (i-th of wave w) moves RPI rows, 64 lanes x 16 bytes
+  {
+    constexpr int RPI = 64 / CPR, NQ = 128 / RPI;
+    const int64_t ko = ((int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)t0 * p.k_st) * 2;
+    const int64_t vo = ((int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)t0 * p.v_st) * 2;
+    const int64_t kslab0 = ((int64_t)b * p.k_sb + (int64_t)h * p.k_sh) * 2;
+    const int64_t vslab0 = ((int64_t)b * p.v_sb + (int64_t)h * p.v_sh) * 2;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)p.k + ko), (short)0, (int)(p.k_slab - (ko - kslab0)), WA_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)((const char*)p.v + vo), (short)0, (int)(p.v_slab - (vo - vslab0)), WA_BUF_DWORD3);
+#pragma unroll
+    for (int i = 0; i < NQ / 4; ++i) {
+      const int q = i * 4 + w, r = q * RPI + lane / CPR, slot = lane % CPR;
+      const int ch = slot ^ (r & 15);
+      lds_dma16(krs, s_k + q * RPI * D, (int)((r * p.k_st + ch * 8) * 2));
+      lds_dma16(vrs, s_v + q * RPI * D, (int)((r * p.v_st + ch * 8) * 2));
+    }
+  }
+  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  const int tr = w * 32 + l32;  // this lane's token (A-operand row) within the tile
+  const bool t_ok = t0 + tr < p.Lkv;
+  bf16x8 vf[DC], pk[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    const int slot = (2 * c + g) ^ (tr & 15);
+    const bf16x8 kk = *(const bf16x8*)(s_k + tr * D + slot * 8);
+    const bf16x8 vv = *(const bf16x8*)(s_v + tr * D + slot * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pk[c][e] = (bf16_t)(t_ok ? elu1f((float)kk[e]) : 0.f);
+      vf[c][e] = t_ok ? vv[e] : (bf16_t)0.f;
+    }
+  }
+  // staging row r sits at physical row r ^ ((r >> 2) & 1): the two rows a wave writes per
+  // register (r and r + 4) then fall in different halves of the banks
+  float* stk = D == 128 ? (float*)s_v : s_stage;  // dK before the elu1' factor
+  float* stv = stk + 128 * 32;                    // dV
+#pragma unroll 1
+  for (int jt = 0; jt < DT; ++jt) {
+    f32x16 dk = f32x16{}, dv = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_hi, c, 32 * jt, lane), dk);
+      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_lo, c, 32 * jt, lane), dk);
+      dv = wa_mfma32(pk[c], tile_row8<D>(s_hi, 32 * jt + l32, 2 * c + g), dv);
+      dv = wa_mfma32(pk[c], tile_row8<D>(s_lo, 32 * jt + l32, 2 * c + g), dv);
+    }
+    __syncthreads();  // the previous column tile's staging has been read (and, first, the fragments)
+    const float zc = s_z[32 * jt + l32];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3), pr = row ^ ((row >> 2) & 1);
+      stk[pr * 32 + l32] = dk[r] + zc;
+      stv[pr * 32 + l32] = dv[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = tid + 256 * i, row = u >> 2, cc = u & 3, pr = row ^ ((row >> 2) & 1);
+      if (t0 + row >= p.Lkv) continue;
+      const f32x4 a0 = *(const f32x4*)(stk + pr * 32 + cc * 8), a1 = *(const f32x4*)(stk + pr * 32 + cc * 8 + 4);
+      const f32x4 b0 = *(const f32x4*)(stv + pr * 32 + cc * 8), b1 = *(const f32x4*)(stv + pr * 32 + cc * 8 + 4);
+      const bf16x8 kk = *(const bf16x8*)(s_k + row * D + (((4 * jt + cc) ^ (row & 15)) * 8));
+      bf16x8 ok, ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ok[e] = (bf16_t)(a0[e] * elu1_grad((float)kk[e]));
+        ok[e + 4] = (bf16_t)(a1[e] * elu1_grad((float)kk[e + 4]));
+        ov[e] = (bf16_t)b0[e];
+        ov[e + 4] = (bf16_t)b1[e];
+      }
+      const int64_t t = t0 + row;
+      *(bf16x8*)((bf16_t*)p.dk + (int64_t)b * p.dk_sb + t * p.dk_st + (int64_t)h * p.dk_sh + 32 * jt + cc * 8) = ok;
+      *(bf16x8*)((bf16_t*)p.dv + (int64_t)b * p.dv_sb + t * p.dv_st + (int64_t)h * p.dv_sh + 32 * jt + cc * 8) = ov;
     }
   }
 }
@@ -880,6 +992,8 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
   bp.dkv_bf16 = a->dkv_dtype == WA_BF16;
+  bp.k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2;
+  bp.v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
   bp.heads = a->heads; bp.n_heads = (int)nh; bp.H = (int)a->H; bp.B = (int)a->B; bp.Lq = (int)a->Lq;
   bp.Lkv = (int)a->Lkv; bp.n_qt = (int)((a->Lq + 127) / 128);
   bp.part = (float*)a->workspace;
@@ -894,7 +1008,17 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   if ((rc = wa_launch_status("elu1_bwd_q"))) return rc;
   hipLaunchKernelGGL(elu1_bwd_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, bp, (int)a->D);
   if ((rc = wa_launch_status("elu1_bwd_reduce"))) return rc;
-  if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv_kernel<128>, gk, dim3(256), 0, s, bp);
-  else hipLaunchKernelGGL(elu1_bwd_kv_kernel<64>, gk, dim3(256), 0, s, bp);
+  // bf16 K / V and bf16 dK / dV with 16-byte aligned rows: the coalesced kernel
+  const bool kv16 = bp.dkv_bf16 && a->kv_dtype == WA_BF16 && wa_aligned16(a->dk) && wa_aligned16(a->dv) &&
+                    a->dk_sb % 8 == 0 && a->dk_st % 8 == 0 && a->dk_sh % 8 == 0 && a->dv_sb % 8 == 0 &&
+                    a->dv_st % 8 == 0 && a->dv_sh % 8 == 0 && bp.k_slab < ((int64_t)1 << 31) &&
+                    bp.v_slab < ((int64_t)1 << 31) && 128 * std::max(a->k_st, a->v_st) < ((int64_t)1 << 30);
+  if (kv16) {
+    if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk, dim3(256), 0, s, bp);
+    else hipLaunchKernelGGL(elu1_bwd_kv16_kernel<64>, gk, dim3(256), 0, s, bp);
+  } else {
+    if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv_kernel<128>, gk, dim3(256), 0, s, bp);
+    else hipLaunchKernelGGL(elu1_bwd_kv_kernel<64>, gk, dim3(256), 0, s, bp);
+  }
   return wa_launch_status("elu1_bwd_kv");
 }
