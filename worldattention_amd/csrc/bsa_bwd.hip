@@ -42,6 +42,7 @@ struct BwdParams {
   void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
+  int dkv_vec;   // ... with 16-byte aligned rows: written through an LDS staging tile
   // workspace
   float* delta;      // [B, n_heads, Lq]
   float* lse2;       // [B, n_heads, Lq]: lse * log2(e), +inf where lse = -inf
@@ -409,7 +410,8 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
   const int32_t* lst = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
   const int nl = p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j];
-  for (int i = tid; i < min(nl, LM); i += 2 * BS) s_lst[i] = lst[i];
+  // the whole row of the table (Nq slots, the first nl valid): no wait for nl before the reads
+  for (int i = tid; i < min(p.Nq, LM); i += 2 * BS) s_lst[i] = lst[i];
 
   // K^T and V^T fragments (B operands): lane holds row `key`, channels 16c + 8g .. +8
   bf16x8 kf[DC], vf[DC];
@@ -529,6 +531,34 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
   // block's end are dropped)
   const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
   const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32;
+  if (p.dkv_vec) {
+    // bf16 tiles staged in the (drained) ring: row r, 16-byte chunk c at chunk c ^ 4 ((r >> 2) & 1),
+    // so the two rows a wave writes per register use different banks; then 16-byte stores
+    __syncthreads();
+    bf16_t* sk = qd0;
+    bf16_t* sv = qd1;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3), col = 32 * tt + l32;
+        const int at = kk * D + (((col >> 3) ^ (4 * ((kk >> 2) & 1))) << 3) + (col & 7);
+        const bool kval = kk < real;
+        sk[at] = (bf16_t)(kval ? dkacc[tt][r] * p.scale : 0.f);
+        sv[at] = (bf16_t)(kval ? dvacc[tt][r] : 0.f);
+      }
+    }
+    __syncthreads();
+    constexpr int CPR = D / 8;
+    for (int u = tid; u < BS * CPR; u += 2 * BS) {
+      const int kk = u / CPR, c = u % CPR, row = j * BS + kk;
+      if (row >= p.Lkv) continue;
+      const int at = kk * D + ((c ^ (4 * ((kk >> 2) & 1))) << 3);
+      *(bf16x8*)((bf16_t*)p.dk + dk0 - l32 + (int64_t)row * p.dk_st + c * 8) = *(const bf16x8*)(sk + at);
+      *(bf16x8*)((bf16_t*)p.dv + dv0 - l32 + (int64_t)row * p.dv_st + c * 8) = *(const bf16x8*)(sv + at);
+    }
+    return;
+  }
   if (p.dkv_bf16) {
 #pragma unroll
     for (int tt = 0; tt < DT; ++tt) {
@@ -655,6 +685,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
   bp.dkv_bf16 = a->dkv_dtype == WA_BF16;
+  bp.dkv_vec = bp.dkv_bf16 && wa_aligned16(a->dk) && wa_aligned16(a->dv) && a->dk_sb % 8 == 0 && a->dk_st % 8 == 0 &&
+               a->dk_sh % 8 == 0 && a->dv_sb % 8 == 0 && a->dv_st % 8 == 0 && a->dv_sh % 8 == 0;
   char* ws = (char*)a->workspace;
   bp.delta = (float*)ws;
   ws += align256(a->B * nh * a->Lq * 4);
