@@ -190,10 +190,13 @@ __global__ void __launch_bounds__(256) k2q_kernel(BwdParams p) {
 // the slab's first rows), so the waits count them: at the top of step t only the loads of the (up to
 // two) later tiles may still be pending. Row lists (with each block's valid row count) are staged
 // in LDS once, so the loop issues no other memory reads while they fit.
-// Ring depth and staged list length: 128-row blocks (one workgroup per CU at D = 128) take four
-// stages, 64-row blocks (two or more workgroups per CU) two.
+// Ring depth and staged list length. dK/dV (one workgroup per CU at D = 128: its accumulators and
+// K/V fragments take ~450 registers per lane) takes four stages for 128-row blocks; dQ fits two
+// waves per SIMD (256 registers), so two workgroups share a CU and it keeps a 2-stage ring (two
+// rings fit the CU's LDS).
 template <int BS> constexpr int bwd_stages() { return BS == 128 ? 4 : 2; }
 template <int BS> constexpr int bwd_list_max() { return BS == 128 ? 4096 : 1024; }
+constexpr int DQ_STAGES = 2, DQ_LIST_MAX = 1024;
 
 template <int N> using IC = std::integral_constant<int, N>;
 
@@ -221,9 +224,9 @@ __device__ __forceinline__ void ring_wait(int ahead) {
 // block); 64-key steps over the row's list, K and V streamed through the ring.
 // ---------------------------------------------------------------------------------------------
 template <int D, int BS>
-__global__ void __launch_bounds__(2 * BS) bwd_dq_kernel(BwdParams p) {
+__global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))) bwd_dq_kernel(BwdParams p) {
   constexpr int NW = BS / 32, DC = D / 16, DT = D / 32;
-  constexpr int TILE = 64 * D, ST = bwd_stages<BS>(), LM = bwd_list_max<BS>();
+  constexpr int TILE = 64 * D, ST = DQ_STAGES, LM = DQ_LIST_MAX;
   using TS = TileStream<D, NW>;
   constexpr int PER = 2 * TS::NI;                  // loads per wave per step: K and V
   constexpr int HPV = BS / 64;                     // 64-key steps per visited block
