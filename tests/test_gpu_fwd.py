@@ -293,3 +293,36 @@ def test_bsa_head_subset_split_units_match_oracle(use_visits, split):
     for hh in (1, 3):
         assert_close(out[:, :, hh], want[:, :, hh], what=f"head {hh} split {split}")
     assert torch.count_nonzero(out[:, :, 0]) == 0 and torch.count_nonzero(out[:, :, 2]) == 0
+
+
+def test_hsa_forward_graph_replays_equal_eager_calls():
+    """The cfg 2 call captured in a HIP graph (as bench.py times it): every replay, with eager work
+    and synchronizations between replays, equals the eager call bit for bit."""
+    cfg = workloads.cfg2(device=DEV, seed=3)
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=None, v_proj_mat=None, gate_lin=None,
+              block_size=cfg["block_size"], tau_min=0.35, tau_max=1.0, proj_segment_len=cfg["proj_segment_len"],
+              routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
+
+    def call():
+        with torch.no_grad():
+            return WA.hsa_forward(q, k, v, **kw)
+
+    want = call().clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = call()
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {i} differs from the eager call"
+        other = call()                    # eager work between replays
+        assert torch.equal(other, want)
+        torch.cuda.synchronize()
