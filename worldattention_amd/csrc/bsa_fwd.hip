@@ -23,6 +23,7 @@
 // trailing block mask, empty list -> 0, LSE output) and block_sparse_torch.py:16-64 (id clamping,
 // listed order, duplicates attended twice, fp32 math).
 #include "common.h"
+#include "tile.h"
 
 namespace {
 
@@ -100,35 +101,26 @@ template <int D>
 __device__ __forceinline__ int k_swizzle(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 __device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3); }
 
-// A K or V head slab (rows 0 .. Lkv-1 of one batch and head) as a buffer resource: byte offsets
-// past the slab read as zero instead of touching memory outside it.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slab_rsrc(const bf16_t* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, WA_BUF_DWORD3);
-}
-
 // One [64, D] bf16 step tile (64 consecutive key rows) streamed into swizzled LDS with
 // direct-to-LDS buffer loads. Wave instruction i moves 1 KiB = RPI whole rows: lane L writes row
 // r0(i) + L / CPR, slot L % CPR, and so reads the chunk that the swizzle stores in that slot. The
-// per-lane byte offsets within a tile are loop-invariant; a tile is selected by the scalar offset
-// of its first row, so issuing a slice costs no vector arithmetic. Rows past a partial block's
-// end read either the following keys (finite, masked or multiplied by a zero probability) or,
-// past the slab, zeros.
+// per-lane byte offsets within a tile are loop-invariant; a tile is selected by its buffer
+// descriptor, which starts at the tile's first row and ends at the slab's end. Rows past a partial
+// block's end read either the following keys (finite, masked or multiplied by a zero probability)
+// or, past the slab, zeros.
 template <int D, int NW>
 struct NextTile {
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;               // rows per wave instruction (4 or 8)
   static constexpr int NI = 64 / (RPI * NW);         // instructions per wave per tensor
-  __amdgpu_buffer_rsrc_t k_rs, v_rs;
+  __amdgpu_buffer_rsrc_t k_rs, v_rs;                 // start at the tile's first row; empty past the list
   bf16_t* k_lds; bf16_t* v_lds;
-  int k_soff, v_soff;                                // byte offset of the tile's first row
   int k_off[NI], v_off[NI];                          // this lane's byte offset per instruction
   __device__ __forceinline__ void k(int i, int w, int) const {
-    if (i < NI)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(k_rs, WA_LDS(k_lds + (i * NW + w) * RPI * D), 16, k_off[i], k_soff, 0, 0);
+    if (i < NI) lds_dma16(k_rs, k_lds + (i * NW + w) * RPI * D, k_off[i]);
   }
   __device__ __forceinline__ void v(int i, int w, int) const {
-    if (i < NI)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(v_rs, WA_LDS(v_lds + (i * NW + w) * RPI * D), 16, v_off[i], v_soff, 0, 0);
+    if (i < NI) lds_dma16(v_rs, v_lds + (i * NW + w) * RPI * D, v_off[i]);
   }
 };
 
@@ -337,12 +329,10 @@ bsa_unit_kernel(FwdParams p) {
   constexpr int NW = BS / 32;   // waves; wave w owns query rows [32w, 32w + 32)
   constexpr int DC = D / 16, DT = D / 32;
   constexpr int TILE = 64 * D;  // elements of one K (or V) step tile
-  // Two step buffers, four distinct arrays so the compiler can tell the in-flight stream of one
-  // buffer from the reads of the other.
-  __shared__ __attribute__((aligned(1024))) bf16_t k0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t v0[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t k1[TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t v1[TILE];
+  // Two K and two V step tiles (64 KiB at D = 128: two workgroups per CU), fed by inline-assembly
+  // direct-to-LDS loads that the compiler does not track (the kernel orders them itself).
+  __shared__ __attribute__((aligned(1024))) bf16_t kr[2 * TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t vr[2 * TILE];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -404,10 +394,10 @@ bsa_unit_kernel(FwdParams p) {
   Cursor cur{__ballot(mine && my_real > 0), 0, 0, 0, false};
   cursor_next<BS>(cur, my_j, my_real);
 
-  // tile streams: slab resources and this lane's loop-invariant chunk offsets
+  // tile streams: this lane's loop-invariant chunk offsets; each tile gets a buffer descriptor that
+  // starts at its first row and ends at the slab's end (rows past the slab read zeros), and a
+  // step past the end of the list an empty one (zeros, no memory traffic)
   using NT = NextTile<D, NW>;
-  const __amdgpu_buffer_rsrc_t k_rs = slab_rsrc(kbase, p.k_slab_bytes);
-  const __amdgpu_buffer_rsrc_t v_rs = slab_rsrc(vbase, p.v_slab_bytes);
   int k_off[NT::NI], v_off[NT::NI];
 #pragma unroll
   for (int i = 0; i < NT::NI; ++i) {
@@ -415,14 +405,22 @@ bsa_unit_kernel(FwdParams p) {
     k_off[i] = (int)(row * p.k_st + (pos ^ k_swizzle<D>(row)) * 8) * 2;
     v_off[i] = (int)(row * p.v_st + (pos ^ v_swizzle(row)) * 8) * 2;
   }
-  // A finished list streams row 0 into the idle buffer (never read): the issue stays branch-free.
-  auto next_tile = [&](bf16_t* kl, bf16_t* vl, const Cursor& c) {
+  auto tile_rs = [&](const Cursor& c, bool is_k) {
+    const bf16_t* base = is_k ? kbase : vbase;
+    int64_t off = 0;
+    int bytes = 0;
+    if (c.valid) {
+      off = (int64_t)(c.j * BS + 64 * c.half) * (is_k ? p.k_st : p.v_st);
+      bytes = (is_k ? p.k_slab_bytes : p.v_slab_bytes) - (int)(off * 2);
+    }
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, bytes, WA_BUF_DWORD3);
+  };
+  auto tiles = [&](bf16_t* kl, const Cursor& ck, bf16_t* vl, const Cursor& cv) {
     NT nt;
-    const int r0 = c.valid ? c.j * BS + 64 * c.half : 0;
-    nt.k_rs = k_rs; nt.v_rs = v_rs;
-    nt.k_lds = kl; nt.v_lds = vl;
-    nt.k_soff = (int)(r0 * p.k_st) * 2;
-    nt.v_soff = (int)(r0 * p.v_st) * 2;
+    nt.k_rs = tile_rs(ck, true);
+    nt.v_rs = tile_rs(cv, false);
+    nt.k_lds = kl;
+    nt.v_lds = vl;
 #pragma unroll
     for (int i = 0; i < NT::NI; ++i) {
       nt.k_off[i] = k_off[i];
@@ -430,13 +428,18 @@ bsa_unit_kernel(FwdParams p) {
     }
     return nt;
   };
+  // Q fragments in registers before the first tile loads (a later first use would wait for them)
+#pragma unroll
+  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
+  // cursor of step t + 1; prologue K(0), V(0)
+  Cursor c1 = cur;
+  cursor_next<BS>(c1, my_j, my_real);
   if (cur.valid) {
-    // K slices before V slices: the step's waits count loads in issue order
-    const NT first = next_tile(k0, v0, cur);
+    const NT a = tiles(kr, cur, vr, cur);
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) first.k(i, w, lane);
+    for (int i = 0; i < NT::NI; ++i) a.k(i, w, lane);
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) first.v(i, w, lane);
+    for (int i = 0; i < NT::NI; ++i) a.v(i, w, lane);
   }
 
   // Per-lane LDS read offsets (elements). K (A operand of S^T = K Q^T): lane reads row kt*32 + l32,
@@ -459,32 +462,23 @@ bsa_unit_kernel(FwdParams p) {
   for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
   float m_i = -INFINITY, l_i = 0.f;
 
-  // Two-stage pipeline with split waits: at the top of a step this step's K has landed (only its
-  // V slices, the last NI loads, may be in flight) and after the barrier every wave's has; every
-  // wave has also finished reading the other buffers (previous step), which the next step's
-  // streams then refill. V is waited for after the softmax (attend_step), which gives its
-  // stream, issued during the previous PV product, the QK product and softmax as extra lead.
+  // Step t computes on K(t), V(t) in stage t % 2; its QK product streams K(t + 1) and its PV
+  // product V(t + 1) into the other stage. At the top of step t only V(t) may still be in flight
+  // (the last NI loads), and before the PV product (attend_step) only K(t + 1); the barriers extend
+  // each wave's wait to the workgroup and order a stage's refill after every wave's reads of it.
+  int t = 0;
   while (cur.valid) {
-    {
-      const int real = cur.real - 64 * cur.half;
-      Cursor nxt = cur;
-      cursor_next<BS>(nxt, my_j, my_real);
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
-      attend_step<D, NW>(k0, v0, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k1, v1, nxt), w, lane);
-      cur = nxt;
-    }
-    if (!cur.valid) break;
-    {
-      const int real = cur.real - 64 * cur.half;
-      Cursor nxt = cur;
-      cursor_next<BS>(nxt, my_j, my_real);
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
-      attend_step<D, NW>(k1, v1, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2, next_tile(k0, v0, nxt), w, lane);
-      cur = nxt;
-    }
+    const int real = cur.real - 64 * cur.half;
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
+    const int vs = t & 1;
+    attend_step<D, NW>(kr + vs * TILE, vr + vs * TILE, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2,
+                       tiles(kr + (vs ^ 1) * TILE, c1, vr + (vs ^ 1) * TILE, c1), w, lane);
+    cur = c1;
+    cursor_next<BS>(c1, my_j, my_real);
+    ++t;
   }
 
-  // the last step streamed into the idle buffer: let it land before the workgroup's LDS is freed
+  // the last steps streamed empty tiles: let them land before the workgroup's LDS is freed
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const float lsum = l_i + __shfl_xor(l_i, 32, 64);
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
