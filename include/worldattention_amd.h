@@ -66,7 +66,9 @@ int wa_block_mean_pool(const wa_pool_args* args, void* stream);
  * index: [B, H, Nq, Nkv] int32, descending by weight, ties lowest block id first.
  * num:   [B, H, Nq] int32. mask (optional): [B, H, Nq, Nkv] uint8 selection mask.
  * probs (optional input) replaces the q_pooled/k_pooled map computation; probs_out (optional)
- * receives the computed map. Rows of heads not listed in `heads` are not written. */
+ * receives the computed map. For heads not listed in `heads`, num rows are written 0 and index /
+ * mask rows are not written; thresholds (optional with TOPK) is written for every head, 0 where no
+ * Gini threshold applies. No output needs initializing. */
 typedef struct wa_route_args {
   const float* probs;
   const float* q_pooled;

@@ -21,7 +21,9 @@ struct PoolParams {
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
   extern __shared__ float red[];  // [rows_per_pass][D + 4]
-  const int blk = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  // consecutive workgroups take the heads of one token block: they read neighbouring chunks of the
+  // same token rows
+  const int hs = blockIdx.x, blk = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tpr = p.D / VEC;             // threads per token row
@@ -80,7 +82,7 @@ __global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
 // ---------------------------------------------------------------------------------------------
 struct RouteParams {
   const float* probs; const float* qp; const float* kp;
-  int B, H, Nq, Nkv, D, NP;
+  int B, H, Nq, Nkv, D, NP, n_heads;
   int mode;
   float tau_min, tau_span, scale;
   const int32_t* head_k;
@@ -111,6 +113,27 @@ __device__ __forceinline__ double block_reduce_sum_d(double v, double* scratch) 
   return r;
 }
 
+// Outputs the row kernels do not produce, written by one extra workgroup (the last x index of
+// the grid, y = z = 0): num = 0 for the rows of heads outside the routed list, and thresholds = 0
+// for every head without a Gini threshold. Returns true for every workgroup of that last x index.
+__device__ bool clear_unrouted(const RouteParams& p) {
+  if (blockIdx.x != gridDim.x - 1) return false;
+  if (blockIdx.y | blockIdx.z) return true;
+  auto routed = [&](int h) {
+    if (!p.heads) return true;
+    for (int s = 0; s < p.n_heads; ++s)
+      if (p.heads[s] == h) return true;
+    return false;
+  };
+  if (p.thresholds)
+    for (int h = threadIdx.x; h < p.H; h += blockDim.x)
+      if (p.mode != WA_ROUTE_GINI || !routed(h)) p.thresholds[h] = 0.f;
+  if (p.heads)
+    for (int64_t u = threadIdx.x; u < (int64_t)p.B * p.H * p.Nq; u += blockDim.x)
+      if (!routed((int)((u / p.Nq) % p.H))) p.num[u] = 0;
+  return true;
+}
+
 __device__ __forceinline__ float key_to_float(uint64_t key) {
   const uint32_t u = (uint32_t)(key >> 32);
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
@@ -121,6 +144,7 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
   __shared__ float qrow[256];
   __shared__ double dscratch[8];
   __shared__ float fscratch[8];
+  if (clear_unrouted(p)) return;
   const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
@@ -259,6 +283,7 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   __shared__ __attribute__((aligned(16))) float q_sh[4][256];
   __shared__ float s_sh[4][NP];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+  if (clear_unrouted(p)) return;
   const int i0 = blockIdx.x * 4, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;  // uniform per workgroup
@@ -461,7 +486,8 @@ extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
   if (a->B == 0 || nh == 0 || a->num_blocks == 0) return WA_OK;
   PoolParams pp{a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype, (int)a->L, (int)a->H, (int)a->D,
                 (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding};
-  dim3 grid((unsigned)a->num_blocks, (unsigned)nh, (unsigned)a->B);
+  WA_CHECK_ARG(a->num_blocks <= 65535, "wa_block_mean_pool: more than 65535 blocks");
+  dim3 grid((unsigned)nh, (unsigned)a->num_blocks, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
   const bool vec_ok = wa_aligned16(a->x);
   if (a->x_dtype == WA_BF16) {
@@ -515,16 +541,16 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.NP = (int)(next_pow2(a->Nkv) < 256 ? 256 : next_pow2(a->Nkv));
   rp.mode = a->mode; rp.tau_min = a->tau_min; rp.tau_span = a->tau_span;
   rp.scale = (float)pow((double)a->D, -0.5);
-  rp.head_k = a->head_k; rp.heads = a->heads;
+  rp.head_k = a->head_k; rp.heads = a->heads; rp.n_heads = (int)nh;
   rp.index = a->index; rp.num = a->num; rp.thresholds = a->thresholds; rp.mask = a->mask;
   rp.probs_out = a->probs_out;
   const int64_t rows = a->B * a->H * a->Nq;
   rp.ws_sorted = (float*)a->workspace;
   rp.ws_gini = a->workspace ? (float*)a->workspace + rows * a->Nkv : nullptr;
-  dim3 grid((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B);
+  dim3 grid((unsigned)a->Nq + 1, (unsigned)nh, (unsigned)a->B);  // + the clearing workgroup
   hipStream_t s = (hipStream_t)stream;
   if (a->mode == WA_ROUTE_TOPK && !a->probs && !a->probs_out && a->Nkv <= 512) {
-    const dim3 wgrid((unsigned)((a->Nq + 3) / 4), (unsigned)nh, (unsigned)a->B);
+    const dim3 wgrid((unsigned)((a->Nq + 3) / 4) + 1, (unsigned)nh, (unsigned)a->B);
     if (a->Nkv <= 64) hipLaunchKernelGGL(route_wave_kernel<1>, wgrid, dim3(256), 0, s, rp);
     else if (a->Nkv <= 128) hipLaunchKernelGGL(route_wave_kernel<2>, wgrid, dim3(256), 0, s, rp);
     else if (a->Nkv <= 256) hipLaunchKernelGGL(route_wave_kernel<4>, wgrid, dim3(256), 0, s, rp);
@@ -534,7 +560,8 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);
   int rc = wa_launch_status("route");
   if (rc != WA_OK || a->mode != WA_ROUTE_GINI) return rc;
-  hipLaunchKernelGGL(gini_count_kernel, grid, dim3(64), (size_t)a->Nkv * sizeof(float), s, rp);
+  hipLaunchKernelGGL(gini_count_kernel, dim3((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B), dim3(64),
+                     (size_t)a->Nkv * sizeof(float), s, rp);
   return wa_launch_status("route_gini_count");
 }
 

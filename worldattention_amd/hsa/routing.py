@@ -128,9 +128,9 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
         bsz, nheads, nq, d = qp.shape
         nkv = kp.shape[2]
     index = torch.empty((bsz, nheads, nq, nkv), dtype=torch.int32, device=dev)
-    # rows of heads outside `heads` are not written by the kernel: give them num = 0
-    num = (torch.zeros if heads is not None else torch.empty)((bsz, nheads, nq), dtype=torch.int32, device=dev)
-    thresholds = torch.zeros((nheads,), dtype=torch.float32, device=dev)
+    # the kernel writes num of unrouted heads (0) and every threshold: no fill needed
+    num = torch.empty((bsz, nheads, nq), dtype=torch.int32, device=dev)
+    thresholds = torch.empty((nheads,), dtype=torch.float32, device=dev)
     mask = torch.zeros((bsz, nheads, nq, nkv), dtype=torch.bool, device=dev) if return_mask else None
     probs_out = (torch.empty((bsz, nheads, nq, nkv), dtype=torch.float32, device=dev)
                  if want_probs and probs is None else None)
