@@ -68,7 +68,9 @@ int wa_block_mean_pool(const wa_pool_args* args, void* stream);
  * probs (optional input) replaces the q_pooled/k_pooled map computation; probs_out (optional)
  * receives the computed map. For heads not listed in `heads`, num rows are written 0 and index /
  * mask rows are not written; thresholds (optional with TOPK) is written for every head, 0 where no
- * Gini threshold applies. No output needs initializing. */
+ * Gini threshold applies. No output needs initializing.
+ * clear (optional, no reference counterpart): n_clear int32 words the launch sets to 0 — the
+ * arrivals buffer of the wa_bsa_fwd launch that follows, cleared here without a launch of its own. */
 typedef struct wa_route_args {
   const float* probs;
   const float* q_pooled;
@@ -84,6 +86,7 @@ typedef struct wa_route_args {
   uint8_t* mask;
   float* probs_out;
   void* workspace;
+  int32_t* clear; int64_t n_clear;
 } wa_route_args;
 int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nkv);
 int wa_route(const wa_route_args* args, void* stream);
@@ -110,12 +113,18 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * — the gated fusion of attention.py:246-254 done in registers.
  *
  * Work is split into units of at most split_visits consecutive list entries (0 = default) per
- * (row = b, head, query block); partial results go to `workspace` and a second kernel merges them
- * in split order (results do not depend on scheduling). max_visits (0 = index_width) must bound
- * every row's num: visits past max_visits are not computed. units (optional, device int32
+ * (row = b, head, query block). A row with one unit is written by it; the units of a longer row
+ * leave normalized partials in `workspace`, and the row's last unit to finish merges them in split
+ * order (results do not depend on scheduling). max_visits (0 = index_width) must bound every
+ * row's num: visits past max_visits are not computed. units (optional, device int32
  * [n_units][2] = (row, split)) lists the units to launch, in launch order; it must contain every
- * split of every row with num > 0 (rows are numbered (b * n_heads + head_slot) * Nq + i). Without
- * it every (row, split < ceil(max_visits / split_visits)) is launched. */
+ * split of every row with num > 0 and split 0 of every row with num = 0, which writes that row
+ * (rows are numbered (b * n_heads + head_slot) * Nq + i). Without it every
+ * (row, split < max(1, ceil(max_visits / split_visits))) is launched.
+ * arrivals (optional): [rows] int32 counters the units use to find each row's last unit; they
+ * must be 0 on entry (e.g. cleared by wa_route's `clear`, or left so by the previous launch that
+ * used them) and are 0 again when the launch completes. NULL: the launch clears counters in
+ * `workspace` with one extra small kernel. Launches that overlap must not share arrivals. */
 #define WA_BSA_DEFAULT_SPLIT 16
 typedef struct wa_bsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
@@ -135,6 +144,7 @@ typedef struct wa_bsa_fwd_args {
   void* workspace;
   const int32_t* units; int64_t n_units;
   int64_t max_visits; int32_t split_visits;
+  int32_t* arrivals;
 } wa_bsa_fwd_args;
 /* Workspace bytes for rows = B * n_heads * ceil(Lq / block_size) rows. */
 int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t split_visits, int64_t block_size,

@@ -238,6 +238,29 @@ def test_hsa_cfg2_wan_chunk_matches_oracle():
     assert_close(got, want, what="cfg2")
 
 
+@pytest.mark.parametrize("gate_dtype", [torch.bfloat16, torch.float32])
+def test_hsa_gated_linear_heads_match_oracle(gate_dtype):
+    """bf16 head-adaptive call whose linear heads take the gated readout with real gate weights,
+    from a bf16 gate layer (pre-activation rounded to bf16) and from an fp32 one."""
+    torch.manual_seed(11)
+    q = torch.randn(1, 700, 4, 128).bfloat16()
+    k = torch.randn(1, 3000, 4, 128).bfloat16()
+    v = torch.randn(1, 3000, 4, 128).bfloat16()
+    w, b = torch.randn(128, 128) * 0.1, torch.randn(128) * 0.2
+    kw = dict(block_size=128, routing="topk", topk=[4, 0, 0, 8], head_modes=["sparse", "linear", "linear", "sparse"],
+              linear_mode="elu1", proj_segment_len=1000)
+    want = O.hsa_attention(q, k, v, gate_weight=w.to(gate_dtype), gate_bias=b.to(gate_dtype), **kw)
+    lin = torch.nn.Linear(128, 128).to(device=DEV, dtype=gate_dtype)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        lin.bias.copy_(b)
+        got = WA.hsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), k_coarse=None, v_coarse=None, k_proj_mat=None,
+                             v_proj_mat=None, gate_lin=lin, tau_min=0.35, tau_max=1.0, **kw)
+    for h in (1, 2):
+        assert_close(got[:, :, h], want[:, :, h], what=f"gated linear head {h} ({gate_dtype})")
+    assert_close(got, want, what=f"gated head-adaptive call ({gate_dtype})")
+
+
 def test_hsa_reference_mode_bf16_matches_oracle():
     torch.manual_seed(7)
     q = torch.randn(1, 1000, 4, 128).bfloat16()
@@ -293,6 +316,45 @@ def test_bsa_head_subset_split_units_match_oracle(use_visits, split):
     for hh in (1, 3):
         assert_close(out[:, :, hh], want[:, :, hh], what=f"head {hh} split {split}")
     assert torch.count_nonzero(out[:, :, 0]) == 0 and torch.count_nonzero(out[:, :, 2]) == 0
+
+
+@pytest.mark.parametrize("use_visits", [False, True])
+def test_bsa_arrival_counters_and_empty_rows(use_visits):
+    """Multi-unit rows are merged by their last unit: with caller-provided arrival counters the
+    output is bit for bit the one of a launch that clears its own, the counters are zero again
+    afterwards (a second launch on them agrees too), and rows with no visits (a launched head
+    whose top-k is 0, and single empty rows) are written as zero rows."""
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(5)
+    bs, d, b, h, nq, nkv = 128, 128, 1, 3, 4, 9
+    lq, lkv = nq * bs, nkv * bs - 30
+    q = torch.randn(b, lq, h, d).bfloat16()
+    k = torch.randn(b, lkv, h, d).bfloat16()
+    v = torch.randn(b, lkv, h, d).bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    ks = [7, 0, 9]
+    num = torch.tensor(ks, dtype=torch.int32).view(1, h, 1).expand(b, h, nq).contiguous()
+    if not use_visits:
+        num[0, 0, 2] = 0                  # one empty row inside a routed head
+    args = dict(index=index.to(DEV), num=num.to(DEV), block_size=bs, layout="blhd", lq=lq, lkv=lkv, split=2,
+                visits=ks if use_visits else None)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ref = torch.full((b, lq, h, d), 7.0, dtype=torch.float32, device=DEV)
+    bsa_forward(qd, kd, vd, out=ref, **args)
+    arrivals = torch.zeros(b * h * nq, dtype=torch.int32, device=DEV)
+    for _ in range(2):
+        got = torch.full((b, lq, h, d), 7.0, dtype=torch.float32, device=DEV)
+        bsa_forward(qd, kd, vd, out=got, arrivals=arrivals, **args)
+        assert torch.equal(got, ref)
+        assert torch.count_nonzero(arrivals) == 0
+    qp = O.pad_to_len(q, nq * bs).transpose(1, 2)
+    kp, vp = (O.pad_to_len(t, nkv * bs).transpose(1, 2) for t in (k, v))
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    want = O.block_sparse_attention(qp.float(), kp.float(), vp.float(), index, num, sizes, bs).transpose(1, 2)[:, :lq]
+    assert_close(ref, want, what="split rows")
+    assert torch.count_nonzero(ref[:, :, 1]) == 0
+    if not use_visits:
+        assert torch.count_nonzero(ref[:, 2 * bs:3 * bs, 0]) == 0
 
 
 def test_hsa_forward_graph_replays_equal_eager_calls():

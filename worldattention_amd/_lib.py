@@ -36,7 +36,7 @@ RouteArgs = _struct("wa_route_args", [
     ("mode", c_int32), ("tau_min", c_float), ("tau_span", c_float),
     ("head_k", c_void_p), ("heads", c_void_p), ("n_heads", c_int64),
     ("index", c_void_p), ("num", c_void_p), ("thresholds", c_void_p), ("mask", c_void_p),
-    ("probs_out", c_void_p), ("workspace", c_void_p),
+    ("probs_out", c_void_p), ("workspace", c_void_p), ("clear", c_void_p), ("n_clear", c_int64),
 ])
 
 BsaFwdArgs = _struct("wa_bsa_fwd_args", [
@@ -55,7 +55,7 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
     ("gate_w", c_void_p), ("gate_b", c_void_p),
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("attn_round_bf16", c_int32),
     ("workspace", c_void_p), ("units", c_void_p), ("n_units", c_int64),
-    ("max_visits", c_int64), ("split_visits", c_int32),
+    ("max_visits", c_int64), ("split_visits", c_int32), ("arrivals", c_void_p),
 ])
 
 BSA_DEFAULT_SPLIT = 16

@@ -53,6 +53,7 @@ struct FwdParams {
   int k_slab_bytes, v_slab_bytes;  // bytes of one (batch, head) K / V slab: rows 0 .. Lkv-1
   float* part_o;         // [rows * max_splits][BS][D] normalized partial outputs
   float* part_lse;       // [rows * max_splits][BS] log2-sum-exp of the partials
+  int* arrivals;         // [rows] units of the row done so far (zeroed by the launch)
 };
 
 // Workgroup barrier without the global-memory fence of __syncthreads (which would wait for the
@@ -358,7 +359,9 @@ bsa_unit_kernel(FwdParams p) {
   const int n = row_visits(p, irow);
   const int s_begin = split * p.split;
   const int s_end = min(n, s_begin + p.split);
-  if (s_begin >= s_end) return;  // unit beyond this row's list (an empty row is all zero)
+  // A unit beyond this row's list returns; split 0 of a row with no visits runs on with an empty
+  // list and writes the empty row (zero attention).
+  if (s_begin >= s_end && (n > 0 || split > 0)) return;
   const int ns = min((n + p.split - 1) / p.split, p.max_splits);
 
   const int qi = qb * BS + w * 32 + l32;
@@ -481,59 +484,141 @@ bsa_unit_kernel(FwdParams p) {
   // the last steps streamed empty tiles: let them land before the workgroup's LDS is freed
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const float lsum = l_i + __shfl_xor(l_i, 32, 64);
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  if (ns == 1) {
-    // the row's only unit: final output straight from registers
-    if (p.lse && g == 0 && q_ok)
-      p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lsum > 0.f ? (m_i + __log2f(lsum)) * WA_LN2 : -INFINITY;
-    write_output<D>(p, oacc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
-    return;
-  }
-  // normalized partial + log2-sum-exp for the combine pass
-  const int64_t slot = row * p.max_splits + split;
-  float* po = p.part_o + slot * (int64_t)(BS * D);
-  const int ql = w * 32 + l32;
-  if (g == 0) p.part_lse[slot * BS + ql] = lsum > 0.f ? m_i + __log2f(lsum) : -INFINITY;
+  float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  // log2-sum-exp of this unit's keys; the row's natural-log lse is this times ln 2
+  float lse2 = lsum > 0.f ? m_i + __log2f(lsum) : -INFINITY;
+  if (ns > 1) {
+    // Normalized partial + log2-sum-exp; the row's last unit to arrive merges every partial, in
+    // split order (its own is still in registers: the same fp32 values it stored). The row's units
+    // may run on different XCDs, whose L2s are not coherent with each other, so the partials are
+    // written and read with device-scope (sc1) buffer accesses instead of L2-wide write-back and
+    // invalidate, and the arrival count is a device-scope atomic taken after this workgroup's
+    // partial stores have completed; the last arrival loads the others' partials only after its
+    // count has returned. A partial is stored in accumulator-fragment order (wave, tile, quad,
+    // lane), so every store and load instruction covers 1 KiB of contiguous memory.
+    const int64_t slot0 = row * p.max_splits;
+    const int ql = w * 32 + l32;
+    constexpr int SLOT_BYTES = BS * D * 4;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(p.part_o + slot0 * (BS * D)), (short)0, ns * SLOT_BYTES, WA_BUF_DWORD3);
+    auto frag_off = [&](int sp, int t, int rq) { return sp * SLOT_BYTES + (((w * DT + t) * 4 + rq) * 64 + lane) * 16; };
+    constexpr int SC1 = 16;  // cache policy: device-scope coherent
+    if (g == 0)
+      __hip_atomic_store(p.part_lse + (slot0 + split) * BS + ql, lse2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
+    for (int t = 0; t < DT; ++t) {
 #pragma unroll
-    for (int rq = 0; rq < 4; ++rq) {
-      const int d0 = t * 32 + 8 * rq + 4 * g;
-      f32x4 ov = {oacc[t][rq * 4] * inv, oacc[t][rq * 4 + 1] * inv, oacc[t][rq * 4 + 2] * inv,
-                  oacc[t][rq * 4 + 3] * inv};
-      *(f32x4*)(po + ql * D + d0) = ov;
+      for (int rq = 0; rq < 4; ++rq) {
+        const f32x4 ov = {oacc[t][rq * 4] * inv, oacc[t][rq * 4 + 1] * inv, oacc[t][rq * 4 + 2] * inv,
+                          oacc[t][rq * 4 + 3] * inv};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ov), prs, frag_off(split, t, rq), 0, SC1);
+      }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    int* s_last = (int*)kr;  // the K ring is free: every tile load has landed and been read
+    if (tid == 0) {
+      const bool last =
+          __hip_atomic_fetch_add(p.arrivals + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ns - 1;
+      if (last) __hip_atomic_store(p.arrivals + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // reusable
+      *s_last = last;
+    }
+    __syncthreads();
+    if (!__builtin_amdgcn_readfirstlane(*s_last)) return;  // uniform: one LDS word for every lane
+    // Another unit's partial comes in by direct-to-LDS loads into this wave's 16 KiB of the free
+    // K/V rings (each wave reads back only what it loaded: no workgroup barrier), the first one
+    // together with the first four log2-sum-exps, so a two-unit row merges after one round trip.
+    float* plse = p.part_lse + slot0 * BS + ql;
+    auto load_lse = [&](int sp) {
+      return sp == split ? lse2 : __hip_atomic_load(plse + sp * BS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    constexpr int WPH = (NW + 1) / 2;  // waves staged in each ring
+    static_assert(WPH * DT * 4 * 1024 <= 2 * TILE * 2, "partial staging does not fit the rings");
+    char* wbuf = (w < WPH ? (char*)kr : (char*)vr) + (w % WPH) * (DT * 4 * 1024);
+    auto fetch_part = [&](int sp) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) lds_dma16_sc1(prs, wbuf + (t * 4 + rq) * 1024, frag_off(sp, t, rq));
+      }
+    };
+    const int sp_first = split == 0 ? 1 : 0;
+    fetch_part(sp_first);
+    const float l0 = load_lse(0), l1 = load_lse(1);
+    const float l2 = ns > 2 ? load_lse(2) : -INFINITY, l3 = ns > 3 ? load_lse(3) : -INFINITY;
+    auto lse_of = [&](int sp) { return sp == 0 ? l0 : sp == 1 ? l1 : sp == 2 ? l2 : sp == 3 ? l3 : load_lse(sp); };
+    float M = -INFINITY;
+#pragma unroll 1
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, lse_of(sp));
+    float Z = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll 1
+      for (int sp = 0; sp < ns; ++sp) {
+        const float wgt = exp2f(lse_of(sp) - M);
+        if (wgt != 0.f) Z += wgt;
+      }
+    }
+    // sum the weighted partials in split order (zero weights skipped)
+    f32x16 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
+#pragma unroll 1
+    for (int sp = 0; sp < ns; ++sp) {
+      const float wgt = M != -INFINITY ? exp2f(lse_of(sp) - M) : 0.f;
+      if (sp == split) {
+        if (wgt != 0.f) {
+#pragma unroll
+          for (int t = 0; t < DT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[t][i] = fmaf(wgt, oacc[t][i] * inv, acc[t][i]);
+          }
+        }
+        continue;
+      }
+      if (sp != sp_first) fetch_part(sp);  // the buffer is free: the previous partial was read
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (wgt != 0.f) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const f32x4 v = *(const f32x4*)(wbuf + (t * 4 + rq) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[t][rq * 4 + i] = fmaf(wgt, v[i], acc[t][rq * 4 + i]);
+          }
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next fetch
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] = acc[t];
+    inv = Z > 0.f ? 1.f / Z : 0.f;
+    lse2 = Z > 0.f ? M + log2f(Z) : -INFINITY;
   }
+  if (p.lse && g == 0 && q_ok) p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lse2 * WA_LN2;
+  write_output<D>(p, oacc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
 }
 
-// Merges the partials of each row that has two or more units, in split order, and writes rows
-// with no visits at all; rows with exactly one unit were written by the unit kernel.
+// Merges the ns normalized partials of one row (slot = row * max_splits + split), in split order,
+// and writes the row's output and lse; ns = 0 writes an empty row (no visits: zero attention).
 template <int D, int BS>
-__global__ void __launch_bounds__(2 * BS) bsa_combine_kernel(FwdParams p) {
+__device__ __forceinline__ void merge_row(const FwdParams& p, int64_t row, int ns, int b, int h, int qb, int w, int lane) {
   constexpr int DC = D / 16, DT = D / 32;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int64_t row = blockIdx.x;
-  const int qb = (int)(row % p.Nq);
-  const int64_t bh = row / p.Nq;
-  const int hs = (int)(bh % p.n_heads), b = (int)(bh / p.n_heads);
-  const int h = p.heads ? p.heads[hs] : hs;
-  if (h < 0 || h >= p.H) return;
-  const int n = row_visits(p, ((int64_t)b * p.H + h) * p.Nq + qb);
-  const int ns = min(n > 0 ? (n + p.split - 1) / p.split : 0, p.max_splits);
-  if (ns == 1) return;
   const int qi = qb * BS + w * 32 + l32;
   const bool q_ok = qi < p.Lq;
   const int ql = w * 32 + l32;
   const int64_t slot0 = row * p.max_splits;
 
   float M = -INFINITY;
+#pragma unroll 1
   for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, p.part_lse[(slot0 + sp) * BS + ql]);
   f32x16 acc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
   float Z = 0.f;
   if (M != -INFINITY) {
+#pragma unroll 1
     for (int sp = 0; sp < ns; ++sp) {
       const float ls = p.part_lse[(slot0 + sp) * BS + ql];
       const float wgt = exp2f(ls - M);
@@ -564,13 +649,34 @@ __global__ void __launch_bounds__(2 * BS) bsa_combine_kernel(FwdParams p) {
   write_output<D>(p, acc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
 }
 
+// Writes every row when there is no unit to launch (all rows empty).
 template <int D, int BS>
-int launch(const FwdParams& fp, int64_t rows, hipStream_t stream) {
+__global__ void __launch_bounds__(2 * BS) bsa_empty_rows_kernel(FwdParams p) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int qb = (int)(row % p.Nq);
+  const int64_t bh = row / p.Nq;
+  const int hs = (int)(bh % p.n_heads), b = (int)(bh / p.n_heads);
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  merge_row<D, BS>(p, row, 0, b, h, qb, w, lane);
+}
+
+__global__ void __launch_bounds__(256) bsa_clear_arrivals_kernel(int* arrivals, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) arrivals[i] = 0;
+}
+
+template <int D, int BS>
+int launch(const FwdParams& fp, int64_t rows, bool cleared, hipStream_t stream) {
+  if (!cleared) {
+    hipLaunchKernelGGL(bsa_clear_arrivals_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream,
+                       fp.arrivals, rows);
+    const int rc = wa_launch_status("bsa_fwd_clear");
+    if (rc != WA_OK) return rc;
+  }
   hipLaunchKernelGGL((bsa_unit_kernel<D, BS>), dim3(fp.n_units), dim3(2 * BS), 0, stream, fp);
-  int rc = wa_launch_status("bsa_fwd_unit");
-  if (rc != WA_OK) return rc;
-  hipLaunchKernelGGL((bsa_combine_kernel<D, BS>), dim3((unsigned)rows), dim3(2 * BS), 0, stream, fp);
-  return wa_launch_status("bsa_fwd_combine");
+  return wa_launch_status("bsa_fwd_unit");
 }
 
 int64_t split_slots(int64_t rows, int64_t max_visits, int64_t split) {
@@ -584,7 +690,7 @@ extern "C" int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, 
                                               int64_t D) {
   if (split <= 0) split = WA_BSA_DEFAULT_SPLIT;
   const int64_t slots = split_slots(rows, max_visits, split);
-  return ((slots * block_size * (D + 1)) * 4 + 255) / 256 * 256;
+  return ((slots * block_size * (D + 1)) * 4 + 255) / 256 * 256 + (rows * 4 + 255) / 256 * 256;
 }
 
 extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
@@ -658,18 +764,22 @@ extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
   fp.v_slab_bytes = (int)v_slab;
   fp.part_o = (float*)a->workspace;
   fp.part_lse = fp.part_o + rows * max_splits * a->block_size * a->D;
+  fp.arrivals = a->arrivals ? a->arrivals
+                            : (int*)((char*)a->workspace +
+                                     (rows * max_splits * a->block_size * (a->D + 1) * 4 + 255) / 256 * 256);
+  const bool cleared = a->arrivals != nullptr;
   if (n_units == 0) fp.n_units = 0;
 
   hipStream_t s = (hipStream_t)stream;
   if (fp.n_units == 0) {
-    // nothing to visit: the combine pass still writes the (empty-row) outputs
-    hipLaunchKernelGGL((a->D == 64 ? (a->block_size == 64 ? bsa_combine_kernel<64, 64> : bsa_combine_kernel<64, 128>)
-                                   : (a->block_size == 64 ? bsa_combine_kernel<128, 64> : bsa_combine_kernel<128, 128>)),
+    // nothing to visit: every row is written as an empty row
+    hipLaunchKernelGGL((a->D == 64 ? (a->block_size == 64 ? bsa_empty_rows_kernel<64, 64> : bsa_empty_rows_kernel<64, 128>)
+                                   : (a->block_size == 64 ? bsa_empty_rows_kernel<128, 64> : bsa_empty_rows_kernel<128, 128>)),
                        dim3((unsigned)rows), dim3(2 * a->block_size), 0, s, fp);
-    return wa_launch_status("bsa_fwd_combine");
+    return wa_launch_status("bsa_fwd_empty_rows");
   }
-  if (a->D == 64 && a->block_size == 64) return launch<64, 64>(fp, rows, s);
-  if (a->D == 64 && a->block_size == 128) return launch<64, 128>(fp, rows, s);
-  if (a->D == 128 && a->block_size == 64) return launch<128, 64>(fp, rows, s);
-  return launch<128, 128>(fp, rows, s);
+  if (a->D == 64 && a->block_size == 64) return launch<64, 64>(fp, rows, cleared, s);
+  if (a->D == 64 && a->block_size == 128) return launch<64, 128>(fp, rows, cleared, s);
+  if (a->D == 128 && a->block_size == 64) return launch<128, 64>(fp, rows, cleared, s);
+  return launch<128, 128>(fp, rows, cleared, s);
 }

@@ -199,14 +199,22 @@ __global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
 // previous one, apply phi in place (each thread owns a fixed 8-channel column, so it also sums z),
 // then the same MFMAs. Rows past the chunk re-read an in-bounds row and get phi = 0, so they add
 // nothing to S or z.
-template <int D>
-__global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
-  constexpr int TC = 64, STAGES = 4;
+// Output tile (dt, et) of S^T (NT x NT tiles of 32 x 32) for the i-th of a wave's TPW tiles: waves
+// take consecutive runs of TPW tiles in row-major tile order.
+template <int NT, int TPW>
+__device__ __forceinline__ int tile_d(int w, int i) { return (w * TPW + i) / NT; }
+template <int NT, int TPW>
+__device__ __forceinline__ int tile_e(int w, int i) { return (w * TPW + i) % NT; }
+
+template <int D, int NW>
+__global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) {
+  constexpr int TC = 64, STAGES = 4, NTH = 64 * NW;
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;           // rows per wave DMA instruction
-  constexpr int NI = TC / (RPI * 4);      // DMA instructions per wave per tensor per tile
-  constexpr int UPT = TC * CPR / 256;     // chunks per thread in the phi pass
-  constexpr int NT = D / 32, TPW = NT * NT / 4;
+  constexpr int NI = TC / (RPI * NW);     // DMA instructions per wave per tensor per tile
+  constexpr int UPT = TC * CPR / NTH;     // chunks per thread in the phi pass
+  constexpr int NT = D / 32, TPW = NT * NT / NW;
+  static_assert(NI >= 1 && UPT >= 1 && TPW >= 1 && NT * NT == TPW * NW, "bad wave count");
   __shared__ __attribute__((aligned(1024))) bf16_t kb[STAGES][TC * D];
   __shared__ __attribute__((aligned(1024))) bf16_t vb[STAGES][TC * D];
 
@@ -224,7 +232,7 @@ __global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
     const int t0 = tbeg + it * TC, st = it % STAGES;
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int r0 = (i * 4 + w) * RPI;
+      const int r0 = (i * NW + w) * RPI;
       const int row = r0 + lane / CPR;
       const int src = t0 + row < tend ? t0 + row : t0;
       const int cc = (lane % CPR) ^ tr_swizzle(row);
@@ -254,7 +262,7 @@ __global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
     bf16_t* kt = kb[st];
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
-      const int r = tid / CPR + u * (256 / CPR);
+      const int r = tid / CPR + u * (NTH / CPR);
       const bool ok = t0 + r < tend;
       bf16x8* cp = (bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8));
       bf16x8 x = *cp;
@@ -271,8 +279,7 @@ __global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
     for (int c = 0; c < TC / 16; ++c) {
 #pragma unroll
       for (int i = 0; i < TPW; ++i) {
-        const int dt = D == 128 ? w : (w >> 1);
-        const int et = D == 128 ? i : (w & 1);
+        const int dt = tile_d<NT, TPW>(w, i), et = tile_e<NT, TPW>(w, i);
         const bf16x8 a = tr_frag<D>(vb[st], c, 32 * dt, lane);
         const bf16x8 bb = tr_frag<D>(kb[st], c, 32 * et, lane);
         acc[i] = wa_mfma32(a, bb, acc[i]);
@@ -284,8 +291,7 @@ __global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
   const int g = lane >> 5, l32 = lane & 31;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    const int dt = D == 128 ? w : (w >> 1);
-    const int et = D == 128 ? i : (w & 1);
+    const int dt = tile_d<NT, TPW>(w, i), et = tile_e<NT, TPW>(w, i);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int d = 32 * dt + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -293,14 +299,14 @@ __global__ void __launch_bounds__(256) elu1_state_dma_kernel(StateParams p) {
     }
   }
   __syncthreads();
-  float* zbuf = (float*)kb[0];  // [256 threads][8]
+  float* zbuf = (float*)kb[0];  // [NTH threads][8]
 #pragma unroll
   for (int e = 0; e < 8; ++e) zbuf[tid * 8 + e] = zacc[e];
   __syncthreads();
   if (tid < D) {
     const int cc = tid / 8, e = tid % 8;
     float sum = 0.f;
-    for (int r = 0; r < 256 / CPR; ++r) sum += zbuf[(r * CPR + cc) * 8 + e];
+    for (int r = 0; r < NTH / CPR; ++r) sum += zbuf[(r * CPR + cc) * 8 + e];
     part[D * D + tid] = sum;
   }
 }
@@ -310,23 +316,31 @@ __global__ void __launch_bounds__(256) elu1_reduce_kernel(StateParams p, int D) 
   const int64_t total = (int64_t)p.B * p.n_heads * per;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  // 16 loads in flight per thread, summed into 8 chains (fixed order: reproducible)
+  float a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = 0.f;
+  const float* src = p.part + i;
   int c = 0;
-  for (; c + 4 <= p.n_chunks; c += 4) {
-    a0 += p.part[(int64_t)c * total + i];
-    a1 += p.part[(int64_t)(c + 1) * total + i];
-    a2 += p.part[(int64_t)(c + 2) * total + i];
-    a3 += p.part[(int64_t)(c + 3) * total + i];
+  for (; c + 16 <= p.n_chunks; c += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = src[(int64_t)(c + j) * total];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a[j & 7] += v[j];
   }
-  for (; c < p.n_chunks; ++c) a0 += p.part[(int64_t)c * total + i];
-  const float s = (a0 + a1) + (a2 + a3);
+  for (; c < p.n_chunks; ++c) a[0] += src[(int64_t)c * total];
+  const float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   const int64_t bh = i / per, r = i % per;
   if (r < (int64_t)D * D) p.state[bh * D * D + r] = s;
   else p.zsum[bh * D + (r - (int64_t)D * D)] = s;
 }
 
 // =============================================================================================
-// readout: one workgroup per (128-query tile, head slot, batch); wave w owns 32 queries.
+// readout: one workgroup of 8 waves per (128-query tile, head slot, batch). Wave w owns 32
+// queries (w % 4) and half of the output channels (w / 4): the two halves share the staged S^T and
+// both compute phi(q) and the denominator of their queries, which halves each wave's MFMA and
+// epilogue work and puts two waves on every SIMD.
 // =============================================================================================
 struct ReadoutParams {
   const void* q; int64_t q_sb, q_st, q_sh; int q_dtype;
@@ -339,9 +353,13 @@ struct ReadoutParams {
   int gate_pre_bf16, gate_out_bf16, lin_round_bf16;
 };
 
-template <int D>
-__global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
-  constexpr int DC = D / 16, DT = D / 32, CPR = D / 8;
+// HOT != 0 fixes the HSA forward's bf16 configuration at compile time: bf16 q and o, gated
+// epilogue with gate weights, bf16 rounding of the linear output and of the gate, and of the gate
+// pre-activation for HOT = 1 only (a bf16 gate layer) but not for HOT = 2 (an fp32 one). HOT = 0
+// reads each option from the params.
+template <int D, int HOT>
+__global__ void __launch_bounds__(512) elu1_readout_kernel(ReadoutParams p) {
+  constexpr int DC = D / 16, DT = D / 32, DTW = DT / 2, CPR = D / 8;
   __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t s_w[D * D];
@@ -351,33 +369,44 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int qg = w & 3, dp = w >> 2;
   const float* S = p.state + ((int64_t)b * p.n_heads + hs) * D * D;
-  const bool use_w = p.epilogue == WA_EPI_GATED && p.gate_w;
+  const bool q_bf = HOT || p.q_dtype == WA_BF16;
+  const bool o_bf = HOT || p.o_dtype == WA_BF16;
+  const bool need_gate = HOT || p.epilogue == WA_EPI_GATED;
+  const bool use_w = HOT ? true : (need_gate && p.gate_w);
+  const bool pre_bf = HOT ? HOT == 1 : p.gate_pre_bf16;
+  const bool gout_bf = HOT || p.gate_out_bf16;
+  const bool lin_bf = HOT || p.lin_round_bf16;
 
   // Every global read of the workgroup is issued up front so the latencies overlap: this lane's
   // query row, S^T (staged as bf16 hi + lo), the gate weights, z and the gate bias (both to LDS).
-  const int qi = tile * 128 + w * 32 + l32;
+  const int qi = tile * 128 + qg * 32 + l32;
   const bool q_ok = qi < p.L;
   const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
   float qraw[DC][8];
 #pragma unroll
   for (int c = 0; c < DC; ++c) {
-    if (p.q_dtype == WA_BF16) load_row8<bf16_t>((const bf16_t*)p.q + qoff + c * 16 + g * 8, qraw[c]);
+    if (q_bf) load_row8<bf16_t>((const bf16_t*)p.q + qoff + c * 16 + g * 8, qraw[c]);
     else load_row8<float>((const float*)p.q + qoff + c * 16 + g * 8, qraw[c]);
   }
-  constexpr int SU = D * CPR / 256;  // 8-element units per thread (8 or 2)
+  constexpr int SU = D * CPR / 512;  // 8-element units per thread (4 or 1)
   f32x4 x0[SU], x1[SU];
   bf16x8 wv[SU];
 #pragma unroll
   for (int k = 0; k < SU; ++k) {
-    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    const int u = tid + 512 * k, d = u / CPR, cc = u % CPR;
     x0[k] = *(const f32x4*)(S + d * D + cc * 8);
     x1[k] = *(const f32x4*)(S + d * D + cc * 8 + 4);
     if (use_w) wv[k] = *(const bf16x8*)(p.gate_w + d * D + cc * 8);
   }
+  for (int e = tid; e < D; e += 512) {
+    s_z[e] = p.zsum[((int64_t)b * p.n_heads + hs) * D + e];
+    s_gb[e] = p.gate_b ? p.gate_b[e] : 0.f;
+  }
 #pragma unroll
   for (int k = 0; k < SU; ++k) {
-    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    const int u = tid + 512 * k, d = u / CPR, cc = u % CPR;
     bf16x8 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -391,14 +420,7 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
     *(bf16x8*)(s_lo + d * D + slot * 8) = lo;
     if (use_w) *(bf16x8*)(s_w + d * D + slot * 8) = wv[k];
   }
-  for (int e = tid; e < D; e += 256) {
-    s_z[e] = p.zsum[((int64_t)b * p.n_heads + hs) * D + e];
-    s_gb[e] = p.gate_b ? p.gate_b[e] : 0.f;
-  }
-  __syncthreads();
-
   bf16x8 qf[DC], phf[DC];
-  float den = 0.f;
 #pragma unroll
   for (int c = 0; c < DC; ++c) {
     float* f = qraw[c];
@@ -406,23 +428,30 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
     for (int e = 0; e < 8; ++e) {
       if (!q_ok) f[e] = 0.f;
       qf[c][e] = (bf16_t)f[e];
-      const float ph = wa_bf16_round(elu1f(f[e]));
-      phf[c][e] = (bf16_t)ph;
-      den = fmaf(ph, s_z[c * 16 + g * 8 + e], den);
+      phf[c][e] = (bf16_t)elu1f(f[e]);
     }
+  }
+  __syncthreads();
+  float den = 0.f;
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) den = fmaf((float)phf[c][e], s_z[c * 16 + g * 8 + e], den);
   }
   den += __shfl_xor(den, 32, 64);
 
-  // O^T[d, q] = S^T[d, :] phi(Q)^T[:, q]; A fragment: row d = 32t + l32, chunk 2c + g
-  f32x16 oacc[DT], gacc[DT];
+  // O^T[d, q] = S^T[d, :] phi(Q)^T[:, q] over this wave's channel tiles; A fragment: row
+  // d = 32 T + l32, chunk 2c + g
+  f32x16 oacc[DTW], gacc[DTW];
   const int rs = row_swizzle<D>(l32);
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
+  for (int t = 0; t < DTW; ++t) {
+    const int T = dp * DTW + t;
     oacc[t] = f32x16{};
     gacc[t] = f32x16{};
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      const int off = (32 * t + l32) * D + ((2 * c + g) ^ rs) * 8;
+      const int off = (32 * T + l32) * D + ((2 * c + g) ^ rs) * 8;
       oacc[t] = wa_mfma32(*(const bf16x8*)(s_hi + off), phf[c], oacc[t]);
       oacc[t] = wa_mfma32(*(const bf16x8*)(s_lo + off), phf[c], oacc[t]);
       if (use_w) gacc[t] = wa_mfma32(*(const bf16x8*)(s_w + off), qf[c], gacc[t]);
@@ -430,39 +459,39 @@ __global__ void __launch_bounds__(256) elu1_readout_kernel(ReadoutParams p) {
   }
   if (!q_ok) return;
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  const bool need_gate = p.epilogue == WA_EPI_GATED;
   const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh;
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
+  for (int t = 0; t < DTW; ++t) {
+    const int T = dp * DTW + t;
     // every global read of the tile (gate bias or q) before its stores (see bsa_fwd.hip)
     float pre[4][4];
     if (need_gate) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const int d0 = t * 32 + 8 * rq + 4 * g;
+        const int d0 = T * 32 + 8 * rq + 4 * g;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          pre[rq][i] = p.gate_w ? gacc[t][rq * 4 + i] + s_gb[d0 + i] : wa_load_f(p.q, qoff + d0 + i, p.q_dtype);
+          pre[rq][i] = use_w ? gacc[t][rq * 4 + i] + s_gb[d0 + i] : wa_load_f(p.q, qoff + d0 + i, p.q_dtype);
       }
     }
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      const int d0 = t * 32 + 8 * rq + 4 * g;
+      const int d0 = T * 32 + 8 * rq + 4 * g;
       float val[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float a = oacc[t][rq * 4 + i] * inv;
-        if (p.lin_round_bf16) a = wa_bf16_round(a);
+        if (lin_bf) a = wa_bf16_round(a);
         if (need_gate) {
           float pr = pre[rq][i];
-          if (p.gate_pre_bf16) pr = wa_bf16_round(pr);
+          if (pre_bf) pr = wa_bf16_round(pr);
           float gs = wa_sigmoid(pr);
-          if (p.gate_out_bf16) gs = wa_bf16_round(gs);
+          if (gout_bf) gs = wa_bf16_round(gs);
           a = __fmul_rn(a, gs);
         }
         val[i] = a;
       }
-      if (p.o_dtype == WA_BF16) {
+      if (o_bf) {
         bf16x4 ov = {(bf16_t)val[0], (bf16_t)val[1], (bf16_t)val[2], (bf16_t)val[3]};
         *(bf16x4*)((bf16_t*)p.o + oo + d0) = ov;
       } else {
@@ -919,10 +948,10 @@ extern "C" int wa_elu1_state(const wa_elu1_state_args* a, void* stream) {
   dim3 grid((unsigned)sp.n_chunks, (unsigned)nh, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
   if (a->D == 128) {
-    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<128>), grid, dim3(256), 0, s, sp);
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<128, 8>), grid, dim3(512), 0, s, sp);
     else hipLaunchKernelGGL((elu1_state_kernel<128, float>), grid, dim3(256), 0, s, sp);
   } else {
-    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<64>), grid, dim3(256), 0, s, sp);
+    if (a->dtype == WA_BF16) hipLaunchKernelGGL((elu1_state_dma_kernel<64, 4>), grid, dim3(256), 0, s, sp);
     else hipLaunchKernelGGL((elu1_state_kernel<64, float>), grid, dim3(256), 0, s, sp);
   }
   int rc = wa_launch_status("elu1_state");
@@ -952,8 +981,18 @@ extern "C" int wa_elu1_readout(const wa_elu1_readout_args* a, void* stream) {
                    (const bf16_t*)a->gate_w, a->gate_b, a->gate_pre_bf16, a->gate_out_bf16, a->lin_round_bf16};
   dim3 grid((unsigned)((a->L + 127) / 128), (unsigned)nh, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
-  if (a->D == 128) hipLaunchKernelGGL(elu1_readout_kernel<128>, grid, dim3(256), 0, s, rp);
-  else hipLaunchKernelGGL(elu1_readout_kernel<64>, grid, dim3(256), 0, s, rp);
+  const bool hot = a->q_dtype == WA_BF16 && a->o_dtype == WA_BF16 && a->epilogue == WA_EPI_GATED && a->gate_w &&
+                   a->gate_out_bf16 && a->lin_round_bf16;
+  const int mode = hot ? (a->gate_pre_bf16 ? 1 : 2) : 0;
+  if (a->D == 128) {
+    if (mode == 1) hipLaunchKernelGGL((elu1_readout_kernel<128, 1>), grid, dim3(512), 0, s, rp);
+    else if (mode == 2) hipLaunchKernelGGL((elu1_readout_kernel<128, 2>), grid, dim3(512), 0, s, rp);
+    else hipLaunchKernelGGL((elu1_readout_kernel<128, 0>), grid, dim3(512), 0, s, rp);
+  } else {
+    if (mode == 1) hipLaunchKernelGGL((elu1_readout_kernel<64, 1>), grid, dim3(512), 0, s, rp);
+    else if (mode == 2) hipLaunchKernelGGL((elu1_readout_kernel<64, 2>), grid, dim3(512), 0, s, rp);
+    else hipLaunchKernelGGL((elu1_readout_kernel<64, 0>), grid, dim3(512), 0, s, rp);
+  }
   return wa_launch_status("elu1_readout");
 }
 

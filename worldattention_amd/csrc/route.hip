@@ -89,6 +89,7 @@ struct RouteParams {
   const int32_t* heads;
   int32_t* index; int32_t* num; float* thresholds; uint8_t* mask; float* probs_out;
   float* ws_sorted; float* ws_gini;
+  int32_t* clear; int64_t n_clear;
 };
 
 __device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
@@ -114,8 +115,9 @@ __device__ __forceinline__ double block_reduce_sum_d(double v, double* scratch) 
 }
 
 // Outputs the row kernels do not produce, written by one extra workgroup (the last x index of
-// the grid, y = z = 0): num = 0 for the rows of heads outside the routed list, and thresholds = 0
-// for every head without a Gini threshold. Returns true for every workgroup of that last x index.
+// the grid, y = z = 0): num = 0 for the rows of heads outside the routed list, thresholds = 0
+// for every head without a Gini threshold, and the caller's `clear` words. Returns true for every
+// workgroup of that last x index.
 __device__ bool clear_unrouted(const RouteParams& p) {
   if (blockIdx.x != gridDim.x - 1) return false;
   if (blockIdx.y | blockIdx.z) return true;
@@ -131,6 +133,7 @@ __device__ bool clear_unrouted(const RouteParams& p) {
   if (p.heads)
     for (int64_t u = threadIdx.x; u < (int64_t)p.B * p.H * p.Nq; u += blockDim.x)
       if (!routed((int)((u / p.Nq) % p.H))) p.num[u] = 0;
+  for (int64_t u = threadIdx.x; u < p.n_clear; u += blockDim.x) p.clear[u] = 0;
   return true;
 }
 
@@ -277,7 +280,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-template <int KPL>
+template <int KPL, int DK>
 __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   constexpr int NP = 64 * KPL;
   __shared__ __attribute__((aligned(16))) float q_sh[4][256];
@@ -287,41 +290,70 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   const int i0 = blockIdx.x * 4, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;  // uniform per workgroup
-  const int N = p.Nkv, D = p.D;
+  const int N = p.Nkv, D = DK ? DK : p.D;
   const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
+  const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * D;
 
-  // 1. scores of the four rows
+  // 1. scores of the four rows. With the head dim known at compile time (and N <= 256: one key
+  // block per thread), this thread's pooled key row is loaded whole before the pooled queries are
+  // staged, so both latencies overlap.
+  f32x4 kv[DK ? DK / 4 : 1];
+  auto load_key = [&](int j) {
+    const float* kr = kbase + (int64_t)min(j, N - 1) * D;
+#pragma unroll
+    for (int c = 0; c < (DK ? DK / 4 : 1); ++c) kv[c] = *(const f32x4*)(kr + 4 * c);
+  };
+  if (DK) load_key(tid);
   for (int u = tid; u < 4 * D; u += 256) {
     const int r = u / D, d = u % D;
     q_sh[r][d] = i0 + r < p.Nq ? p.qp[(row0 + i0 + r) * D + d] : 0.f;
   }
   __syncthreads();
-  const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * D;
   for (int j = tid; j < N; j += 256) {
-    const float* kr = kbase + (int64_t)j * D;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    if ((D & 31) == 0) {
-      for (int d0 = 0; d0 < D; d0 += 32) {
-        f32x4 kv[8];
+    if (DK) {
+      // groups of four chunks: the fences keep the compiler from hoisting every LDS read of the
+      // pooled queries ahead of the products (which would not fit in registers)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) kv[c] = *(const f32x4*)(kr + d0 + 4 * c);
+      for (int c0 = 0; c0 < DK / 4; c0 += 4) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int c = c0; c < c0 + 4; ++c) {
 #pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const f32x4 qv = *(const f32x4*)(&q_sh[r][d0 + 4 * c]);
+          for (int r = 0; r < 4; ++r) {
+            const f32x4 qv = *(const f32x4*)(&q_sh[r][4 * c]);
             acc[r] = fmaf(qv[0], kv[c][0], acc[r]);
             acc[r] = fmaf(qv[1], kv[c][1], acc[r]);
             acc[r] = fmaf(qv[2], kv[c][2], acc[r]);
             acc[r] = fmaf(qv[3], kv[c][3], acc[r]);
           }
         }
+        asm volatile("" ::: "memory");
       }
     } else {
-      for (int d = 0; d < D; ++d) {
-        const float kd = kr[d];
+      const float* kr = kbase + (int64_t)j * D;
+      if ((D & 31) == 0) {
+        for (int d0 = 0; d0 < D; d0 += 32) {
+          f32x4 kc[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
+          for (int c = 0; c < 8; ++c) kc[c] = *(const f32x4*)(kr + d0 + 4 * c);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+              const f32x4 qv = *(const f32x4*)(&q_sh[r][d0 + 4 * c]);
+              acc[r] = fmaf(qv[0], kc[c][0], acc[r]);
+              acc[r] = fmaf(qv[1], kc[c][1], acc[r]);
+              acc[r] = fmaf(qv[2], kc[c][2], acc[r]);
+              acc[r] = fmaf(qv[3], kc[c][3], acc[r]);
+            }
+          }
+        }
+      } else {
+        for (int d = 0; d < D; ++d) {
+          const float kd = kr[d];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
+        }
       }
     }
 #pragma unroll
@@ -544,6 +576,8 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.head_k = a->head_k; rp.heads = a->heads; rp.n_heads = (int)nh;
   rp.index = a->index; rp.num = a->num; rp.thresholds = a->thresholds; rp.mask = a->mask;
   rp.probs_out = a->probs_out;
+  WA_CHECK_ARG(a->n_clear >= 0 && (a->n_clear == 0 || a->clear), "wa_route: clear is NULL with n_clear > 0");
+  rp.clear = a->clear; rp.n_clear = a->n_clear;
   const int64_t rows = a->B * a->H * a->Nq;
   rp.ws_sorted = (float*)a->workspace;
   rp.ws_gini = a->workspace ? (float*)a->workspace + rows * a->Nkv : nullptr;
@@ -551,10 +585,16 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a->mode == WA_ROUTE_TOPK && !a->probs && !a->probs_out && a->Nkv <= 512) {
     const dim3 wgrid((unsigned)((a->Nq + 3) / 4) + 1, (unsigned)nh, (unsigned)a->B);
-    if (a->Nkv <= 64) hipLaunchKernelGGL(route_wave_kernel<1>, wgrid, dim3(256), 0, s, rp);
-    else if (a->Nkv <= 128) hipLaunchKernelGGL(route_wave_kernel<2>, wgrid, dim3(256), 0, s, rp);
-    else if (a->Nkv <= 256) hipLaunchKernelGGL(route_wave_kernel<4>, wgrid, dim3(256), 0, s, rp);
-    else hipLaunchKernelGGL(route_wave_kernel<8>, wgrid, dim3(256), 0, s, rp);
+    if (a->D == 128 && a->Nkv <= 256) {
+      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 128>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 128>), wgrid, dim3(256), 0, s, rp);
+      else hipLaunchKernelGGL((route_wave_kernel<4, 128>), wgrid, dim3(256), 0, s, rp);
+    } else {
+      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 0>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 0>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 256) hipLaunchKernelGGL((route_wave_kernel<4, 0>), wgrid, dim3(256), 0, s, rp);
+      else hipLaunchKernelGGL((route_wave_kernel<8, 0>), wgrid, dim3(256), 0, s, rp);
+    }
     return wa_launch_status("route_wave");
   }
   hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);

@@ -287,29 +287,40 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     out = torch.empty((bsz, q_len, heads, head_dim), dtype=comp_dtype, device=dev)
     lin_tmp = torch.empty_like(out) if plan.both else None
 
-    # ---- linear branch -------------------------------------------------------------------
     # With both branches present the linear branch runs on a side stream, concurrently with
     # routing and the sparse branch on the caller's stream; the two write disjoint heads of `out`
-    # (or `lin_tmp`, joined before the fused sparse epilogue reads it).
+    # (or `lin_tmp`, joined before the fused sparse epilogue reads it). The side stream forks from
+    # the start of the call, but its kernels are issued after the block pooling: the caller's
+    # stream gets its first kernels first.
     main = torch.cuda.current_stream(dev)
     side = _branch_stream(dev) if plan.linear and plan.sparse else None
     if side is not None:
         side.wait_stream(main)
-    with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
-        _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat,
-                          proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save)
 
-    # ---- sparse branch -------------------------------------------------------------------
+    # ---- sparse branch: block pooling -----------------------------------------------------
     if plan.sparse:
         _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
         sp_t = plan.t["sparse"]
         qp = pool_blhd(q, q_len, nq, block_size, heads=sp_t)
         kp = pool_blhd(k, kv_len, nkv, block_size, heads=sp_t)
+
+    # ---- linear branch -------------------------------------------------------------------
+    with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
+        _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat,
+                          proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save)
+
+    # ---- sparse branch: routing and attention ----------------------------------------------
+    if plan.sparse:
+        # the routing launch also zeroes the arrival counters of the attention launches below
+        n_only = len(plan.sparse_only) if plan.sparse_only else 0
+        rows_only, rows_both = bsz * n_only * nq, bsz * (len(plan.both) if plan.both else 0) * nq
+        arrivals = torch.empty((rows_only + rows_both,), dtype=torch.int32, device=dev)
         if routing == "gini":
-            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t)
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t,
+                              clear=arrivals)
         else:
             ks = _per_head_k(topk, heads)
-            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t)
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t, clear=arrivals)
         if save is not None:
             save.update(route=route)
         # top-k routing fixes every row's visit count on the host: launch exactly those units
@@ -317,13 +328,14 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
         if plan.sparse_only:
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
                         heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True,
-                        visits=vis_of(plan.sparse_only))
+                        visits=vis_of(plan.sparse_only), arrivals=arrivals[:rows_only])
         if plan.both:
             if side is not None:
                 main.wait_stream(side)
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
                         heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
-                        x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), **gate.kwargs())
+                        x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), arrivals=arrivals[rows_only:],
+                        **gate.kwargs())
     if side is not None:
         main.wait_stream(side)
     return out if out.dtype == out_dtype else out.to(out_dtype)

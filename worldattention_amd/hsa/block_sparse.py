@@ -41,7 +41,8 @@ _UNIT_CACHE: dict = {}
 def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[torch.Tensor, int]:
     """Device ``[n, 2]`` int32 list of (row, split) units when every row's visit count is known on
     the host (top-k routing: ``num = min(k_h, Nkv)``), ordered head by head so that consecutive
-    units — which the kernel places on the same XCD — share key blocks. Cached per shape."""
+    units — which the kernel places on the same XCD — share key blocks. A row with no visits gets
+    its split-0 unit, which writes the empty row. Cached per shape."""
     key = (str(device), bsz, tuple(visits_per_slot), nq, split)
     hit = _UNIT_CACHE.get(key)
     if hit is None:
@@ -49,7 +50,7 @@ def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[
         n_slots = len(visits_per_slot)
         for b in range(bsz):
             for hs, nv in enumerate(visits_per_slot):
-                ns = -(-int(nv) // split) if nv > 0 else 0
+                ns = -(-int(nv) // split) if nv > 0 else 1
                 for qb in range(nq):
                     row = (b * n_slots + hs) * nq + qb
                     units.extend((row, sp) for sp in range(ns))
@@ -62,12 +63,14 @@ def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[
 def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=None, heads=None,
                 out=None, out_dtype=None, want_lse=False, epilogue=_lib.WA_EPI_PLAIN, x=None, gate_w=None,
                 gate_b=None, gate_pre_bf16=False, gate_out_bf16=False, attn_round_bf16=False, lq=None,
-                lkv=None, visits=None, split=None):
+                lkv=None, visits=None, split=None, arrivals=None):
     """Launch ``wa_bsa_fwd`` on bf16 q/k/v in ``layout`` ("bhld" = [B, H, L, D], "blhd" = [B, L, H, D]).
 
     ``index=None`` attends densely to every key block. ``visits`` (optional) gives each launched
     head's exact visit count ``min(num, width)`` when the host knows it (top-k routing): the launch
-    then covers exactly the needed (row, split) units. Returns ``(out, lse)``.
+    then covers exactly the needed (row, split) units. ``arrivals`` (optional): an int32 tensor of
+    at least ``B * n_heads * ceil(lq / block_size)`` zeros (left zero), which spares the launch
+    clearing its own. Returns ``(out, lse)``.
     """
     dev = _lib.require_gpu(q, k, v)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -105,6 +108,9 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         units, n_units = unit_table(bsz, vis, nq, split, dev)
         max_visits = max(max(vis), 1)
     rows = bsz * n_slots * nq
+    if arrivals is not None and (arrivals.dtype != torch.int32 or arrivals.numel() < rows
+                                 or not arrivals.is_contiguous() or arrivals.device != dev):
+        raise ValueError(f"arrivals must be a contiguous int32 tensor of >= {rows} elements on {dev}")
     ws_bytes = _lib.lib().wa_bsa_fwd_workspace_bytes(rows, max_visits, split, block_size, d)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     args = _lib.BsaFwdArgs(
@@ -115,7 +121,7 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
         xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
         int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16),
-        ws.data_ptr(), _lib.ptr(units), n_units, max_visits, split)
+        ws.data_ptr(), _lib.ptr(units), n_units, max_visits, split, _lib.ptr(arrivals))
     _lib.call("wa_bsa_fwd", args, _lib.stream_ptr(dev))
     return out, lse
 

@@ -115,7 +115,9 @@ def block_mean_pool(x: torch.Tensor, logical_len: int, num_blocks: int, block_si
 
 
 def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=None,
-           return_mask=False, want_probs=False):
+           return_mask=False, want_probs=False, clear=None):
+    """``clear`` (optional): a contiguous int32 device tensor the launch zeroes (the arrivals of
+    the block-sparse launch that follows)."""
     src = probs if probs is not None else qp
     dev = _lib.require_gpu(src, kp)
     if probs is not None:
@@ -145,7 +147,8 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
     args = _lib.RouteArgs(_lib.ptr(probs), _lib.ptr(qp), _lib.ptr(kp), bsz, nheads, nq, nkv, d, mode,
                           float(tau_min), float(tau_max - tau_min), _lib.ptr(head_k_t), _lib.ptr(heads),
                           0 if heads is None else heads.numel(), index.data_ptr(), num.data_ptr(),
-                          thresholds.data_ptr(), _lib.ptr(mask), _lib.ptr(probs_out), _lib.ptr(ws))
+                          thresholds.data_ptr(), _lib.ptr(mask), _lib.ptr(probs_out), _lib.ptr(ws),
+                          _lib.ptr(clear), 0 if clear is None else clear.numel())
     _lib.call("wa_route", args, _lib.stream_ptr(dev))
     return BlockRouting(index=index, num=num, mask=mask, thresholds=thresholds), probs_out
 
