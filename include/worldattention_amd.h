@@ -54,6 +54,10 @@ typedef struct wa_pool_args {
   int32_t emulate_rounding;
 } wa_pool_args;
 int wa_block_mean_pool(const wa_pool_args* args, void* stream);
+/* Several pooling jobs (e.g. the query and key tensors of one routing call) with as few launches
+ * as possible: jobs of one kernel variant (dtype, 16-byte alignment) share a launch. No reference
+ * counterpart: the reference pools q and k with two calls (routing.py:45-61, attention.py:212-213). */
+int wa_block_mean_pool_n(const wa_pool_args* jobs, int32_t n_jobs, void* stream);
 
 /* Block routing for one call: the block attention map softmax(qp kp^T / sqrt(D)) (or a given
  * map), the stable descending permutation of every row, and the selected count per row.

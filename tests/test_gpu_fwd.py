@@ -45,6 +45,22 @@ def test_block_mean_pool_matches_oracle(dtype, logical):
         assert torch.allclose(got.cpu(), want, atol=1e-5, rtol=1e-5)
 
 
+def test_pooling_jobs_in_one_launch_equal_separate_launches():
+    """wa_block_mean_pool_n (query + key tensors of one call, plus an fp32 job that needs its own
+    launch) writes exactly what one wa_block_mean_pool call per tensor writes."""
+    from worldattention_amd.hsa.routing import pool_blhd, pool_blhd_many
+    torch.manual_seed(3)
+    heads = torch.tensor([4, 0, 2], dtype=torch.int32, device=DEV)
+    q = torch.randn(2, 300, 5, 128, device=DEV).bfloat16()
+    k = torch.randn(2, 1000, 5, 128, device=DEV).bfloat16()
+    x = torch.randn(2, 256, 5, 64, device=DEV)
+    jobs = [(q, 300, 3), (k, 1000, 8), (x, 256, 2)]
+    got = pool_blhd_many(jobs, 128, heads=heads)
+    for (t, n, nb), g in zip(jobs, got):
+        want = pool_blhd(t, n, nb, 128, heads=heads)
+        assert torch.equal(g[:, heads.long()], want[:, heads.long()])
+
+
 def test_gini_routing_is_bit_exact_on_reference_golden_maps():
     for c in torch.load(os.path.join(GOLDEN, "routing_gini.pt"), weights_only=True):
         r = W.build_block_routing(c["block_attn"].to(DEV), c["tau_min"], c["tau_max"], return_mask=True)

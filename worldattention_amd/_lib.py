@@ -181,6 +181,7 @@ SIGNATURES = {
     "wa_version": (c_int, []),
     "wa_last_error": (c_char_p, []),
     "wa_block_mean_pool": (c_int, [POINTER(PoolArgs), c_void_p]),
+    "wa_block_mean_pool_n": (c_int, [POINTER(PoolArgs), c_int32, c_void_p]),
     "wa_route_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_route": (c_int, [POINTER(RouteArgs), c_void_p]),
     "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),

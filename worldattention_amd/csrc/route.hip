@@ -2,6 +2,8 @@
 // selection (Gini cumulative mass or per-head top-k), and mask -> index compaction.
 //
 // Reference semantics: wan/modules/hsa/routing.py:45-118 and block_sparse_triton.py:20-57.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -16,14 +18,29 @@ struct PoolParams {
   const int32_t* heads;
   float* out;
   int emulate;
+  int nh;  // head slots (heads listed, or H)
+};
+
+// Several pooling jobs (e.g. the query and key tensors of one call) in one launch: job j takes
+// workgroups [start[j], start[j + 1]) of a 1-D grid.
+constexpr int POOL_MAX_JOBS = 4;
+struct PoolJobs {
+  PoolParams job[POOL_MAX_JOBS];
+  int64_t start[POOL_MAX_JOBS + 1];
+  int n;
 };
 
 template <typename T, int VEC>
-__global__ void __launch_bounds__(256) pool_kernel(PoolParams p) {
+__global__ void __launch_bounds__(256) pool_kernel(PoolJobs pj) {
   extern __shared__ float red[];  // [rows_per_pass][D + 4]
+  const int64_t id = blockIdx.x;
+  int j = 0;
+  while (j + 1 < pj.n && id >= pj.start[j + 1]) ++j;
+  const PoolParams& p = pj.job[j];
   // consecutive workgroups take the heads of one token block: they read neighbouring chunks of the
   // same token rows
-  const int hs = blockIdx.x, blk = blockIdx.y, b = blockIdx.z;
+  const int64_t local = id - pj.start[j];
+  const int hs = (int)(local % p.nh), blk = (int)((local / p.nh) % p.N), b = (int)(local / ((int64_t)p.nh * p.N));
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tpr = p.D / VEC;             // threads per token row
@@ -506,7 +523,20 @@ __global__ void __launch_bounds__(64) map_to_index_kernel(const uint8_t* mask, i
 
 }  // namespace
 
-extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
+namespace {
+
+// Kernel variant of a job: 0 bf16 x8, 1 bf16 x1, 2 fp32 x4, 3 fp32 x1 (-1: invalid job).
+int pool_variant(const wa_pool_args* a) {
+  const bool vec_ok = wa_aligned16(a->x);
+  if (a->x_dtype == WA_BF16) {
+    if (vec_ok && a->D % 8 == 0 && a->x_sb % 8 == 0 && a->x_st % 8 == 0 && a->x_sh % 8 == 0 && a->D / 8 <= 256) return 0;
+    return a->D <= 256 ? 1 : -1;
+  }
+  if (vec_ok && a->D % 4 == 0 && a->x_sb % 4 == 0 && a->x_st % 4 == 0 && a->x_sh % 4 == 0 && a->D / 4 <= 256) return 2;
+  return a->D <= 256 ? 3 : -1;
+}
+
+int pool_check(const wa_pool_args* a) {
   WA_CHECK_ARG(a && a->x && a->out, "wa_block_mean_pool: null argument");
   WA_CHECK_ARG(a->x_dtype == WA_F32 || a->x_dtype == WA_BF16, "wa_block_mean_pool: bad dtype");
   WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->D > 0 && a->D <= 1024 && a->block_size > 0 && a->num_blocks >= 0,
@@ -514,36 +544,74 @@ extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
   WA_CHECK_ARG(a->L <= a->num_blocks * a->block_size && a->L > (a->num_blocks - 1) * a->block_size,
                "wa_block_mean_pool: L=%lld does not fill %lld blocks of %lld", (long long)a->L,
                (long long)a->num_blocks, (long long)a->block_size);
-  const int64_t nh = a->heads ? a->n_heads : a->H;
-  if (a->B == 0 || nh == 0 || a->num_blocks == 0) return WA_OK;
-  PoolParams pp{a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype, (int)a->L, (int)a->H, (int)a->D,
-                (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding};
-  WA_CHECK_ARG(a->num_blocks <= 65535, "wa_block_mean_pool: more than 65535 blocks");
-  dim3 grid((unsigned)nh, (unsigned)a->num_blocks, (unsigned)a->B);
-  hipStream_t s = (hipStream_t)stream;
-  const bool vec_ok = wa_aligned16(a->x);
-  if (a->x_dtype == WA_BF16) {
-    const bool v8 = vec_ok && a->D % 8 == 0 && a->x_sb % 8 == 0 && a->x_st % 8 == 0 && a->x_sh % 8 == 0 && a->D / 8 <= 256;
-    if (v8) {
-      const int rpp = 256 / (int)(a->D / 8);
-      hipLaunchKernelGGL((pool_kernel<bf16_t, 8>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
-    } else {
-      WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned bf16 input needs D <= 256");
-      const int rpp = 256 / (int)a->D;
-      hipLaunchKernelGGL((pool_kernel<bf16_t, 1>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
-    }
-  } else {
-    const bool v4 = vec_ok && a->D % 4 == 0 && a->x_sb % 4 == 0 && a->x_st % 4 == 0 && a->x_sh % 4 == 0 && a->D / 4 <= 256;
-    if (v4) {
-      const int rpp = 256 / (int)(a->D / 4);
-      hipLaunchKernelGGL((pool_kernel<float, 4>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
-    } else {
-      WA_CHECK_ARG(a->D <= 256, "wa_block_mean_pool: unaligned fp32 input needs D <= 256");
-      const int rpp = 256 / (int)a->D;
-      hipLaunchKernelGGL((pool_kernel<float, 1>), grid, dim3(256), rpp * (a->D + 4) * sizeof(float), s, pp);
-    }
+  WA_CHECK_ARG(pool_variant(a) >= 0, "wa_block_mean_pool: an unaligned input needs D <= 256");
+  return WA_OK;
+}
+
+// One launch over jobs that share a kernel variant.
+int pool_launch(const wa_pool_args* const* jobs, int n, int variant, hipStream_t s) {
+  PoolJobs pj{};
+  int64_t total = 0;
+  size_t lds = 0;
+  pj.n = 0;
+  for (int i = 0; i < n; ++i) {
+    const wa_pool_args* a = jobs[i];
+    const int64_t nh = a->heads ? a->n_heads : a->H;
+    if (a->B == 0 || nh == 0 || a->num_blocks == 0) continue;
+    pj.job[pj.n] = PoolParams{a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype, (int)a->L, (int)a->H, (int)a->D,
+                              (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding, (int)nh};
+    pj.start[pj.n] = total;
+    total += nh * a->num_blocks * a->B;
+    const int vec = variant == 0 ? 8 : variant == 2 ? 4 : 1;
+    const int rpp = 256 / (int)(a->D / vec);
+    lds = std::max(lds, (size_t)rpp * (a->D + 4) * sizeof(float));
+    ++pj.n;
+  }
+  if (pj.n == 0) return WA_OK;
+  pj.start[pj.n] = total;
+  WA_CHECK_ARG(total < ((int64_t)1 << 31), "wa_block_mean_pool: too many blocks for one launch");
+  const dim3 grid((unsigned)total);
+  switch (variant) {
+    case 0: hipLaunchKernelGGL((pool_kernel<bf16_t, 8>), grid, dim3(256), lds, s, pj); break;
+    case 1: hipLaunchKernelGGL((pool_kernel<bf16_t, 1>), grid, dim3(256), lds, s, pj); break;
+    case 2: hipLaunchKernelGGL((pool_kernel<float, 4>), grid, dim3(256), lds, s, pj); break;
+    default: hipLaunchKernelGGL((pool_kernel<float, 1>), grid, dim3(256), lds, s, pj); break;
   }
   return wa_launch_status("block_mean_pool");
+}
+
+}  // namespace
+
+extern "C" int wa_block_mean_pool(const wa_pool_args* a, void* stream) {
+  const int rc = pool_check(a);
+  if (rc != WA_OK) return rc;
+  return pool_launch(&a, 1, pool_variant(a), (hipStream_t)stream);
+}
+
+extern "C" int wa_block_mean_pool_n(const wa_pool_args* jobs, int32_t n_jobs, void* stream) {
+  WA_CHECK_ARG(jobs && n_jobs >= 0, "wa_block_mean_pool_n: bad job list");
+  for (int i = 0; i < n_jobs; ++i) {
+    const int rc = pool_check(&jobs[i]);
+    if (rc != WA_OK) return rc;
+  }
+  // jobs of one kernel variant share a launch (up to POOL_MAX_JOBS at a time)
+  bool done[64] = {};
+  WA_CHECK_ARG(n_jobs <= 64, "wa_block_mean_pool_n: at most 64 jobs");
+  for (int i = 0; i < n_jobs; ++i) {
+    if (done[i]) continue;
+    const int v = pool_variant(&jobs[i]);
+    const wa_pool_args* group[POOL_MAX_JOBS];
+    int g = 0;
+    for (int k = i; k < n_jobs && g < POOL_MAX_JOBS; ++k) {
+      if (!done[k] && pool_variant(&jobs[k]) == v) {
+        group[g++] = &jobs[k];
+        done[k] = true;
+      }
+    }
+    const int rc = pool_launch(group, g, v, (hipStream_t)stream);
+    if (rc != WA_OK) return rc;
+  }
+  return WA_OK;
 }
 
 static int64_t next_pow2(int64_t n) {

@@ -30,7 +30,7 @@ import torch.nn as nn
 from .. import _lib
 from . import distill
 from .block_sparse import bsa_forward
-from .routing import _route, block_counts, pool_blhd
+from .routing import _route, block_counts, pool_blhd_many
 
 __all__ = [
     "HSAAttention",
@@ -289,25 +289,23 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
 
     # With both branches present the linear branch runs on a side stream, concurrently with
     # routing and the sparse branch on the caller's stream; the two write disjoint heads of `out`
-    # (or `lin_tmp`, joined before the fused sparse epilogue reads it). The side stream forks from
-    # the start of the call, but its kernels are issued after the block pooling: the caller's
-    # stream gets its first kernels first.
+    # (or `lin_tmp`, joined before the fused sparse epilogue reads it). Its kernels are issued
+    # first (measured: 3 us per call faster in graph replay than issuing the pooling first).
     main = torch.cuda.current_stream(dev)
     side = _branch_stream(dev) if plan.linear and plan.sparse else None
     if side is not None:
         side.wait_stream(main)
 
-    # ---- sparse branch: block pooling -----------------------------------------------------
-    if plan.sparse:
-        _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
-        sp_t = plan.t["sparse"]
-        qp = pool_blhd(q, q_len, nq, block_size, heads=sp_t)
-        kp = pool_blhd(k, kv_len, nkv, block_size, heads=sp_t)
-
     # ---- linear branch -------------------------------------------------------------------
     with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
         _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat,
                           proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save)
+
+    # ---- sparse branch: block pooling -----------------------------------------------------
+    if plan.sparse:
+        _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+        sp_t = plan.t["sparse"]
+        qp, kp = pool_blhd_many([(q, q_len, nq), (k, kv_len, nkv)], block_size, heads=sp_t)
 
     # ---- sparse branch: routing and attention ----------------------------------------------
     if plan.sparse:

@@ -91,6 +91,29 @@ def pool_blhd(x: torch.Tensor, logical_len: int, num_blocks: int, block_size: in
     return out
 
 
+def pool_blhd_many(jobs, block_size: int, heads: Optional[torch.Tensor] = None, emulate: bool = True):
+    """:func:`pool_blhd` of several ``(x, logical_len, num_blocks)`` jobs in as few launches as
+    possible (one for tensors of one dtype and alignment); returns their outputs in order."""
+    if not jobs:
+        return []
+    dev = _lib.require_gpu(*(x for x, _, _ in jobs))
+    outs, keep = [], []
+    arr = (_lib.PoolArgs * len(jobs))()
+    for i, (x, logical_len, num_blocks) in enumerate(jobs):
+        x = x if x.dtype in (torch.float32, torch.bfloat16) else x.float()
+        if x.stride(-1) != 1:
+            x = x.contiguous()
+        b, _, h, d = x.shape
+        out = torch.empty((b, h, num_blocks, d), dtype=torch.float32, device=dev)
+        p, sb, st, sh = _lib.blhd(x)
+        arr[i] = _lib.PoolArgs(p, sb, st, sh, _lib.dtype_code(x), b, logical_len, h, d, block_size, num_blocks,
+                               _lib.ptr(heads), 0 if heads is None else heads.numel(), out.data_ptr(), int(emulate))
+        outs.append(out)
+        keep.append(x)
+    _lib.call("wa_block_mean_pool_n", arr, len(jobs), _lib.stream_ptr(dev))
+    return outs
+
+
 def block_mean_pool(x: torch.Tensor, logical_len: int, num_blocks: int, block_size: int) -> torch.Tensor:
     """Mean-pool ``[B, H, num_blocks*block_size, D]`` into ``[B, H, num_blocks, D]``.
 
