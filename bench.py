@@ -66,7 +66,7 @@ def copy_calibration(dev) -> None:
 
 
 def measured_traffic():
-    """HBM bytes per launch of the sparse pair from the committed counter summary (FETCH_SIZE and
+    """HBM bytes per launch of the sparse kernel from the committed counter summary (FETCH_SIZE and
     WRITE_SIZE runs scaled by a plain-copy calibration), or None when it is absent."""
     path = os.path.join(ROOT, "profiles", "bsa_fwd_cfg2_traffic.md")
     try:
