@@ -8,7 +8,9 @@ seeded synthetic inputs already resident in HBM: B=1, H=12 (8 sparse heads with 
 {8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16. The timed steps replay
 the call captured once in a HIP graph (the eager per-call time is reported beside it). ``value`` is
 the effective sparse TFLOP/s of the whole call (useful sparse FLOP / call time); ``roofline`` is the
-sparse kernel's own rate, timed with HIP events on the stream it runs on.
+sparse kernel's own rate, timed with HIP events on the stream it runs on. ``hbm_bound_launches``
+gives the HBM rate of the memory-bound launches of the same call (Q/K block pooling, elu1 state,
+elu1 readout), each timed alone.
 
 Also on the same line:
 * ``hkv`` (cfg 3): page-summary HBM GB/s over the 120-frame history, selection time, the pinned
@@ -198,8 +200,56 @@ def bench_cfg2(args, dev):
     achieved = useful_flop / (sparse_ms * 1e-3) / 1e12
     log(f"cfg2: {ms_per_step:.4f} ms/call (graph replay; eager {eager_ms:.4f}), sparse kernel {sparse_ms:.4f} ms = "
         f"{achieved:.1f} TFLOP/s")
+    hbm = memory_legs(cfg, plan, route, gate, dev, max(args.steps, 20))
     return cfg, proj, dict(ms_per_step=ms_per_step, eager_ms=eager_ms, useful_flop=useful_flop, tile_flop=tile_flop,
-                           sparse_ms=sparse_ms, achieved=achieved)
+                           sparse_ms=sparse_ms, achieved=achieved, hbm=hbm)
+
+
+def memory_legs(cfg, plan, route, gate, dev, iters):
+    """HBM rates of the memory-bound launches of one cfg 2 call, each timed alone with HIP events:
+    the block pooling of the routed heads' Q and K (one launch), the elu1 state pass over the
+    linear heads' K and V (state + chunk reduce), and the gated elu1 readout. Bytes are the
+    algorithmic ones: every input element read once, every output element written once."""
+    from worldattention_amd.hsa import attention as WA
+    from worldattention_amd.hsa.routing import pool_blhd_many
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    bs = cfg["block_size"]
+    b, lq, h, d = q.shape
+    lkv = k.shape[1]
+    nq, nkv = -(-lq // bs), -(-lkv // bs)
+    sp_t, lin_t = plan.t["sparse"], plan.t["linear_only"]
+    n_sp, n_lin = sp_t.numel(), lin_t.numel()
+
+    def pool():
+        pool_blhd_many([(q, lq, nq), (k, lkv, nkv)], bs, heads=sp_t)
+
+    state_out = {}
+
+    def state():
+        state_out["s"] = WA.elu1_state(k, v, lin_t)
+
+    out = torch.empty_like(q)
+
+    spec = WA.GateSpec(gate, v.dtype)  # what hsa_forward passes for this call's gate
+
+    def readout():
+        s, z = state_out["s"]
+        WA.elu1_readout(q, s, z, lin_t, out, epilogue=WA._lib.WA_EPI_GATED, lin_round_bf16=True, **spec.kwargs())
+
+    legs = {}
+    for name, fn, nbytes in (
+            ("pool_q_k", pool, (lq + lkv) * n_sp * d * 2 + (nq + nkv) * n_sp * d * 4),
+            ("elu1_state", state, 2 * lkv * n_lin * d * 2 + n_lin * (d * d + d) * 4),
+            ("elu1_readout", readout, 2 * lq * n_lin * d * 2 + n_lin * (d * d + d) * 4)):
+        for _ in range(3):
+            fn()
+        ms = stream_time_ms(fn, iters)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        legs[name] = {"ms": round(ms, 4), "bytes": int(nbytes), "gb_s": round(gbs, 1),
+                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    log("cfg2 memory-bound launches: " + ", ".join(f"{n} {x['gb_s']:.0f} GB/s ({x['ms'] * 1e3:.1f} us)"
+                                                  for n, x in legs.items()))
+    return legs
 
 
 # ---------------------------------------------------------------------------------------------
@@ -547,6 +597,7 @@ def main():
         "sparse_useful_gflop": round(c2["useful_flop"] / 1e9, 3),
         "sparse_tile_gflop": round(c2["tile_flop"] / 1e9, 3),
         "pct_mfma_peak_sparse": round(100 * achieved / MFMA_BF16_PEAK_TFLOPS, 2),
+        "hbm_bound_launches": c2["hbm"],
         "roofline": {"bound": "mfma", "kernel": "bsa_unit_kernel<128,128>",
                      "achieved": round(achieved, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic()},

@@ -195,7 +195,9 @@ __global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
 
 // bf16 K / V: raw [64 token][D] tiles stream global -> LDS by direct-to-LDS loads into a 4-stage
 // ring, so three tiles are in flight while one is processed (the register-staged kernel above
-// keeps one). Per tile: wait for it, issue the tile three ahead into the stage freed by the
+// keeps one). The loads are inline assembly that the compiler does not track: through the builtin
+// it made the first LDS read of every tile wait for all loads in flight (s_waitcnt vmcnt(0)),
+// which drained the ring each step; the waits below count the loads instead. Per tile: wait for it, issue the tile three ahead into the stage freed by the
 // previous one, apply phi in place (each thread owns a fixed 8-channel column, so it also sums z),
 // then the same MFMAs. Rows past the chunk re-read an in-bounds row and get phi = 0, so they add
 // nothing to S or z.
@@ -236,10 +238,8 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
       const int row = r0 + lane / CPR;
       const int src = t0 + row < tend ? t0 + row : t0;
       const int cc = (lane % CPR) ^ tr_swizzle(row);
-      __builtin_amdgcn_global_load_lds((const void*)(kbase + (int64_t)src * p.k_st + cc * 8),
-                                       WA_LDS_PTR(&kb[st][r0 * D]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vbase + (int64_t)src * p.v_st + cc * 8),
-                                       WA_LDS_PTR(&vb[st][r0 * D]), 16, 0, 0);
+      lds_dma16_global(kbase + (int64_t)src * p.k_st + cc * 8, &kb[st][r0 * D]);
+      lds_dma16_global(vbase + (int64_t)src * p.v_st + cc * 8, &vb[st][r0 * D]);
     }
   };
 
@@ -299,7 +299,8 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
     }
   }
   __syncthreads();
-  float* zbuf = (float*)kb[0];  // [NTH threads][8]
+  static_assert(NTH * 8 * 4 <= STAGES * TC * D * 2, "z staging exceeds the K ring");
+  float* zbuf = (float*)kb[0];  // [NTH threads][8], over the drained K ring
 #pragma unroll
   for (int e = 0; e < 8; ++e) zbuf[tid * 8 + e] = zacc[e];
   __syncthreads();

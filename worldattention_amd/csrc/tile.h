@@ -31,6 +31,11 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, void* lds, 
   const unsigned m0 = (unsigned)(size_t)WA_LDS_PTR(lds);
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
 }
+// The same from a 64-bit per-lane global address (no buffer descriptor, no 32-bit offset limit).
+__device__ __forceinline__ void lds_dma16_global(const void* src, void* lds) {
+  const unsigned m0 = (unsigned)(size_t)WA_LDS_PTR(lds);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
 // The same with device-scope coherence (sc1): reads data another XCD wrote with sc1 stores.
 __device__ __forceinline__ void lds_dma16_sc1(__amdgpu_buffer_rsrc_t rs, void* lds, int voff) {
   const unsigned m0 = (unsigned)(size_t)WA_LDS_PTR(lds);
