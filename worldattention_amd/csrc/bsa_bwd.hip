@@ -71,6 +71,58 @@ __device__ __forceinline__ float load_any(const void* base, int64_t i, int dtype
 // ---------------------------------------------------------------------------------------------
 // pre: 16 threads per query row (8 channels each).
 // ---------------------------------------------------------------------------------------------
+// O and dO rows loaded 8 elements at a time (16-byte aligned rows; the host checks, and otherwise
+// launches bwd_pre_kernel, which loads element by element).
+template <typename T>
+__device__ __forceinline__ void load8(const void* base, int64_t i, float (&f)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const bf16x8 v = *(const bf16x8*)((const bf16_t*)base + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
+  } else {
+    const f32x4 a = *(const f32x4*)((const float*)base + i), c = *(const f32x4*)((const float*)base + i + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = a[e];
+      f[e + 4] = c[e];
+    }
+  }
+}
+
+template <int D, typename OT, typename DTY>
+__global__ void __launch_bounds__(256) bwd_pre_vec_kernel(BwdParams p) {
+  constexpr int TPR = D / 8;
+  const int hs = blockIdx.y, b = blockIdx.z;
+  const int h = head_of(p, hs);
+  if (h < 0 || h >= p.H) return;
+  const int qi = blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
+  const int c0 = (threadIdx.x % TPR) * 8;
+  float s = 0.f;
+  float l = 0.f;
+  if (qi < p.Lq) {
+    const int64_t oo = (int64_t)b * p.o_sb + (int64_t)qi * p.o_st + (int64_t)h * p.o_sh + c0;
+    const int64_t dd = (int64_t)b * p.d_sb + (int64_t)qi * p.d_st + (int64_t)h * p.d_sh + c0;
+    float ov[8], dv[8];
+    load8<OT>(p.o, oo, ov);
+    load8<DTY>(p.dout, dd, dv);
+    if (threadIdx.x % TPR == 0) l = p.lse[((int64_t)b * p.H + h) * p.Lq + qi];
+    bf16x8 db;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s = fmaf(ov[e], dv[e], s);
+      db[e] = (bf16_t)dv[e];
+    }
+    *(bf16x8*)(p.dob + (((int64_t)b * p.n_heads + hs) * p.Lq + qi) * D + c0) = db;
+  }
+#pragma unroll
+  for (int m = TPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if (qi < p.Lq && threadIdx.x % TPR == 0) {
+    const int64_t r = ((int64_t)b * p.n_heads + hs) * p.Lq + qi;
+    p.delta[r] = s;
+    p.lse2[r] = l > -INFINITY ? l * WA_LOG2E : INFINITY;
+  }
+}
+
 template <int D>
 __global__ void __launch_bounds__(256) bwd_pre_kernel(BwdParams p) {
   constexpr int TPR = D / 8;
@@ -118,14 +170,32 @@ __global__ void __launch_bounds__(256) k2q_count_kernel(BwdParams p) {
   if (h < 0 || h >= p.H) return;
   const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
   const int width = (int)p.index_width, nq = p.Nq;
+  __shared__ int s_maxn;
+  if (threadIdx.x == 0) s_maxn = 0;
   for (int u = threadIdx.x; u < K2Q_COUNT_KB * nq; u += 256) cnt[u] = 0;
-  for (int i = threadIdx.x; i < nq; i += 256) s_num[i] = row_visits(p, row0 + i);
   __syncthreads();
-  for (int u = threadIdx.x; u < nq * width; u += 256) {
-    const int i = u / width, s2 = u - i * width;
-    if (s2 < s_num[i]) {
-      const int j = min(max(p.index[row0 * width + u], 0), p.Nkv - 1) - j0;
-      if (j >= 0 && j < K2Q_COUNT_KB) atomicAdd(&cnt[j * nq + i], 1u);
+  for (int i = threadIdx.x; i < nq; i += 256) {
+    const int n = row_visits(p, row0 + i);
+    s_num[i] = n;
+    atomicMax(&s_maxn, n);
+  }
+  __syncthreads();
+  // only the listed entries: (row, slot < the longest row's count), four loads in flight per thread
+  const int maxn = s_maxn, total = nq * maxn;
+  for (int u0 = threadIdx.x; u0 < total; u0 += 4 * 256) {
+    int jj[4], ii[4];
+    bool on[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int u = u0 + k * 256;
+      ii[k] = u / maxn;  // maxn > 0 whenever the loop runs
+      on[k] = u < total && u - ii[k] * maxn < s_num[min(ii[k], nq - 1)];
+      jj[k] = on[k] ? p.index[(row0 + ii[k]) * width + (u - ii[k] * maxn)] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = min(max(jj[k], 0), p.Nkv - 1) - j0;
+      if (on[k] && j >= 0 && j < K2Q_COUNT_KB) atomicAdd(&cnt[j * nq + ii[k]], 1u);
     }
   }
   __syncthreads();
@@ -607,8 +677,23 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
 template <int D, int BS>
 int launch_bwd(const BwdParams& bp, hipStream_t s) {
   const int nh = bp.n_heads;
-  hipLaunchKernelGGL((bwd_pre_kernel<D>), dim3((unsigned)((bp.Lq + (256 / (D / 8)) - 1) / (256 / (D / 8))), nh, bp.B),
-                     dim3(256), 0, s, bp);
+  const dim3 pre_grid((unsigned)((bp.Lq + (256 / (D / 8)) - 1) / (256 / (D / 8))), nh, bp.B);
+  // 8-element row vectors: a 16-byte aligned base and strides in multiples of 8 elements
+  auto vec_ok = [](const void* ptr, int64_t sb, int64_t st, int64_t sh) {
+    return wa_aligned16(ptr) && sb % 8 == 0 && st % 8 == 0 && sh % 8 == 0;
+  };
+  const bool ov = vec_ok(bp.o, bp.o_sb, bp.o_st, bp.o_sh);
+  const bool dv = vec_ok(bp.dout, bp.d_sb, bp.d_st, bp.d_sh);
+  if (ov && dv && bp.o_dtype == WA_F32 && bp.d_dtype == WA_BF16)
+    hipLaunchKernelGGL((bwd_pre_vec_kernel<D, float, bf16_t>), pre_grid, dim3(256), 0, s, bp);
+  else if (ov && dv && bp.o_dtype == WA_BF16 && bp.d_dtype == WA_BF16)
+    hipLaunchKernelGGL((bwd_pre_vec_kernel<D, bf16_t, bf16_t>), pre_grid, dim3(256), 0, s, bp);
+  else if (ov && dv && bp.o_dtype == WA_F32 && bp.d_dtype == WA_F32)
+    hipLaunchKernelGGL((bwd_pre_vec_kernel<D, float, float>), pre_grid, dim3(256), 0, s, bp);
+  else if (ov && dv && bp.o_dtype == WA_BF16 && bp.d_dtype == WA_F32)
+    hipLaunchKernelGGL((bwd_pre_vec_kernel<D, bf16_t, float>), pre_grid, dim3(256), 0, s, bp);
+  else
+    hipLaunchKernelGGL((bwd_pre_kernel<D>), pre_grid, dim3(256), 0, s, bp);
   int rc = wa_launch_status("bsa_bwd_pre");
   if (rc) return rc;
   if (bp.index && bp.Nq <= K2Q_COUNT_NQ)

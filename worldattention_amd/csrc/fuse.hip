@@ -55,13 +55,6 @@ __device__ __forceinline__ void gate_preact(const FuseParams& p, const bf16_t* q
   }
 }
 
-__device__ __forceinline__ float gate_value(const FuseParams& p, float pre_mfma, const bf16_t* qrow, int d) {
-  float pre = p.gate_w ? pre_mfma + (p.gate_b ? p.gate_b[d] : 0.f) : (float)qrow[d];
-  if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
-  float gs = wa_sigmoid(pre);
-  if (p.gate_out_bf16) gs = wa_bf16_round(gs);
-  return gs;
-}
 
 template <int D>
 __global__ void __launch_bounds__(256) fuse_fwd_kernel(FuseParams p) {
@@ -73,9 +66,42 @@ __global__ void __launch_bounds__(256) fuse_fwd_kernel(FuseParams p) {
   const int t = tile * 128 + w * 32 + l32;
   const bool ok = t < p.L;
   const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)(ok ? t : 0) * p.q_st + (int64_t)h * p.q_sh;
+  // Every read of the row (sparse and linear outputs, q and the gate weights for the gate) is
+  // issued before the first store: on gfx9 loads and stores share one counter, so a load issued
+  // after a store waits for that store.
+  const int64_t trow = ok ? t : 0;
+  f32x4 sv[DT][4], lv[DT][4];
+  if (mode & MODE_SPARSE) {
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+        sv[tt][rq] = *(const f32x4*)(p.sparse + (int64_t)b * p.s_sb + trow * p.s_st + (int64_t)h * p.s_sh +
+                                     32 * tt + 8 * rq + 4 * g);
+  }
+  if (mode & MODE_LINEAR) {
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+        lv[tt][rq] = *(const f32x4*)(p.lin + (int64_t)b * p.l_sb + trow * p.l_st + (int64_t)h * p.l_sh +
+                                     32 * tt + 8 * rq + 4 * g);
+  }
   f32x16 gacc[DT];
   bf16x8 qf[DC];
   if (mode & MODE_LINEAR) gate_preact<D>(p, qrow, ok, g, l32, gacc, qf);
+  float pre_in[DT][4][4];  // gate bias, or q itself for the sigmoid(q) gate, before any store
+  if (mode & MODE_LINEAR) {
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * tt + 8 * rq + 4 * g + i;
+          pre_in[tt][rq][i] = p.gate_w ? (p.gate_b ? p.gate_b[d] : 0.f) : (float)qrow[d];
+        }
+  }
   if (!ok) return;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
@@ -84,17 +110,19 @@ __global__ void __launch_bounds__(256) fuse_fwd_kernel(FuseParams p) {
       const int d0 = 32 * tt + 8 * rq + 4 * g;
       float val[4] = {0.f, 0.f, 0.f, 0.f};
       if (mode & MODE_SPARSE) {
-        const f32x4 sv = *(const f32x4*)(p.sparse + (int64_t)b * p.s_sb + (int64_t)t * p.s_st + (int64_t)h * p.s_sh + d0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) val[i] = p.attn_round_bf16 ? wa_bf16_round(sv[i]) : sv[i];
+        for (int i = 0; i < 4; ++i) val[i] = p.attn_round_bf16 ? wa_bf16_round(sv[tt][rq][i]) : sv[tt][rq][i];
       }
       if (mode & MODE_LINEAR) {
-        const f32x4 lv = *(const f32x4*)(p.lin + (int64_t)b * p.l_sb + (int64_t)t * p.l_st + (int64_t)h * p.l_sh + d0);
         f32x4 gs;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          gs[i] = gate_value(p, gacc[tt][rq * 4 + i], qrow, d0 + i);
-          const float l = p.lin_round_bf16 ? wa_bf16_round(lv[i]) : lv[i];
+          float pre = p.gate_w ? gacc[tt][rq * 4 + i] + pre_in[tt][rq][i] : pre_in[tt][rq][i];
+          if (p.gate_pre_bf16) pre = wa_bf16_round(pre);
+          float gv = wa_sigmoid(pre);
+          if (p.gate_out_bf16) gv = wa_bf16_round(gv);
+          gs[i] = gv;
+          const float l = p.lin_round_bf16 ? wa_bf16_round(lv[tt][rq][i]) : lv[tt][rq][i];
           val[i] = (mode & MODE_SPARSE) ? __fadd_rn(val[i], __fmul_rn(l, gs[i])) : __fmul_rn(l, gs[i]);
         }
         if (p.gate) *(f32x4*)(p.gate + (int64_t)b * p.g_sb + (int64_t)t * p.g_st + (int64_t)h * p.g_sh + d0) = gs;
@@ -230,33 +258,50 @@ __global__ void __launch_bounds__(256) fuse_bwd_kernel(FuseParams p) {
   }
 }
 
-// dW, db: sum of the tile partials over (tile, batch, linear head) in a fixed order.
-// dW / db: sum of the per-(tile, batch, linear head) partials. A workgroup covers 32 elements with
-// 8 partial groups (group g sums the partials g, g + 8, ... of the fixed list order); the groups
-// are then added in a fixed order, so the result is bitwise reproducible.
+// dW, db: sum of the per-(tile, batch, linear head) partials in a fixed order (bitwise
+// reproducible). A workgroup covers 32 consecutive elements (one 128-byte line of every partial)
+// with 8 groups of 32 threads; group g sums the linear-head partials g, g + 8, ... (in the order
+// tile, batch, linear head) in eight chains with eight loads in flight, and the group sums are
+// added in group order. Partials of heads without a linear branch are never read.
+constexpr int FR_EL = 32, FR_G = 8, FR_MAX_H = 256;
 __global__ void __launch_bounds__(256) fuse_reduce_kernel(FuseParams p, int D) {
-  __shared__ float red[8][32];
+  __shared__ float red[FR_G][FR_EL];
+  __shared__ int s_lin[FR_MAX_H];
+  __shared__ int s_nlin;
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int h = 0; h < p.H; ++h)
+      if (p.modes[h] & MODE_LINEAR) s_lin[n++] = h;
+    s_nlin = n;
+  }
+  __syncthreads();
   const int64_t per = (int64_t)D * D + D;
-  const int el = threadIdx.x & 31, grp = threadIdx.x >> 5;
-  const int64_t i = (int64_t)blockIdx.x * 32 + el;
-  const int n_src = p.n_tiles * p.B * p.H;
-  float s0 = 0.f, s1 = 0.f;
+  const int el = threadIdx.x % FR_EL, grp = threadIdx.x / FR_EL;
+  const int64_t i = (int64_t)blockIdx.x * FR_EL + el;
+  const int nlin = s_nlin, n_src = p.n_tiles * p.B * nlin;
+  float a[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) a[k] = 0.f;
   if (i < per) {
-    int k = 0;
-    for (int src = grp; src < n_src; src += 8, ++k) {
-      const int h = src % p.H;
-      if (!(p.modes[h] & MODE_LINEAR)) continue;
-      const float v = p.part[(int64_t)src * per + i];   // src = (tile * B + b) * H + h
-      if (k & 1) s1 += v;
-      else s0 += v;
+    const float* col = p.part + i;
+    for (int k0 = grp; k0 < n_src; k0 += 8 * FR_G) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = k0 + q * FR_G;
+        const int tb = k / max(nlin, 1);  // (tile * B + b)
+        v[q] = k < n_src ? col[((int64_t)tb * p.H + s_lin[k - tb * nlin]) * per] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) a[q] += v[q];
     }
   }
-  red[grp][el] = s0 + s1;
+  red[grp][el] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   __syncthreads();
   if (grp == 0 && i < per) {
     float s = 0.f;
 #pragma unroll
-    for (int g2 = 0; g2 < 8; ++g2) s += red[g2][el];
+    for (int g2 = 0; g2 < FR_G; ++g2) s += red[g2][el];
     if (i < (int64_t)D * D) p.dw[i] = s;
     else p.db[i - (int64_t)D * D] = s;
   }
@@ -320,6 +365,7 @@ extern "C" int wa_hsa_fuse_bwd(const wa_hsa_fuse_args* a, void* stream) {
   WA_CHECK_ARG(wa_aligned16(a->dlin) && a->dl_sb % 4 == 0 && a->dl_st % 4 == 0 && a->dl_sh % 4 == 0,
                "wa_hsa_fuse_bwd: dlin alignment");
   if (a->gate_w) WA_CHECK_ARG(a->workspace && a->dgate_w && a->dgate_b, "wa_hsa_fuse_bwd: gate_w needs workspace, dgate_w, dgate_b");
+  WA_CHECK_ARG(a->H <= FR_MAX_H, "wa_hsa_fuse_bwd: at most %d heads", FR_MAX_H);
   if (a->B == 0 || a->L == 0) return WA_OK;
   FuseParams fp{};
   fill_common(fp, a);
@@ -335,7 +381,7 @@ extern "C" int wa_hsa_fuse_bwd(const wa_hsa_fuse_args* a, void* stream) {
   if ((rc = wa_launch_status("hsa_fuse_bwd"))) return rc;
   if (a->gate_w) {
     const int64_t per = a->D * a->D + a->D;
-    hipLaunchKernelGGL(fuse_reduce_kernel, dim3((unsigned)((per + 31) / 32)), dim3(256), 0, s, fp, (int)a->D);
+    hipLaunchKernelGGL(fuse_reduce_kernel, dim3((unsigned)((per + FR_EL - 1) / FR_EL)), dim3(256), 0, s, fp, (int)a->D);
     return wa_launch_status("hsa_fuse_reduce");
   }
   return WA_OK;
