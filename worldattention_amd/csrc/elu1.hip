@@ -520,6 +520,7 @@ struct Elu1BwdParams {
   void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
+  int kv_tiles_per_wg;  // 128-token tiles per workgroup of the bf16 key-side kernel
   int64_t k_slab, v_slab;  // bytes of one (batch, head) K / V slab, first row to last row's end
   const int32_t* heads; int n_heads, H, B, Lq, Lkv, n_qt;
   float* part;    // [n_qt][B][n_heads][D*D + D]
@@ -785,7 +786,8 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
 }
 
 // Key side, bf16 K / V in and bf16 dK / dV out (written once): the same products as
-// elu1_bwd_kv_kernel with every global access coalesced. The workgroup's K and V tiles (128 tokens)
+// elu1_bwd_kv_kernel with every global access coalesced. A workgroup stages the state gradient
+// once and then walks a run of 128-token tiles (about one workgroup per CU): each tile's K and V
 // stream into LDS by direct-to-LDS loads, chunk-swizzled by token (chunk ^ (token & 15)), and give
 // the A fragments; per 32-channel column tile the results go through an LDS staging tile, from
 // which each thread forms 8 consecutive channels of a token (the dK factor elu1'(k) read from the
@@ -801,12 +803,19 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
   // else its own array
   __shared__ __attribute__((aligned(1024))) float s_stage[D == 128 ? 4 : 2 * 128 * 32];
   __shared__ float s_z[D];
-  const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  const int hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int64_t bh = (int64_t)b * p.n_heads + hs;
+  // this workgroup's run of 128-token tiles: the state gradient is staged once for all of them
+  const int n_tiles = (p.Lkv + 127) / 128;
+  const int tile_beg = blockIdx.x * p.kv_tiles_per_wg, tile_end = min(n_tiles, tile_beg + p.kv_tiles_per_wg);
+  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
+#pragma unroll 1
+  for (int tile = tile_beg; tile < tile_end; ++tile) {
   const int t0 = tile * 128;
 
   // K / V tiles: wave instruction q (i-th of wave w) moves RPI rows, 64 lanes x 16 bytes
@@ -828,8 +837,6 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
       lds_dma16(vrs, s_v + q * RPI * D, (int)((r * p.v_st + ch * 8) * 2));
     }
   }
-  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
-  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -889,6 +896,8 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
       *(bf16x8*)((bf16_t*)p.dk + (int64_t)b * p.dk_sb + t * p.dk_st + (int64_t)h * p.dk_sh + 32 * jt + cc * 8) = ok;
       *(bf16x8*)((bf16_t*)p.dv + (int64_t)b * p.dv_sb + t * p.dv_st + (int64_t)h * p.dv_sh + 32 * jt + cc * 8) = ov;
     }
+  }
+  __syncthreads();  // every read of this tile's K (and of the staging) before the next tile's loads
   }
 }
 
@@ -1054,8 +1063,13 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
                     a->dv_st % 8 == 0 && a->dv_sh % 8 == 0 && bp.k_slab < ((int64_t)1 << 31) &&
                     bp.v_slab < ((int64_t)1 << 31) && 128 * std::max(a->k_st, a->v_st) < ((int64_t)1 << 30);
   if (kv16) {
-    if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk, dim3(256), 0, s, bp);
-    else hipLaunchKernelGGL(elu1_bwd_kv16_kernel<64>, gk, dim3(256), 0, s, bp);
+    // about one workgroup per CU: each stages the state gradient once for its run of tiles
+    const int64_t n_tiles = (a->Lkv + 127) / 128;
+    const int64_t per_bh = std::max<int64_t>(1, std::min<int64_t>(n_tiles, (256 + a->B * nh - 1) / (a->B * nh)));
+    bp.kv_tiles_per_wg = (int)((n_tiles + per_bh - 1) / per_bh);
+    const dim3 gk16((unsigned)((n_tiles + bp.kv_tiles_per_wg - 1) / bp.kv_tiles_per_wg), (unsigned)nh, (unsigned)a->B);
+    if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk16, dim3(256), 0, s, bp);
+    else hipLaunchKernelGGL(elu1_bwd_kv16_kernel<64>, gk16, dim3(256), 0, s, bp);
   } else {
     if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv_kernel<128>, gk, dim3(256), 0, s, bp);
     else hipLaunchKernelGGL(elu1_bwd_kv_kernel<64>, gk, dim3(256), 0, s, bp);
