@@ -268,33 +268,42 @@ __device__ __forceinline__ void attend_step(const bf16_t* kb, const bf16_t* vb, 
       }
     }
   }
-  float mx = -INFINITY;
+  // Exponentials against the running max m_i, which may lag the scores: the step is accepted when
+  // every lane's sum of exponentials is at most 2^16 (so is each exponential: far from fp32 / bf16
+  // overflow). Otherwise (the first step, or scores more than ~11 above m_i) m_i moves to the step
+  // max, the accumulators are rescaled and the exponentials recomputed. The final normalization
+  // uses the same m_i, so the result does not depend on how far m_i lags.
+  float rs;
+  bf16x8 pb[PC];
+  auto exps = [&]() {
+    rs = 0.f;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-  }
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
-  // Lazy rescale: keep the running max unless the step max exceeds it by more than 8 (so every
-  // exponential stays <= 2^8); the final normalization uses the same max, so results are exact.
-  if (__any(mx > m_i + 8.f)) {
-    const float m_new = mx > m_i + 8.f ? mx : m_i;
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], scale_log2, -m_i));
+        rs += pv;
+        pb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)pv;
+      }
+    }
+  };
+  exps();
+  if (__any(!(rs <= 65536.f))) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
+    }
+    // every step has a real key, so mx is finite; on the first step m_i = -inf and alpha = 0
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    const float m_new = fmaxf(mx, m_i);
     const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
     l_i *= alpha;
     m_i = m_new;
 #pragma unroll
     for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-  }
-  float rs = 0.f;
-  bf16x8 pb[PC];
-#pragma unroll
-  for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], scale_log2, -m_i));
-      rs += pv;
-      pb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)pv;
-    }
+    exps();
   }
   l_i += rs;
   // V of this step: everything but the next step's K slices (the last NI loads) has landed, and
@@ -469,16 +478,19 @@ bsa_unit_kernel(FwdParams p) {
   // product V(t + 1) into the other stage. At the top of step t only V(t) may still be in flight
   // (the last NI loads), and before the PV product (attend_step) only K(t + 1); the barriers extend
   // each wave's wait to the workgroup and order a stage's refill after every wave's reads of it.
-  int t = 0;
+  // Two steps per iteration (stage 0, then stage 1), so every LDS address is a loop-invariant
+  // register plus an immediate offset.
   while (cur.valid) {
-    const int real = cur.real - 64 * cur.half;
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
-    const int vs = t & 1;
-    attend_step<D, NW>(kr + vs * TILE, vr + vs * TILE, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2,
-                       tiles(kr + (vs ^ 1) * TILE, c1, vr + (vs ^ 1) * TILE, c1), w, lane);
-    cur = c1;
-    cursor_next<BS>(c1, my_j, my_real);
-    ++t;
+#pragma unroll
+    for (int vs = 0; vs < 2; ++vs) {
+      if (!cur.valid) break;
+      const int real = cur.real - 64 * cur.half;
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
+      attend_step<D, NW>(kr + vs * TILE, vr + vs * TILE, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2,
+                         tiles(kr + (vs ^ 1) * TILE, c1, vr + (vs ^ 1) * TILE, c1), w, lane);
+      cur = c1;
+      cursor_next<BS>(c1, my_j, my_real);
+    }
   }
 
   // the last steps streamed empty tiles: let them land before the workgroup's LDS is freed
