@@ -49,6 +49,7 @@ struct BwdParams {
   bf16_t* dob;       // [B, n_heads, Lq, D]
   int32_t* k2q;      // [B, n_heads, Nkv, Nq]: (query block) | (multiplicity << 16)
   int32_t* k2q_num;  // [B, n_heads, Nkv]
+  int32_t* kv_order; // [B * n_heads * Nkv] key blocks by descending list length (dkdv launch order)
 };
 
 __device__ __forceinline__ int head_of(const BwdParams& p, int hs) { return p.heads ? p.heads[hs] : hs; }
@@ -454,6 +455,44 @@ __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))
 }
 
 // ---------------------------------------------------------------------------------------------
+// kv_order: the dkdv launch order, longest transposed list first, so that the longest workgroups
+// start first and the kernel does not end on a tail of long ones (a counting sort by list length
+// in one workgroup; blocks of equal length land in any order, which changes nothing but the
+// schedule: every block's dK / dV is computed by one workgroup alone). Needs Nq < KV_ORDER_T.
+// ---------------------------------------------------------------------------------------------
+constexpr int KV_ORDER_T = 1024;
+
+__global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
+  __shared__ int hist[KV_ORDER_T];
+  const int tid = threadIdx.x, n = p.B * p.n_heads * p.Nkv;
+  hist[tid] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += KV_ORDER_T) atomicAdd(&hist[min(max(p.k2q_num[i], 0), p.Nq)], 1);
+  __syncthreads();
+  // start[c] = number of blocks longer than c: an inclusive scan over c = Nq, Nq - 1, ..., 0
+  const int c = p.Nq - tid;  // this thread's length, for tid <= Nq
+  int v = c >= 0 ? hist[c] : 0;
+  __syncthreads();
+  hist[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < KV_ORDER_T; off <<= 1) {
+    const int add = tid >= off ? hist[tid - off] : 0;
+    __syncthreads();
+    hist[tid] += add;
+    __syncthreads();
+  }
+  // hist[t] now counts the blocks of length >= Nq - t; the first slot of length c is hist[Nq - c] - count(c)
+  const int first = c >= 0 ? hist[tid] - v : 0;
+  __syncthreads();
+  if (c >= 0) hist[c] = first;
+  __syncthreads();
+  for (int i = tid; i < n; i += KV_ORDER_T) {
+    const int len = min(max(p.k2q_num[i], 0), p.Nq);
+    p.kv_order[atomicAdd(&hist[len], 1)] = i;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // dkdv: one workgroup (BS / 32 waves, wave w = keys 32w..) per (batch, head slot, key block);
 // 64-query steps over the query blocks that listed it; Q, dO and the rows' log-sum-exp and delta
 // stream through the ring (the statistics as 4-byte direct-to-LDS loads, scaled at use).
@@ -474,7 +513,9 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
   __shared__ int32_t s_lst[LM];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
-  const int j = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  // 1-D grid over (batch, head slot, key block), in kv_order when there is one
+  const int id = p.kv_order ? p.kv_order[blockIdx.x] : (int)blockIdx.x;
+  const int j = id % p.Nkv, hs = (id / p.Nkv) % p.n_heads, b = id / (p.Nkv * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
   const int real = kv_real(p, j, BS);
@@ -707,7 +748,14 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     if ((rc = wa_launch_status("bsa_bwd_dq"))) return rc;
   }
   if (bp.dk && bp.dv) {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3(bp.Nkv, nh, bp.B), dim3(2 * BS), 0, s, bp);
+    BwdParams kp = bp;
+    if (bp.Nq < KV_ORDER_T) {
+      hipLaunchKernelGGL(kv_order_kernel, dim3(1), dim3(KV_ORDER_T), 0, s, bp);
+      if ((rc = wa_launch_status("bsa_bwd_kv_order"))) return rc;
+    } else {
+      kp.kv_order = nullptr;
+    }
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(2 * BS), 0, s, kp);
     if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return rc;
   }
   return WA_OK;
@@ -721,7 +769,7 @@ extern "C" int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_
                                               int64_t block_size) {
   const int64_t nq = (Lq + block_size - 1) / block_size, nkv = (Lkv + block_size - 1) / block_size;
   return 2 * align256(B * n_heads * Lq * 4) + align256(B * n_heads * Lq * D * 2) +
-         align256(B * n_heads * nkv * nq * 4) + align256(B * n_heads * nkv * 4);
+         align256(B * n_heads * nkv * nq * 4) + 2 * align256(B * n_heads * nkv * 4);
 }
 
 extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
@@ -747,6 +795,7 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(nq <= 65535 && nkv <= 65535 && a->Lq < (1 << 30) && a->Lkv < (1 << 30), "wa_bsa_bwd: problem too large");
   const int64_t nh = a->heads ? a->n_heads : a->H;
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_bwd: bad head count");
+  WA_CHECK_ARG(a->B * nh * nkv < ((int64_t)1 << 31), "wa_bsa_bwd: too many key blocks");
   // the tile streams address one (batch, head) slab with 32-bit byte offsets
   const int64_t q_slab = ((a->Lq - 1) * a->q_st + a->D) * 2;
   const int64_t k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2, v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
@@ -785,6 +834,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.k2q = (int32_t*)ws;
   ws += align256(a->B * nh * nkv * nq * 4);
   bp.k2q_num = (int32_t*)ws;
+  ws += align256(a->B * nh * nkv * 4);
+  bp.kv_order = (int32_t*)ws;
 
   hipStream_t s = (hipStream_t)stream;
   if (a->D == 64 && a->block_size == 64) return launch_bwd<64, 64>(bp, s);
