@@ -373,6 +373,39 @@ def test_bsa_arrival_counters_and_empty_rows(use_visits):
         assert torch.count_nonzero(ref[:, 2 * bs:3 * bs, 0]) == 0
 
 
+@pytest.mark.parametrize("order", ["rising", "falling"])
+@pytest.mark.parametrize("split", [2, 16])
+def test_bsa_large_logits_rescale_matches_oracle(order, split):
+    """Logits up to ~170 (log2 units) whose maxima rise (or fall) by ~15 per key block along the
+    visit order (ascending block id): the forward's running max lags the scores, and the sum check
+    must move it (rescaling the accumulators) on the first step and on most later ones, or never
+    after the first when the scores fall. Split rows merge partials whose log-sum-exps differ by
+    far more than fp32 exponents of the raw scores could hold."""
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(11)
+    bs, d, b, h, nq, nkv = 128, 128, 1, 2, 2, 12
+    lq, lkv = nq * bs, nkv * bs - 50
+    q = torch.randn(b, lq, h, d) * 2
+    grow = torch.arange(nkv, dtype=torch.float32) * 2 + 1
+    if order == "falling":
+        grow = grow.flip(0)
+    k = torch.randn(b, nkv * bs, h, d) * grow.repeat_interleave(bs).view(1, -1, 1, 1)
+    k = k[:, :lkv]
+    v = torch.randn(b, lkv, h, d)
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    num = torch.full((b, h, nq), nkv, dtype=torch.int32)
+    num[0, 1, 1] = 5
+    got, _ = bsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), index=index.to(DEV), num=num.to(DEV), block_size=bs,
+                         layout="blhd", lq=lq, lkv=lkv, split=split, out_dtype=torch.float32)
+    qp = O.pad_to_len(q, nq * bs).transpose(1, 2)
+    kp, vp = (O.pad_to_len(t, nkv * bs).transpose(1, 2) for t in (k, v))
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    want = O.block_sparse_attention(qp.float(), kp.float(), vp.float(), index, num, sizes, bs).transpose(1, 2)[:, :lq]
+    assert torch.isfinite(got).all()
+    assert_close(got, want, what=f"{order} logits, split {split}")
+
+
 def test_hsa_forward_graph_replays_equal_eager_calls():
     """The cfg 2 call captured in a HIP graph (as bench.py times it): every replay, with eager work
     and synchronizations between replays, equals the eager call bit for bit."""
