@@ -284,10 +284,11 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
   }
 }
 
-// Top-k routing, four rows (query blocks i0 .. i0 + 3 of one head) per workgroup, rows of at most
-// 512 blocks. Scores: thread t owns key j (= t, t + 256, ...) and forms its four rows' dot
-// products from one pass over the key's pooled vector (the rows share the head's pooled keys; the
-// pooled queries are broadcast from LDS). Then one wave per row: slot e*64 + lane lives in
+// Top-k routing, R rows (query blocks i0 .. i0 + R - 1 of one head) per workgroup, rows of at most
+// 512 blocks (R = 2: twice the workgroups in flight of R = 4, 14.8 -> 13.5 us at cfg 2; R = 1 is
+// 16 us). Scores: thread t owns key j (= t, t + 256, ...) and forms its R rows' dot products from
+// one pass over the key's pooled vector (the rows share the head's pooled keys; the pooled queries
+// are broadcast from LDS). Then one wave per row: slot e*64 + lane lives in
 // register e of the lane, so the softmax reduces over the wave and the bitonic network runs in
 // registers (strides >= 64) and lane shuffles (strides < 64) without further barriers. The
 // softmax takes the max, fp32 exponentials and a double row sum, then p = e * (1 / sum).
@@ -297,14 +298,14 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-template <int KPL, int DK>
+template <int KPL, int DK, int R>
 __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   constexpr int NP = 64 * KPL;
-  __shared__ __attribute__((aligned(16))) float q_sh[4][256];
-  __shared__ float s_sh[4][NP];
+  __shared__ __attribute__((aligned(16))) float q_sh[R][256];
+  __shared__ float s_sh[R][NP];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
   if (clear_unrouted(p)) return;
-  const int i0 = blockIdx.x * 4, hs = blockIdx.y, b = blockIdx.z;
+  const int i0 = blockIdx.x * R, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;  // uniform per workgroup
   const int N = p.Nkv, D = DK ? DK : p.D;
@@ -321,13 +322,15 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
     for (int c = 0; c < (DK ? DK / 4 : 1); ++c) kv[c] = *(const f32x4*)(kr + 4 * c);
   };
   if (DK) load_key(tid);
-  for (int u = tid; u < 4 * D; u += 256) {
+  for (int u = tid; u < R * D; u += 256) {
     const int r = u / D, d = u % D;
     q_sh[r][d] = i0 + r < p.Nq ? p.qp[(row0 + i0 + r) * D + d] : 0.f;
   }
   __syncthreads();
   for (int j = tid; j < N; j += 256) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
     if (DK) {
       // groups of four chunks: the fences keep the compiler from hoisting every LDS read of the
       // pooled queries ahead of the products (which would not fit in registers)
@@ -336,7 +339,7 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
 #pragma unroll
         for (int c = c0; c < c0 + 4; ++c) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
+          for (int r = 0; r < R; ++r) {
             const f32x4 qv = *(const f32x4*)(&q_sh[r][4 * c]);
             acc[r] = fmaf(qv[0], kv[c][0], acc[r]);
             acc[r] = fmaf(qv[1], kv[c][1], acc[r]);
@@ -354,7 +357,7 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) kc[c] = *(const f32x4*)(kr + d0 + 4 * c);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
+          for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
               const f32x4 qv = *(const f32x4*)(&q_sh[r][d0 + 4 * c]);
@@ -369,16 +372,16 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
         for (int d = 0; d < D; ++d) {
           const float kd = kr[d];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
+          for (int r = 0; r < R; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
         }
       }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s_sh[r][j] = acc[r] * p.scale;
+    for (int r = 0; r < R; ++r) s_sh[r][j] = acc[r] * p.scale;
   }
   __syncthreads();
   const int i = i0 + w;
-  if (i >= p.Nq) return;
+  if (w >= R || i >= p.Nq) return;
   const int64_t row = row0 + i;
   float* ss = s_sh[w];
 
@@ -652,16 +655,16 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   dim3 grid((unsigned)a->Nq + 1, (unsigned)nh, (unsigned)a->B);  // + the clearing workgroup
   hipStream_t s = (hipStream_t)stream;
   if (a->mode == WA_ROUTE_TOPK && !a->probs && !a->probs_out && a->Nkv <= 512) {
-    const dim3 wgrid((unsigned)((a->Nq + 3) / 4) + 1, (unsigned)nh, (unsigned)a->B);
+    const dim3 wgrid((unsigned)((a->Nq + 1) / 2) + 1, (unsigned)nh, (unsigned)a->B);
     if (a->D == 128 && a->Nkv <= 256) {
-      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 128>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 128>), wgrid, dim3(256), 0, s, rp);
-      else hipLaunchKernelGGL((route_wave_kernel<4, 128>), wgrid, dim3(256), 0, s, rp);
+      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 128, 2>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 128, 2>), wgrid, dim3(256), 0, s, rp);
+      else hipLaunchKernelGGL((route_wave_kernel<4, 128, 2>), wgrid, dim3(256), 0, s, rp);
     } else {
-      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 0>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 0>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 256) hipLaunchKernelGGL((route_wave_kernel<4, 0>), wgrid, dim3(256), 0, s, rp);
-      else hipLaunchKernelGGL((route_wave_kernel<8, 0>), wgrid, dim3(256), 0, s, rp);
+      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 0, 2>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 0, 2>), wgrid, dim3(256), 0, s, rp);
+      else if (a->Nkv <= 256) hipLaunchKernelGGL((route_wave_kernel<4, 0, 2>), wgrid, dim3(256), 0, s, rp);
+      else hipLaunchKernelGGL((route_wave_kernel<8, 0, 2>), wgrid, dim3(256), 0, s, rp);
     }
     return wa_launch_status("route_wave");
   }
