@@ -13,10 +13,12 @@ gives the HBM rate of the memory-bound launches of the same call (Q/K block pool
 elu1 readout), each timed alone.
 
 Also on the same line:
-* ``hkv`` (cfg 3): page-summary HBM GB/s over the 120-frame history, selection time, the pinned
-  host -> device page gather GB/s (8 one-frame pages of K+V per layer, side stream) against a plain
-  pinned copy of the same size class, the re-rope, the HSA forward over the 14-frame pool, and the
-  per-layer time with the next layer's gather overlapped with this layer's attention;
+* ``hkv`` (cfg 3), through ``HKVCache.store / retrieve / apply``: page-summary HBM GB/s over the
+  120-frame history, the store rate into the pinned tier, retrieval time, the install rate of
+  ``apply`` (8 one-frame pages of K+V per layer: pinned host -> device copies and re-rope on the
+  side stream) against a plain pinned copy, the re-rope kernel, the HSA forward over the 14-frame
+  pool, and the per-layer time with later layers' installs overlapped with attention
+  (``apply(wait=False)`` + ``wait_layer``);
 * ``train`` (cfg 5): HSA forward + backward at the cfg 2 shape with top-k 16;
 * ``wan14b`` (cfg 4): 40 layers x 4 denoising steps of QKV projection + HSA + out projection.
 """
@@ -256,10 +258,14 @@ def memory_legs(cfg, plan, route, gate, dev, iters):
 # cfg 3 — HKV retrieval, gather, re-rope and attention over the page pool
 # ---------------------------------------------------------------------------------------------
 def bench_cfg3(args, dev):
+    """cfg 3 through the product API: the history is banked with ``HKVCache.store`` (19 six-frame
+    chunks, one-frame pages, every layer), the pages are chosen with ``HKVCache.retrieve`` and
+    installed with ``HKVCache.apply`` into the online cache of each layer, which is the first 8
+    frame slots of that layer's page pool (the 6 resident frames follow it), and the HSA forward
+    runs over the 21,840-token pool."""
     from worldattention_amd import hkv as W
     from worldattention_amd import workloads
     from worldattention_amd.hkv import _ops
-    from worldattention_amd.hkv.cache import _copy
     from worldattention_amd.hsa import attention as WA
 
     layers = args.hkv_layers
@@ -268,14 +274,15 @@ def bench_cfg3(args, dev):
     hist = cfg["history_frames"]
     heads, d = cfg["q"].shape[2], cfg["q"].shape[3]
     nt = W.temporal_complex_dims(d)
-    main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    band = W.temporal_band(cfg["freqs"], d)
+    main = torch.cuda.current_stream()
     log(f"cfg3: workload ready ({layers} layers, {hist} frames, pinned host pool "
         f"{sum(t.numel() * 2 for t in cfg['host_k'] + cfg['host_v']) / 2**30:.2f} GiB)")
 
-    # page summaries over the whole history (layer-0 keys, one page per frame)
+    # page-summary kernel over the whole history (layer-0 keys, one page per frame)
     keys0 = cfg["keys0"]
     frames = torch.arange(hist)
-    factors = _ops.factor_table(cfg["freqs"][:, :nt], torch.zeros_like(frames), frames, keys0.device)
+    factors = _ops.factor_table(band, torch.zeros_like(frames), frames, keys0.device)
     flat = keys0.view(1, keys0.shape[1], heads * d)
 
     def summary_kernel():
@@ -284,69 +291,99 @@ def bench_cfg3(args, dev):
     summary_kernel()
     sum_ms = stream_time_ms(summary_kernel, 20)
     sum_bytes = keys0.numel() * keys0.element_size()
-    spans = [(f * ft, (f + 1) * ft) for f in range(hist)]
-    page_index = W.page_key_index(keys0, spans, frame_seq_length=ft, start_frame=0, temporal_freqs=cfg["freqs"])
-    api_ms = stream_time_ms(lambda: W.page_key_index(keys0, spans, frame_seq_length=ft, start_frame=0,
-                                                     temporal_freqs=cfg["freqs"]), 10)
 
-    # selection: query index + scores + top-8 among the host-tier pages
-    mask = torch.zeros(hist, dtype=torch.uint8, device=dev)
-    mask[hf:] = 1
+    # bank frames 0..113 of every layer: HKVCache.store per six-frame chunk (page summaries from the
+    # layer-0 keys, device -> pinned blob copies on the side stream)
+    chunk_frames = 6
+    n_chunks = hf // chunk_frames
+    bank = W.HKVCache(frame_seq_length=ft, page_size_frames=1, topk_pages=nret, stage1_topk_chunks=n_chunks,
+                      cpu_max_chunks=max(64, n_chunks), rerope=True)
+    dev_k = [keys0[:, : hf * ft]] + [cfg["host_k"][layer].to(dev) for layer in range(1, layers)]
+    dev_v = [cfg["host_v"][layer].to(dev) for layer in range(layers)]
+    gp = torch.Generator().manual_seed(args.seed + 7)
+    prompts = [torch.randn(1, 4, 64, generator=gp).to(dev) for _ in range(n_chunks + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for c in range(n_chunks):
+        s, e = c * chunk_frames * ft, (c + 1) * chunk_frames * ft
+        kv = [{"k": dev_k[layer][:, s:e], "v": dev_v[layer][:, s:e], "local_end_index": torch.tensor(e - s, device=dev),
+               "global_end_index": torch.tensor(e, device=dev)} for layer in range(layers)]
+        bank.store(kv, prompt_embeds=prompts[c], current_start_frame=(c + 1) * chunk_frames, temporal_freqs=band)
+    torch.cuda.synchronize()
+    store_ms = (time.perf_counter() - t0) * 1e3
+    store_bytes = 2 * layers * hf * ft * heads * d * 2
+    del dev_k, dev_v
+    for layer in range(1, layers):
+        cfg["host_k"][layer] = cfg["host_v"][layer] = None
+    cfg["host_v"][0] = None
 
-    def select():
-        qv = W.query_index(cfg["q_content"])
-        return W.select_pages(page_index, qv, nret, mask=mask)
+    # retrieval: stage 1 over the prompt bank, stage 2 over the banked pages, chronological order
+    qvec = W.query_index(cfg["q_content"])
 
-    sel, _ = select()
-    sel_ms = stream_time_ms(select, 50)
-    chosen = sorted(int(i) for i in sel.tolist())
+    def retrieve():
+        return bank.retrieve(prompt_embeds=prompts[-1], query_vec=qvec)
+
+    pairs = retrieve()
+    times = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        retrieve()
+        times.append((time.perf_counter() - t0) * 1e3)
+    retrieve_ms = statistics.median(times)
+    chosen = [c * chunk_frames + p for c, p in pairs]
     recall = len(set(chosen) & set(cfg["truth"])) / nret
 
-    # gather plan: page i of the selection -> pool slot i, re-roped to frame (hist - nres - nret) + i
-    base = hist - nres - nret
-    pool_tokens = (nret + nres) * ft
-    rerope_f = _ops.factor_table(cfg["freqs"][:, :nt], torch.tensor([base + i for i in range(nret)]),
-                                 torch.tensor(chosen), dev)
-    rows = torch.arange(nret, dtype=torch.int32, device=dev).repeat_interleave(ft)
+    # install: each layer's online cache is the first nret frame slots of its page pool
+    base = hist - nres
+    caches = [{"k": cfg["pool_k"][layer][:, : nret * ft], "v": cfg["pool_v"][layer][:, : nret * ft],
+               "global_end_index": torch.zeros([], dtype=torch.long, device=dev),
+               "local_end_index": torch.zeros([], dtype=torch.long, device=dev)} for layer in range(layers)]
 
-    def layer_copies(layer):
-        cps = []
-        for name, host, pool in (("k", cfg["host_k"][layer], cfg["pool_k"][layer]),
-                                 ("v", cfg["host_v"][layer], cfg["pool_v"][layer])):
-            for i, f in enumerate(chosen):
-                cps.append(_copy(host[:, f * ft:(f + 1) * ft], pool[:, i * ft:(i + 1) * ft]))
-        return cps
+    def install(wait):
+        return bank.apply(caches, pairs, current_start_frame=base, temporal_freqs=band, wait=wait)
 
-    plans = [layer_copies(layer) for layer in range(layers)]
+    install(True)
+    torch.cuda.synchronize()
+    side = bank._side(torch.device(dev))
+    spans, walls = [], []
+    for _ in range(5):
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        s_ev.record(side)
+        install(False)
+        e_ev.record(side)
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) * 1e3)
+        spans.append(s_ev.elapsed_time(e_ev))
+    install_ms = statistics.median(spans) / layers
+    install_wall_ms = statistics.median(walls) / layers
     gather_bytes = 2 * nret * ft * heads * d * 2
 
-    def gather(layer):
-        _ops.copy_pages(plans[layer], to_device=True, stream=side)
+    # re-rope kernel alone (the K band of the installed pages, in place)
+    rerope_f = _ops.factor_table(band, torch.tensor([base - nret + i for i in range(nret)]),
+                                 torch.tensor(chosen), dev)
+    rows = torch.arange(nret, dtype=torch.int32, device=dev).repeat_interleave(ft)
+    scratch = cfg["pool_k"][0][:, : nret * ft].clone()
 
-    def rerope(layer):
-        with torch.cuda.stream(side):
-            _ops.rotate_temporal(cfg["pool_k"][layer], rerope_f, rows=rows, t0=0, t1=nret * ft)
+    def rerope():
+        _ops.rotate_temporal(scratch, rerope_f, rows=rows, t0=0, t1=nret * ft)
 
-    side.wait_stream(main)
-    for layer in range(layers):
-        gather(layer)
-        rerope(layer)
-    torch.cuda.synchronize()
-    gather_ms = stream_time_ms(lambda: [gather(layer) for layer in range(layers)], 5, stream=side) / layers
-    rerope_ms = stream_time_ms(lambda: [rerope(layer) for layer in range(layers)], 10, stream=side) / layers
+    rerope()
+    rerope_ms = stream_time_ms(rerope, 20)
     rerope_bytes = 2 * nret * ft * heads * (2 * nt) * 2
+    del scratch
 
     # plain pinned -> device copy of one layer's whole host K pool: the host-link reference rate
     big = cfg["host_k"][0]
     dst = torch.empty(big.shape, dtype=big.dtype, device=dev)
-    peak_copy = [_copy(big, dst)]
-    h2d_ms = stream_time_ms(lambda: _ops.copy_pages(peak_copy, to_device=True, stream=side), 3, stream=side)
+    h2d_ms = stream_time_ms(lambda: dst.copy_(big, non_blocking=True), 3)
     h2d_gbs = big.numel() * 2 / (h2d_ms * 1e-3) / 1e9
     del dst
 
     # the reference's pattern: per-page synchronous copies from pageable host memory (cache.py:229-242)
-    pageable_k = cfg["host_k"][0][:, : (max(chosen) + 1) * ft].clone()
-    pageable_v = cfg["host_v"][0][:, : (max(chosen) + 1) * ft].clone()
+    pageable_k = big[:, : (max(chosen) + 1) * ft].clone()
+    pageable_v = pageable_k.clone()
 
     def reference_style():
         ks = [pageable_k[:, f * ft:(f + 1) * ft].to(dev) for f in chosen]
@@ -360,8 +397,9 @@ def bench_cfg3(args, dev):
     torch.cuda.synchronize()
     ref_ms = (time.perf_counter() - t0) * 1e3 / 3
     del pageable_k, pageable_v
+    cfg["host_k"][0] = None
 
-    # HSA forward over the pool (8 retrieved + 6 resident frames = 21,840 tokens)
+    # HSA forward over each layer's pool (8 installed + 6 resident frames = 21,840 tokens)
     gate, proj = gate_and_proj(d, dev)
     kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=proj, v_proj_mat=proj, gate_lin=gate, block_size=128,
               tau_min=0.35, tau_max=1.0, proj_segment_len=ft, routing="topk", topk=cfg["topk"],
@@ -375,56 +413,61 @@ def bench_cfg3(args, dev):
     attn_ms = stream_time_ms(lambda: [attend(layer) for layer in range(layers)], 5) / layers
 
     def serial():
+        install(True)
         for layer in range(layers):
-            side.wait_stream(main)
-            gather(layer)
-            rerope(layer)
-            main.wait_stream(side)
             attend(layer)
 
     def pipelined():
-        side.wait_stream(main)
-        events = []
+        install(False)
         for layer in range(layers):
-            gather(layer)
-            rerope(layer)
-            ev = torch.cuda.Event()
-            ev.record(side)
-            events.append(ev)
-        for layer in range(layers):
-            main.wait_event(events[layer])
+            bank.wait_layer(layer)
             attend(layer)
 
-    serial()
-    serial_ms = stream_time_ms(serial, 3) / layers
-    pipelined()
-    pipe_ms = stream_time_ms(pipelined, 3) / layers
+    def wall_ms(fn, iters=3):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / iters / layers
+
+    serial_ms = wall_ms(serial)
+    pipe_ms = wall_ms(pipelined)
     res = {
         "workload": f"cfg3: {hist}-frame history x {ft} tokens, H={heads} D={d} bf16, one-frame pages; frames "
-                    f"0..{hf - 1} in pinned host memory, {nres} resident; top-{nret} of the {hf} host pages "
-                    f"(resident pages masked), gathered into pool slots 0..{nret - 1} and re-roped to frames "
-                    f"{base}..{base + nret - 1}; HSA over {pool_tokens} pool tokens; {layers} layers",
+                    f"0..{hf - 1} banked with HKVCache.store as {n_chunks} chunks of {chunk_frames} frames "
+                    f"(pinned host tier), {nres} resident frames; HKVCache.retrieve picks the top-{nret} pages, "
+                    f"HKVCache.apply installs them into each layer's online cache (pool slots 0..{nret - 1}, "
+                    f"re-roped to frames {base - nret}..{base - 1}); HSA over {(nret + nres) * ft} pool tokens; "
+                    f"{layers} layers",
         "summary_gbs": round(sum_bytes / (sum_ms * 1e-3) / 1e9, 1),
         "summary_kernel_ms": round(sum_ms, 4),
         "summary_hbm_frac": round(sum_bytes / (sum_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "summary_api_ms": round(api_ms, 4),
-        "select_ms": round(sel_ms, 4),
+        "store_ms_all_layers": round(store_ms, 3),
+        "store_gbs": round(store_bytes / (store_ms * 1e-3) / 1e9, 2),
+        "retrieve_ms": round(retrieve_ms, 4),
         "recall_vs_planted": recall,
         "gather_bytes_per_layer": gather_bytes,
-        "gather_ms_per_layer": round(gather_ms, 4),
-        "gather_gbs": round(gather_bytes / (gather_ms * 1e-3) / 1e9, 2),
+        "apply_ms_per_layer": round(install_ms, 4),
+        "apply_wall_ms_per_layer": round(install_wall_ms, 4),
+        "apply_gbs": round(gather_bytes / (install_ms * 1e-3) / 1e9, 2),
         "pinned_h2d_copy_gbs": round(h2d_gbs, 2),
-        "gather_frac_of_pinned_copy": round(gather_bytes / (gather_ms * 1e-3) / 1e9 / h2d_gbs, 3),
+        "apply_frac_of_pinned_copy": round(gather_bytes / (install_ms * 1e-3) / 1e9 / h2d_gbs, 3),
         "reference_style_pageable_gbs": round(gather_bytes / (ref_ms * 1e-3) / 1e9, 2),
-        "rerope_ms_per_layer": round(rerope_ms, 4),
+        "rerope_kernel_ms": round(rerope_ms, 4),
         "rerope_gbs": round(rerope_bytes / (rerope_ms * 1e-3) / 1e9, 1),
         "hsa_fwd_ms_per_layer": round(attn_ms, 4),
         "serial_ms_per_layer": round(serial_ms, 4),
         "overlapped_ms_per_layer": round(pipe_ms, 4),
+        "timing": "apply_ms_per_layer: GPU span of HKVCache.apply(wait=False) on its side stream (zero-copy "
+                  "pinned gather + re-rope + end indices, all layers) / layers; apply_wall_ms_per_layer: the "
+                  "same call's wall time including host work; serial: apply(wait=True) then the layers' HSA "
+                  "calls; overlapped: apply(wait=False), then per layer wait_layer + HSA call",
     }
-    log(f"cfg3: summary {res['summary_gbs']} GB/s, gather {res['gather_gbs']} GB/s "
+    log(f"cfg3: summary {res['summary_gbs']} GB/s, store {res['store_gbs']} GB/s, apply {res['apply_gbs']} GB/s "
         f"(pinned copy {res['pinned_h2d_copy_gbs']}), overlapped {pipe_ms:.3f} ms/layer vs serial {serial_ms:.3f}")
-    del cfg
+    del cfg, bank
     torch.cuda.empty_cache()
     return res
 
@@ -535,8 +578,38 @@ def bench_cfg4(args, dev):
 
 
 # ---------------------------------------------------------------------------------------------
+def usable_cpus() -> int:
+    """CPUs this process may run on: the affinity set, capped by a cgroup CPU quota when one is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    for path in ("/sys/fs/cgroup/cpu.max", "/sys/fs/cgroup/cpu/cpu.cfs_quota_us"):
+        try:
+            fields = open(path).read().split()
+        except OSError:
+            continue
+        if path.endswith("cpu.max") and fields and fields[0] != "max":
+            n = min(n, max(1, -(-int(fields[0]) // int(fields[1]))))
+        elif path.endswith("quota_us") and fields and int(fields[0]) > 0:
+            period = int(open("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read())
+            n = min(n, max(1, -(-int(fields[0]) // period)))
+        break
+    return n
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(args, cfg, proj, useful_flop):
     from oracle import hsa as O
+    threads_before = torch.get_num_threads()
+    threads = usable_cpus()
+    torch.set_num_threads(threads)
     d = cfg["q"].shape[-1]
     cpu = {k2: (t.cpu() if torch.is_tensor(t) else t) for k2, t in cfg.items()}
     projc = proj.cpu()
@@ -550,12 +623,14 @@ def cpu_baseline(args, cfg, proj, useful_flop):
         if i:
             times.append(time.perf_counter() - t1)
     cpu_s = statistics.median(times)
-    log(f"cpu baseline: {cpu_s * 1e3:.1f} ms/call")
+    torch.set_num_threads(threads_before)
+    log(f"cpu baseline: {cpu_s * 1e3:.1f} ms/call on {threads} threads")
     return {"value": round(useful_flop / cpu_s / 1e12, 4), "unit": "TFLOP/s (effective sparse, whole HSA fwd call)",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{args.cpu_sample_calls} full cfg2 HSA forward calls of the CPU oracle (fp32 math), "
-                      f"median {cpu_s * 1e3:.1f} ms/call after 1 warm-up",
-            "ms_per_call": round(cpu_s * 1e3, 2)}
+            "cores": threads, "kind": "port",
+            "sample": f"{args.cpu_sample_calls} full cfg2 HSA forward calls of the CPU oracle (fp32 math, "
+                      f"torch.set_num_threads({threads})), median {cpu_s * 1e3:.1f} ms/call after 1 warm-up",
+            "ms_per_call": round(cpu_s * 1e3, 2), "os_cpu_count": os.cpu_count(), "usable_cpus": threads,
+            "cpu_model": cpu_model()}
 
 
 def main():

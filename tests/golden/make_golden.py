@@ -10,7 +10,10 @@ name (so the heavy ``wan/__init__.py`` is never executed) and records, on seeded
 * ``routing_gini.pt`` — ``build_block_routing`` (Gini thresholds, counts, permutation): the fp32
   rounding of the Gini mean/threshold and the double ``cumsum`` decide ``num`` near boundaries;
 * ``hsa_attention.pt`` — ``hsa_attention`` end to end (torch backend, fp32 and bf16 inputs, padded
-  lengths, a trained-looking gate): the composed cast sequence of ``attention.py:184-259``.
+  lengths, a trained-looking gate): the composed cast sequence of ``attention.py:184-259``;
+* ``routing_boundary.pt`` — ``build_block_routing`` on maps crafted so that some rows' exclusive
+  prefix lies -3..+3 fp32 ulp from the head threshold: where ``num`` turns on the threshold's
+  last bits.
 
 Only inputs and outputs are written; no reference source is copied.
 """
@@ -44,6 +47,58 @@ def routing_cases(ref):
             r = ref.build_block_routing(attn, tau_min, tau_max, return_mask=True)
             cases.append(dict(block_attn=attn, tau_min=tau_min, tau_max=tau_max, index=r.index,
                               num=r.num, mask=r.mask, thresholds=r.thresholds))
+    return cases
+
+
+def _ulp(x: float) -> float:
+    import math
+    m, e = math.frexp(abs(x))
+    return 2.0 ** (e - 24)
+
+
+def routing_boundary_cases(ref):
+    """Maps with rows whose exclusive prefix sits a few fp32 ulp from the head threshold.
+
+    For head 0 of each map, target rows get their largest weight nudged (iterating, since every row
+    moves the head's Gini mean) until the reference's exclusive prefix at a chosen slot lands
+    ``delta`` ulp from the reference's threshold: there ``num`` depends on the last bits of the
+    fp32 Gini mean. Each case records, per target row, the slot and the offset actually reached
+    (measured with the reference's own outputs)."""
+    cases = []
+    g = torch.Generator().manual_seed(777)
+    for shape, temp in (((1, 2, 12, 16), 2.0), ((1, 2, 37, 256), 3.0)):
+        attn = torch.softmax(torch.randn(shape, generator=g) * temp, dim=-1)
+        deltas = [-3, -2, -1, 0, 1, 2, 3]
+        rows = list(range(len(deltas)))
+        slots = {}
+        for _ in range(60):
+            r = ref.build_block_routing(attn, 0.35, 1.0)
+            tau = float(r.thresholds[0])
+            sp, si = torch.sort(attn.float(), dim=-1, descending=True)
+            excl = torch.cumsum(sp, dim=-1) - sp
+            done = True
+            for row, delta in zip(rows, deltas):
+                e = excl[0, 0, row]
+                if row not in slots:
+                    slots[row] = int(torch.argmin((e[1:] - tau).abs())) + 1
+                m = slots[row]
+                want = tau + delta * _ulp(tau)
+                err = want - float(e[m])
+                if abs(err) > 0.25 * _ulp(tau):
+                    done = False
+                    top = int(si[0, 0, row, 0])
+                    attn[0, 0, row, top] = float(attn[0, 0, row, top]) + err
+            if done:
+                break
+        r = ref.build_block_routing(attn, 0.35, 1.0, return_mask=True)
+        tau = float(r.thresholds[0])
+        sp, _ = torch.sort(attn.float(), dim=-1, descending=True)
+        excl = torch.cumsum(sp, dim=-1) - sp
+        reached = [round((float(excl[0, 0, row, slots[row]]) - tau) / _ulp(tau)) for row in rows]
+        cases.append(dict(block_attn=attn.clone(), tau_min=0.35, tau_max=1.0, index=r.index, num=r.num, mask=r.mask,
+                          thresholds=r.thresholds, boundary_head=0, boundary_rows=torch.tensor(rows),
+                          boundary_slots=torch.tensor([slots[row] for row in rows]),
+                          boundary_ulps=torch.tensor(reached)))
     return cases
 
 
@@ -81,12 +136,22 @@ def attention_cases(ref):
     return cases
 
 
-def main(ref_root: str) -> None:
+WRITERS = {
+    "routing_gini.pt": routing_cases,
+    "hsa_attention.pt": attention_cases,
+    "routing_boundary.pt": routing_boundary_cases,
+}
+
+
+def main(ref_root: str, only=None) -> None:
     ref = load_reference_hsa(ref_root)
-    torch.save(routing_cases(ref), os.path.join(HERE, "routing_gini.pt"))
-    torch.save(attention_cases(ref), os.path.join(HERE, "hsa_attention.pt"))
-    print("wrote", os.listdir(HERE))
+    for name, make in WRITERS.items():
+        if only and name not in only:
+            continue
+        torch.save(make(ref), os.path.join(HERE, name))
+        print("wrote", name)
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    # python tests/golden/make_golden.py [reference root] [file names to write (default: all)]
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", sys.argv[2:])

@@ -116,8 +116,10 @@ def test_elu1_backward_matches_oracle_autograd(d):
     assert torch.count_nonzero(dq[:, :, 1]) == 0
 
 
-def _grads_both(cfg, gate_w, gate_b, do, proj=None):
-    """(GPU grads, oracle grads, GPU route, oracle route) of hsa_attention for one config."""
+def _grads_both(cfg, gate_w, gate_b, do, proj=None, keep_dtype=False):
+    """(GPU grads, oracle grads, oracle parts) of hsa_attention for one config. The oracle runs fp32
+    autograd on the same input values; the GPU gets fp32 copies, or (``keep_dtype``) the tensors
+    themselves, e.g. bf16 as the benchmark feeds them."""
     q, k, v = cfg["q"], cfg["k"], cfg["v"]
     d = q.shape[-1]
     kw = dict(block_size=cfg["block_size"], routing=cfg["routing"], topk=cfg.get("topk"),
@@ -134,7 +136,8 @@ def _grads_both(cfg, gate_w, gate_b, do, proj=None):
     with torch.no_grad():
         lin.weight.copy_(gate_w)
         lin.bias.copy_(gate_b)
-    qg, kg, vg = (t.detach().float().to(DEV).requires_grad_() for t in (q, k, v))
+    qg, kg, vg = ((t.detach().to(DEV) if keep_dtype else t.detach().float().to(DEV)).requires_grad_()
+                  for t in (q, k, v))
     out_g = W.hsa_attention(qg, kg, vg, k_proj_mat=proj.to(DEV), v_proj_mat=proj.to(DEV), gate_lin=lin, **kw)
     out_g.float().backward(do.to(DEV).float())
     return ((out_g, qg.grad, kg.grad, vg.grad, lin.weight.grad, lin.bias.grad),
@@ -167,14 +170,22 @@ def test_hsa_reference_mode_gradients_match_oracle():
         assert_close(g, r, *tol, what=name)
 
 
-def test_cfg5_wan_chunk_fwd_bwd_matches_oracle():
-    """cfg 5: Lq=4680, Lkv=32760, H=12, D=128, bf16, block 128, top-k 16 on 8 sparse heads + 4 elu1
-    heads; dO ~ N(0, 1). Compares dQ, dK, dV of both branches with the oracle's fp32 autograd."""
+@pytest.mark.parametrize("keep_dtype", [True, False], ids=["bf16", "fp32"])
+def test_cfg5_wan_chunk_fwd_bwd_matches_oracle(keep_dtype):
+    """cfg 5: Lq=4680, Lkv=32760, H=12, D=128, block 128, top-k 16 on 8 sparse heads + 4 elu1 heads;
+    dO ~ N(0, 1); a gate with N(0, 0.02) weights. Compares the output and dQ, dK, dV of both
+    branches with the oracle's fp32 autograd at max-abs 2e-2 / mean-abs 2e-3. ``bf16``: the bf16
+    tensors go in as the benchmark feeds them (bf16 elu1 state and key-side kernels, dK / dV written
+    once in bf16); ``fp32``: fp32 copies of the same values (the fp32 kernels)."""
     cfg = workloads.cfg5()
     d = cfg["q"].shape[-1]
-    got, want, parts = _grads_both(cfg, torch.zeros(d, d), torch.zeros(d), cfg["do"])
-    for name, g, r in zip(("out", "dq", "dk", "dv"), got[:4], want[:4]):
-        assert_close(g, r, what=f"cfg5 {name}")
+    g = torch.Generator().manual_seed(5)
+    gate_w = torch.randn(d, d, generator=g) * 0.02
+    got, want, parts = _grads_both(cfg, gate_w, torch.zeros(d), cfg["do"], keep_dtype=keep_dtype)
+    if keep_dtype:
+        assert got[2].dtype == got[3].dtype == torch.bfloat16
+    for name, gg, r in zip(("out", "dq", "dk", "dv"), got[:4], want[:4]):
+        assert_close(gg, r, what=f"cfg5 {name}")
 
 
 def test_bf16_dk_dv_are_the_fp32_gradients_rounded():
@@ -234,4 +245,4 @@ def test_hsa_bf16_inputs_get_bf16_gradients_within_tolerance():
     W.hsa_attention(qg, kg, vg, k_proj_mat=None, v_proj_mat=None, **kw).float().backward(do.to(DEV))
     assert kg.grad.dtype == vg.grad.dtype == torch.bfloat16
     for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
-        assert_close(g, r, 3e-2, 3e-3, what=f"bf16 {name}")
+        assert_close(g, r, what=f"bf16 {name}")

@@ -61,13 +61,35 @@ def test_pooling_jobs_in_one_launch_equal_separate_launches():
         assert torch.equal(g[:, heads.long()], want[:, heads.long()])
 
 
-def test_gini_routing_is_bit_exact_on_reference_golden_maps():
-    for c in torch.load(os.path.join(GOLDEN, "routing_gini.pt"), weights_only=True):
+@pytest.mark.parametrize("fixture", ["routing_gini.pt", "routing_boundary.pt"])
+def test_gini_routing_is_bit_exact_on_reference_golden_maps(fixture):
+    """Thresholds, counts, permutations and masks equal the reference's bit for bit, including the
+    rows whose exclusive prefix sits within 3 fp32 ulp of the threshold (the row Gini sums and the
+    head mean follow torch's CPU fp32 summation order)."""
+    for c in torch.load(os.path.join(GOLDEN, fixture), weights_only=True):
         r = W.build_block_routing(c["block_attn"].to(DEV), c["tau_min"], c["tau_max"], return_mask=True)
+        assert torch.equal(r.thresholds.cpu(), c["thresholds"])
         assert torch.equal(r.index.cpu(), c["index"])
         assert torch.equal(r.num.cpu(), c["num"])
         assert torch.equal(r.mask.cpu(), c["mask"])
-        assert torch.allclose(r.thresholds.cpu(), c["thresholds"], rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("shape", [(1, 12, 37, 256), (3, 2, 9, 40), (2, 1, 11, 16), (5, 9, 1, 64), (6, 3, 1, 17),
+                                   (17, 33, 1, 16), (5, 6, 1, 16), (1, 3, 5, 1000)])
+def test_gini_thresholds_equal_torch_fp32_reductions(shape):
+    """Thresholds equal the reference formula evaluated by torch on the CPU (fp32 sum over blocks,
+    fp32 mean over batch and query blocks), over shapes that take each reduction path: contiguous
+    runs of >= 8 and < 8 elements, a single head, a single query block with heads grouped by 4 /
+    32 or not."""
+    torch.manual_seed(sum(shape))
+    attn = torch.softmax(torch.randn(shape) * 3, -1)
+    b, h, nq, n = shape
+    sp, _ = torch.sort(attn, dim=-1, descending=True)
+    ranks = torch.arange(1, n + 1, dtype=torch.float32)
+    gini = torch.sum((n + 1 - 2 * ranks) * sp, dim=-1) / n
+    want = 0.35 + gini.mean(dim=(0, 2)) * (1.0 - 0.35)
+    got = W.build_block_routing(attn.to(DEV), 0.35, 1.0).thresholds.cpu()
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("nkv", [16, 37, 256, 512, 1100])

@@ -27,6 +27,33 @@ def test_routing_matches_reference_golden_vectors_bit_exactly():
         assert torch.equal(r.mask, c["mask"])
 
 
+def _f32_ulp(x: float) -> float:
+    return 2.0 ** (math.frexp(abs(x))[1] - 24)
+
+
+def test_routing_matches_reference_boundary_goldens():
+    """Rows whose exclusive prefix lies -3..+3 fp32 ulp from the head threshold (crafted with the
+    reference itself): num there depends on the threshold's last bits, and the oracle reproduces
+    the reference's count on every row."""
+    cases = torch.load(os.path.join(GOLDEN, "routing_boundary.pt"), weights_only=True)
+    assert len(cases) == 2
+    for c in cases:
+        r = O.build_block_routing(c["block_attn"], c["tau_min"], c["tau_max"], return_mask=True)
+        assert torch.equal(r.thresholds, c["thresholds"])
+        assert torch.equal(r.num, c["num"]) and torch.equal(r.index, c["index"]) and torch.equal(r.mask, c["mask"])
+        # the fixture does what it claims: the listed slots sit within 3 ulp of the threshold
+        h = int(c["boundary_head"])
+        tau = float(c["thresholds"][h])
+        sp, _ = torch.sort(c["block_attn"].float(), dim=-1, descending=True)
+        excl = torch.cumsum(sp, dim=-1) - sp
+        for row, slot, ulps in zip(c["boundary_rows"].tolist(), c["boundary_slots"].tolist(),
+                                   c["boundary_ulps"].tolist()):
+            off = (float(excl[0, h, row, slot]) - tau) / _f32_ulp(tau)
+            assert abs(off) <= 3 and round(off) == ulps
+            # num is the first slot whose exclusive prefix reaches the threshold
+            assert (int(c["num"][0, h, row]) > slot) == (off < 0)
+
+
 def test_hsa_attention_matches_reference_golden_vectors():
     """Same routing and rounding points as the reference: at least 99.9% of output elements are
     bit-identical; the rest differ by one rounding step of the output dtype (the sparse matmuls

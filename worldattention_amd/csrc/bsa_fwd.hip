@@ -1,10 +1,12 @@
 // Block-sparse flash-attention forward for gfx950 (bf16 MFMA 32x32x16, fp32 accumulation).
 //
 // Work decomposition. A "row" is one (batch, head, query block) with its list of key blocks
-// index[b,h,i,0:num]. A row's list is cut into splits of `split` consecutive visits; one workgroup
-// processes one (row, split) unit and writes a normalized partial output plus its log2-sum-exp to
-// the workspace. A second kernel merges the partials of each row in split order, applies the
-// fusion epilogue and writes the output, so every result is independent of scheduling.
+// index[b,h,i,0:num]. A row's list is cut into up to max_splits units of at most `split` visits;
+// one workgroup processes one (row, split) unit. A row with one unit writes its output directly.
+// The units of a longer row write a normalized partial output plus its log2-sum-exp to the
+// workspace and count their arrival on a per-row counter; the last unit to arrive merges every
+// partial in split order, applies the fusion epilogue and writes the row, so every result is
+// independent of scheduling (one launch, no merge kernel).
 //
 // Unit kernel (one workgroup = BS/32 waves; wave w owns query rows [32w, 32w+32) of the block).
 // Per visited key block the K and V tiles are streamed global -> LDS with direct-to-LDS loads

@@ -154,6 +154,81 @@ __device__ bool clear_unrouted(const RouteParams& p) {
   return true;
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp32 sums in the order of torch's CPU reduction kernel (aten/src/ATen/native/cpu/SumKernel.cpp,
+// cascade_sum), which computes the reference's Gini sums and head means (routing.py:99-101):
+//   * cascade: one accumulator chain over n elements, pushed up a 4-level cascade every 2^p
+//     elements (p = max(4, ceil(log2 n) / 4)) and folded at the end (multi_row_sum);
+//   * row_sum: 4 interleaved cascades over n / 4 groups, the tail added to the first, then the
+//     four folded in order;
+//   * inner_sum: a contiguous run of n >= 8 is summed as 8 lanes (lane l = row_sum of elements
+//     l, l + 8, ...), then the scalar tail and the 8 lanes are added one by one to 0; n < 8 uses
+//     row_sum directly.
+// One thread evaluates these sequentially with round-to-nearest adds (no contraction or
+// reassociation), so the result is bit-identical to the reference's fp32 value.
+// ---------------------------------------------------------------------------------------------
+__device__ int tc_ceil_log2(int n) {
+  if (n <= 2) return 1;
+  return 32 - __clz((unsigned)(n - 1));
+}
+
+template <typename Load>
+__device__ float tc_cascade(const Load& x, int start, int stride, int n) {
+  const int power = max(4, tc_ceil_log2(n) / 4);
+  const int step = 1 << power, mask = step - 1;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int i = 0;
+  while (i + step <= n) {
+    for (int j = 0; j < step; ++j, ++i) acc[0] = __fadd_rn(acc[0], x(start + i * stride));
+    for (int j = 1; j < 4; ++j) {
+      acc[j] = __fadd_rn(acc[j], acc[j - 1]);
+      acc[j - 1] = 0.f;
+      if ((i & (mask << (j * power))) != 0) break;
+    }
+  }
+  for (; i < n; ++i) acc[0] = __fadd_rn(acc[0], x(start + i * stride));
+  for (int j = 1; j < 4; ++j) acc[0] = __fadd_rn(acc[0], acc[j]);
+  return acc[0];
+}
+
+template <typename Load>
+__device__ float tc_row_sum(const Load& x, int start, int stride, int n) {
+  const int groups = n / 4;
+  float part[4];
+  for (int k = 0; k < 4; ++k) part[k] = tc_cascade(x, start + k * stride, 4 * stride, groups);
+  for (int i = groups * 4; i < n; ++i) part[0] = __fadd_rn(part[0], x(start + i * stride));
+  for (int k = 1; k < 4; ++k) part[0] = __fadd_rn(part[0], part[k]);
+  return part[0];
+}
+
+template <typename Load>
+__device__ float tc_inner_sum(const Load& x, int start, int n) {
+  constexpr int L = 8;
+  if (n < L) return tc_row_sum(x, start, 1, n);
+  const int nv = n / L;
+  float fin = 0.f;
+  for (int k = nv * L; k < n; ++k) fin = __fadd_rn(fin, x(start + k));
+  for (int l = 0; l < L; ++l) fin = __fadd_rn(fin, tc_row_sum(x, start + l, L, nv));
+  return fin;
+}
+
+// Sum over (batch, query block) of one head's row Ginis g[(b * H + h) * Nq + i], as torch sums
+// a [B, H, Nq] tensor over dims (0, 2): with H == 1 the two dims merge into one contiguous run;
+// with Nq == 1 it is an outer reduction over b of column h (columns in groups of 32 when H >= 8,
+// of 4 when H < 8, take one cascade each; the other columns a row_sum); otherwise the per-batch
+// inner sums over Nq are added in batch order.
+template <typename Load>
+__device__ float tc_head_sum(const Load& g, int B, int H, int Nq, int h) {
+  if (H == 1) return tc_inner_sum(g, 0, B * Nq);
+  if (Nq == 1) {
+    const int grouped = H >= 8 ? H / 32 * 32 : H / 4 * 4;
+    return h < grouped ? tc_cascade(g, h, H, B) : tc_row_sum(g, h, H, B);
+  }
+  float s = 0.f;
+  for (int b = 0; b < B; ++b) s = __fadd_rn(s, tc_inner_sum(g, (b * H + h) * Nq, Nq));
+  return s;
+}
+
 __device__ __forceinline__ float key_to_float(uint64_t key) {
   const uint32_t u = (uint32_t)(key >> 32);
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u);
@@ -272,15 +347,29 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
       for (int m = tid; m < N; m += 256) mrow[(int32_t)(0xFFFFFFFFu - (uint32_t)keys[m])] = m < n ? 1 : 0;
     }
   } else {
-    double gs = 0.0;
-    for (int m = tid; m < N; m += 256) {
-      const float pm = key_to_float(keys[m]);
-      p.ws_sorted[row * N + m] = pm;
-      const float coef = (float)(N + 1 - 2 * (m + 1));
-      gs += (double)(coef * pm);
+    // Gini terms (N + 1 - 2 m) p_(m), each rounded to fp32 as the reference's product tensor is,
+    // then their sum in the reference's fp32 order, divided by N in fp32
+    float terms[16];
+    for (int e = 0; e < per; ++e) {
+      const int m = tid + e * 256;
+      terms[e] = 0.f;
+      if (m < N) {
+        const float pm = key_to_float(keys[m]);
+        p.ws_sorted[row * N + m] = pm;
+        terms[e] = __fmul_rn((float)(N + 1 - 2 * (m + 1)), pm);
+      }
     }
-    gs = block_reduce_sum_d(gs, dscratch);
-    if (tid == 0) p.ws_gini[row] = (float)gs / (float)N;
+    __syncthreads();  // every key read: the buffer takes the terms
+    float* tl = (float*)keys;
+    for (int e = 0; e < per; ++e) {
+      const int m = tid + e * 256;
+      if (m < N) tl[m] = terms[e];
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const float s = tc_inner_sum([&](int m) { return tl[m]; }, 0, N);
+      p.ws_gini[row] = __fdiv_rn(s, (float)N);
+    }
   }
 }
 
@@ -471,14 +560,15 @@ __global__ void __launch_bounds__(64) gini_count_kernel(RouteParams p) {
   const int64_t row = ((int64_t)b * p.H + h) * p.Nq + i;
   const int N = p.Nkv;
 
-  double s = 0.0;
-  for (int r = lane; r < p.B * p.Nq; r += 64) {
-    const int bb = r / p.Nq, ii = r % p.Nq;
-    s += (double)p.ws_gini[((int64_t)bb * p.H + h) * p.Nq + ii];
+  // the head's mean Gini in the reference's fp32 order (one lane), then the threshold
+  float thr = 0.f;
+  if (lane == 0) {
+    const float* gw = p.ws_gini;
+    const float s = tc_head_sum([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h);
+    const float mean = __fdiv_rn(s, (float)(p.B * p.Nq));
+    thr = __fadd_rn(p.tau_min, __fmul_rn(mean, p.tau_span));
   }
-  s = wa_wave_sum_d(s);
-  const float mean = (float)(s / (double)(p.B * p.Nq));
-  const float thr = __fadd_rn(p.tau_min, __fmul_rn(mean, p.tau_span));
+  thr = __shfl(thr, 0, 64);
   if (b == 0 && i == 0 && lane == 0) p.thresholds[h] = thr;
 
   for (int m = lane; m < N; m += 64) sp[m] = p.ws_sorted[row * N + m];

@@ -188,6 +188,22 @@ def cfg3(device, seed: int = 0, layers: int = 4, history_frames: int = 120, resi
                 topk=[16 if m == "sparse" else 0 for m in modes], linear_mode="elu1")
 
 
+def cfg4_layer(seed: int = 0, heads: int = 40, d: int = 128, q_len: int = 3 * FRAME_TOKENS,
+               kv_len: int = 28080 + 3 * FRAME_TOKENS, dtype=torch.bfloat16) -> dict:
+    """One H=40 HSA layer call of the cfg 4 stack with seeded N(0,1) activations (CPU tensors):
+    q ``[1, 4680, 40, 128]``, k / v ``[1, 32760, 40, 128]``, heads 0..29 sparse (top-16), 30..39
+    elu1 linear. The stack's projections of N(0,1) inputs by 1/sqrt(dim)-scaled weights give
+    unit-variance q / k / v, which is what this draws directly."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, q_len, heads, d, generator=g).to(dtype)
+    k = torch.randn(1, kv_len, heads, d, generator=g).to(dtype)
+    v = torch.randn(1, kv_len, heads, d, generator=g).to(dtype)
+    n_sparse = heads * 3 // 4
+    modes = ["sparse"] * n_sparse + ["linear"] * (heads - n_sparse)
+    return dict(q=q, k=k, v=v, block_size=128, routing="topk", topk=[16 if m == "sparse" else 0 for m in modes],
+                head_modes=modes, linear_mode="elu1", proj_segment_len=FRAME_TOKENS)
+
+
 def cfg4(device, seed: int = 0, layers: int = 40, heads: int = 40, d: int = 128, history: int = 28080,
          chunk: int = 3 * FRAME_TOKENS) -> dict:
     """Wan-14B stack workload (see the module docstring): weights and caches on ``device``."""
