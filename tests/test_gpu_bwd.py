@@ -119,7 +119,7 @@ def test_elu1_backward_matches_oracle_autograd(d):
 def _grads_both(cfg, gate_w, gate_b, do, proj=None, keep_dtype=False):
     """(GPU grads, oracle grads, oracle parts) of hsa_attention for one config. The oracle runs fp32
     autograd on the same input values; the GPU gets fp32 copies, or (``keep_dtype``) the tensors
-    themselves, e.g. bf16 as the benchmark feeds them."""
+    themselves, e.g. bf16 as the benchmark feeds them, and then so does the oracle's forward."""
     q, k, v = cfg["q"], cfg["k"], cfg["v"]
     d = q.shape[-1]
     kw = dict(block_size=cfg["block_size"], routing=cfg["routing"], topk=cfg.get("topk"),
@@ -129,7 +129,11 @@ def _grads_both(cfg, gate_w, gate_b, do, proj=None, keep_dtype=False):
         proj = O.init_projection(rank, cfg["proj_segment_len"], cfg["block_size"])
     qr, kr, vr = (t.detach().float().clone().requires_grad_() for t in (q, k, v))
     wr, br = gate_w.clone().requires_grad_(), gate_b.clone().requires_grad_()
-    out_r, parts = O.hsa_attention(qr, kr, vr, k_proj_mat=proj, v_proj_mat=proj, gate_weight=wr, gate_bias=br,
+    # With keep_dtype the oracle's forward sees the inputs in their own dtype too (bf16 inputs make
+    # the reference round the pooled block means to bf16, which decides the routing), while its
+    # math runs in fp32 and the gradients reach the fp32 leaves through the casts.
+    qi, ki, vi = (t.to(s.dtype) for t, s in zip((qr, kr, vr), (q, k, v))) if keep_dtype else (qr, kr, vr)
+    out_r, parts = O.hsa_attention(qi, ki, vi, k_proj_mat=proj, v_proj_mat=proj, gate_weight=wr, gate_bias=br,
                                    return_parts=True, **kw)
     out_r.float().backward(do.float())
     lin = torch.nn.Linear(d, d).to(DEV)
@@ -240,7 +244,7 @@ def test_hsa_bf16_inputs_get_bf16_gradients_within_tolerance():
     q16, k16, v16 = (t.bfloat16() for t in (q, k, v))
     do = torch.randn(q.shape)
     qr, kr, vr = (t.float().requires_grad_() for t in (q16, k16, v16))
-    O.hsa_attention(qr, kr, vr, **kw).float().backward(do)
+    O.hsa_attention(qr.bfloat16(), kr.bfloat16(), vr.bfloat16(), **kw).float().backward(do)
     qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q16, k16, v16))
     W.hsa_attention(qg, kg, vg, k_proj_mat=None, v_proj_mat=None, **kw).float().backward(do.to(DEV))
     assert kg.grad.dtype == vg.grad.dtype == torch.bfloat16

@@ -4,7 +4,8 @@ H = 40 layer call of the Wan-14B stack) and cfg 3 (the HKV tier at its real page
 
 Tolerances: attention outputs max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle; routing
 and page selections bit-exact given identical scores; page summaries within fp32 reduction-order
-noise; installed keys within one bf16 ulp of the oracle's re-rope, values bit-exact.
+noise; installed keys within one bf16 ulp (plus the fp32 product error where a rotation cancels)
+of the oracle's re-rope, values bit-exact.
 """
 import pytest
 import torch
@@ -61,6 +62,25 @@ def check_topk_routing(route, parts, ks, heads, what, tie_rel=1e-5, max_tie_rows
         assert torch.equal(same_scores.index.cpu()[:, h, :, :k], want.index[:, h, :, :k]), f"{what}: head {h}"
         assert torch.equal(same_scores.num.cpu()[:, h], want.num[:, h])
     return swapped
+
+
+def within_bf16_of_rotation(got, want, what):
+    """Rotated bf16 keys: both sides form the fp32 complex product of a key pair and a unit factor
+    (error up to ~2^-21 of the pair's magnitude, depending on how each side fuses the products) and
+    round it to bf16, so they may differ by one bf16 ulp of the value plus that fp32 error (which
+    dominates where the product cancels to near zero)."""
+    g, w = got.detach().cpu().float(), want.detach().cpu().float()
+    pair = w.reshape(*w.shape[:-1], w.shape[-1] // 2, 2).norm(dim=-1)
+    mag = pair.repeat_interleave(2, dim=-1)
+    tol = w.abs() * 2.0 ** -7 + mag * 2.0 ** -20
+    bad = (g - w).abs() > tol
+    if bad.any():
+        i = torch.nonzero(bad)[0].tolist()
+        raise AssertionError(f"{what}: {int(bad.sum())} elements beyond one bf16 ulp (first {i}: "
+                             f"{g[tuple(i)].item():.6g} vs {w[tuple(i)].item():.6g}, pair magnitude "
+                             f"{mag[tuple(i)].item():.4g})")
+    frac = (g != w).float().mean().item()
+    assert frac < 0.01, f"{what}: {frac:.3%} of elements differ"
 
 
 def hsa_both(q, k, v, cfg, gate_w=None, gate_b=None):
@@ -176,11 +196,7 @@ def test_cfg3_hkv_page_geometry_through_the_cache_api():
     for i, f in enumerate(frames):
         src_k = host_k[:, f * ft:(f + 1) * ft]
         want_k = OK.shift_temporal_rope(src_k, band_cpu, base - nret + i, f)
-        g = got_k[:, i * ft:(i + 1) * ft].float()
-        w = want_k.float()
-        ulp = torch.where(w == 0, torch.full_like(w, 2.0 ** -133), w.abs() * 2.0 ** -7)
-        assert not ((g - w).abs() > ulp).any(), f"page {f}: re-roped keys beyond one bf16 ulp"
-        assert (g != w).float().mean().item() < 0.01
+        within_bf16_of_rotation(got_k[:, i * ft:(i + 1) * ft], want_k, f"page {f}: re-roped keys")
         assert torch.equal(got_v[:, i * ft:(i + 1) * ft], host_v[:, f * ft:(f + 1) * ft]), f"page {f}: values"
 
     # the HSA call over the 21,840-token pool (171 key blocks, the last with 80 real tokens)

@@ -183,7 +183,7 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
           if (p.gate_pre_bf16) pr = wa_bf16_round(pr);
           float gs = wa_sigmoid(pr);
           if (p.gate_out_bf16) gs = wa_bf16_round(gs);
-          a = p.epilogue == WA_EPI_FUSE ? __fadd_rn(a, __fmul_rn(xv[rq][i], gs)) : __fmul_rn(a, gs);
+          a = p.epilogue == WA_EPI_FUSE ? wa_add_rn(a, wa_mul_rn(xv[rq][i], gs)) : wa_mul_rn(a, gs);
         }
         val[i] = a;
       }

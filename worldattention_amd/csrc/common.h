@@ -49,6 +49,27 @@ static inline bool wa_aligned16(const void* p) { return (((uintptr_t)p) & 15u) =
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float wa_bf16_round(float x) { return (float)(bf16_t)x; }
 
+// Single-rounding fp32 operations that the compiler may not fuse with a neighbouring multiply or
+// add: HIP's __fadd_rn / __fmul_rn are plain operators, which the default -ffp-contract=fast turns
+// into fused multiply-adds (one rounding instead of two). Used where results must round as the
+// reference's separate torch operations do.
+__device__ __forceinline__ float wa_add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ float wa_sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+__device__ __forceinline__ float wa_mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float wa_div_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a / b;
+}
+
 __device__ __forceinline__ float wa_load_f(const void* p, int64_t i, int dtype) {
   return dtype == WA_BF16 ? (float)((const bf16_t*)p)[i] : ((const float*)p)[i];
 }

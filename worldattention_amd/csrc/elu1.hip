@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(512) elu1_readout_kernel(ReadoutParams p) {
           if (pre_bf) pr = wa_bf16_round(pr);
           float gs = wa_sigmoid(pr);
           if (gout_bf) gs = wa_bf16_round(gs);
-          a = __fmul_rn(a, gs);
+          a = wa_mul_rn(a, gs);
         }
         val[i] = a;
       }

@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(256) fuse_fwd_kernel(FuseParams p) {
           if (p.gate_out_bf16) gv = wa_bf16_round(gv);
           gs[i] = gv;
           const float l = p.lin_round_bf16 ? wa_bf16_round(lv[tt][rq][i]) : lv[tt][rq][i];
-          val[i] = (mode & MODE_SPARSE) ? __fadd_rn(val[i], __fmul_rn(l, gs[i])) : __fmul_rn(l, gs[i]);
+          val[i] = (mode & MODE_SPARSE) ? wa_add_rn(val[i], wa_mul_rn(l, gs[i])) : wa_mul_rn(l, gs[i]);
         }
         if (p.gate) *(f32x4*)(p.gate + (int64_t)b * p.g_sb + (int64_t)t * p.g_st + (int64_t)h * p.g_sh + d0) = gs;
       }

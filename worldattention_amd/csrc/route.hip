@@ -179,15 +179,15 @@ __device__ float tc_cascade(const Load& x, int start, int stride, int n) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   int i = 0;
   while (i + step <= n) {
-    for (int j = 0; j < step; ++j, ++i) acc[0] = __fadd_rn(acc[0], x(start + i * stride));
+    for (int j = 0; j < step; ++j, ++i) acc[0] = wa_add_rn(acc[0], x(start + i * stride));
     for (int j = 1; j < 4; ++j) {
-      acc[j] = __fadd_rn(acc[j], acc[j - 1]);
+      acc[j] = wa_add_rn(acc[j], acc[j - 1]);
       acc[j - 1] = 0.f;
       if ((i & (mask << (j * power))) != 0) break;
     }
   }
-  for (; i < n; ++i) acc[0] = __fadd_rn(acc[0], x(start + i * stride));
-  for (int j = 1; j < 4; ++j) acc[0] = __fadd_rn(acc[0], acc[j]);
+  for (; i < n; ++i) acc[0] = wa_add_rn(acc[0], x(start + i * stride));
+  for (int j = 1; j < 4; ++j) acc[0] = wa_add_rn(acc[0], acc[j]);
   return acc[0];
 }
 
@@ -196,8 +196,8 @@ __device__ float tc_row_sum(const Load& x, int start, int stride, int n) {
   const int groups = n / 4;
   float part[4];
   for (int k = 0; k < 4; ++k) part[k] = tc_cascade(x, start + k * stride, 4 * stride, groups);
-  for (int i = groups * 4; i < n; ++i) part[0] = __fadd_rn(part[0], x(start + i * stride));
-  for (int k = 1; k < 4; ++k) part[0] = __fadd_rn(part[0], part[k]);
+  for (int i = groups * 4; i < n; ++i) part[0] = wa_add_rn(part[0], x(start + i * stride));
+  for (int k = 1; k < 4; ++k) part[0] = wa_add_rn(part[0], part[k]);
   return part[0];
 }
 
@@ -207,8 +207,8 @@ __device__ float tc_inner_sum(const Load& x, int start, int n) {
   if (n < L) return tc_row_sum(x, start, 1, n);
   const int nv = n / L;
   float fin = 0.f;
-  for (int k = nv * L; k < n; ++k) fin = __fadd_rn(fin, x(start + k));
-  for (int l = 0; l < L; ++l) fin = __fadd_rn(fin, tc_row_sum(x, start + l, L, nv));
+  for (int k = nv * L; k < n; ++k) fin = wa_add_rn(fin, x(start + k));
+  for (int l = 0; l < L; ++l) fin = wa_add_rn(fin, tc_row_sum(x, start + l, L, nv));
   return fin;
 }
 
@@ -225,7 +225,7 @@ __device__ float tc_head_sum(const Load& g, int B, int H, int Nq, int h) {
     return h < grouped ? tc_cascade(g, h, H, B) : tc_row_sum(g, h, H, B);
   }
   float s = 0.f;
-  for (int b = 0; b < B; ++b) s = __fadd_rn(s, tc_inner_sum(g, (b * H + h) * Nq, Nq));
+  for (int b = 0; b < B; ++b) s = wa_add_rn(s, tc_inner_sum(g, (b * H + h) * Nq, Nq));
   return s;
 }
 
@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
       if (m < N) {
         const float pm = key_to_float(keys[m]);
         p.ws_sorted[row * N + m] = pm;
-        terms[e] = __fmul_rn((float)(N + 1 - 2 * (m + 1)), pm);
+        terms[e] = wa_mul_rn((float)(N + 1 - 2 * (m + 1)), pm);
       }
     }
     __syncthreads();  // every key read: the buffer takes the terms
@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
     __syncthreads();
     if (tid == 0) {
       const float s = tc_inner_sum([&](int m) { return tl[m]; }, 0, N);
-      p.ws_gini[row] = __fdiv_rn(s, (float)N);
+      p.ws_gini[row] = wa_div_rn(s, (float)N);
     }
   }
 }
@@ -560,13 +560,14 @@ __global__ void __launch_bounds__(64) gini_count_kernel(RouteParams p) {
   const int64_t row = ((int64_t)b * p.H + h) * p.Nq + i;
   const int N = p.Nkv;
 
-  // the head's mean Gini in the reference's fp32 order (one lane), then the threshold
+  // the head's mean Gini in the reference's fp32 order (one lane), then the threshold (the
+  // product and the sum round separately, as the reference's two tensor operations do)
   float thr = 0.f;
   if (lane == 0) {
     const float* gw = p.ws_gini;
     const float s = tc_head_sum([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h);
-    const float mean = __fdiv_rn(s, (float)(p.B * p.Nq));
-    thr = __fadd_rn(p.tau_min, __fmul_rn(mean, p.tau_span));
+    const float mean = wa_div_rn(s, (float)(p.B * p.Nq));
+    thr = wa_add_rn(p.tau_min, wa_mul_rn(mean, p.tau_span));
   }
   thr = __shfl(thr, 0, 64);
   if (b == 0 && i == 0 && lane == 0) p.thresholds[h] = thr;
@@ -579,7 +580,7 @@ __global__ void __launch_bounds__(64) gini_count_kernel(RouteParams p) {
     for (int m = 0; m < N; ++m) {
       const float pm = sp[m];
       c += (double)pm;
-      const float excl = __fsub_rn((float)c, pm);
+      const float excl = wa_sub_rn((float)c, pm);
       const bool keep = excl < thr;
       count += keep;
       sp[m] = keep ? 1.f : 0.f;
