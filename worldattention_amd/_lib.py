@@ -12,8 +12,12 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_void_p
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libworldattention_amd.so")
+# WORLDATTENTION_AMD_LIB selects another build of the library (e.g. to compare two builds); the
+# default is the in-tree build next to this file
+LIB_PATH = os.environ.get("WORLDATTENTION_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                                   "libworldattention_amd.so")
 
+WA_OK, WA_ERR_ARG, WA_ERR_UNSUPPORTED = 0, -1, -2
 WA_F32, WA_BF16 = 0, 1
 WA_ROUTE_GINI, WA_ROUTE_TOPK = 0, 1
 WA_EPI_PLAIN, WA_EPI_FUSE, WA_EPI_GATED = 0, 1, 2
