@@ -3,8 +3,9 @@
  *
  * Every entry point takes plain device pointers, element strides and sizes, launches on the
  * caller's HIP stream (`stream` is a hipStream_t passed as void*), allocates nothing and keeps no
- * global device state. Inputs, outputs and workspaces are owned by the caller; workspace sizes
- * come from the matching *_workspace_bytes query.
+ * global device state, except wa_bsa_fwd_noalloc, whose workspace is a static device array of the
+ * library. Inputs, outputs and workspaces are owned by the caller; workspace sizes come from the
+ * matching *_workspace_bytes query.
  *
  * Return value: WA_OK (0) on success; a negative WA_ERR_* for argument errors; a positive
  * hipError_t for runtime failures. wa_last_error() returns the calling thread's last message.
@@ -154,6 +155,18 @@ typedef struct wa_bsa_fwd_args {
 int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t split_visits, int64_t block_size,
                                    int64_t D);
 int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
+
+/* wa_bsa_fwd that allocates nothing and takes no workspace. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The split partials and arrival counters live in a
+ * static device array of the library, WA_BSA_FWD_NOALLOC_SCRATCH_BYTES per GPU, held from the
+ * library's first use on that GPU until the process ends. args->workspace and args->arrivals must
+ * be NULL; a launch whose wa_bsa_fwd_workspace_bytes exceeds the array is rejected (WA_ERR_ARG)
+ * before anything runs. The counters are cleared by a fill kernel at the start of every call. All
+ * calls on one GPU share its array, so calls that overlap on one GPU (on different streams) race;
+ * calls in one stream are ordered and safe. Results equal wa_bsa_fwd's bit for bit. */
+#define WA_BSA_FWD_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* args, void* stream);
 
 /* Backward of wa_bsa_fwd: dQ, dK, dV (fp32, BLHD) of the block-sparse attention output o.
  * Replaces _bwd_preprocess/_bwd_kernel/_backward, wan/modules/hsa/block_sparse_triton.py:142-368

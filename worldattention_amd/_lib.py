@@ -63,6 +63,7 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
 ])
 
 BSA_DEFAULT_SPLIT = 16
+BSA_FWD_NOALLOC_SCRATCH_BYTES = 64 << 20   # WA_BSA_FWD_NOALLOC_SCRATCH_BYTES
 
 CompressArgs = _struct("wa_compress_args", [
     ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
@@ -191,6 +192,7 @@ SIGNATURES = {
     "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "wa_bsa_fwd_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
+    "wa_bsa_fwd_noalloc": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_compress_kv": (c_int, [POINTER(CompressArgs), c_void_p]),
     "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_elu1_state": (c_int, [POINTER(Elu1StateArgs), c_void_p]),

@@ -24,6 +24,8 @@
 // Reference semantics: wan/modules/hsa/block_sparse_triton.py:67-139 (online softmax, partial
 // trailing block mask, empty list -> 0, LSE output) and block_sparse_torch.py:16-64 (id clamping,
 // listed order, duplicates attended twice, fp32 math).
+#include <mutex>
+
 #include "common.h"
 #include "tile.h"
 
@@ -693,29 +695,106 @@ int launch(const FwdParams& fp, int64_t rows, bool cleared, hipStream_t stream) 
   return wa_launch_status("bsa_fwd_unit");
 }
 
-int64_t split_slots(int64_t rows, int64_t max_visits, int64_t split) {
-  const int64_t ms = max_visits > 0 ? (max_visits + split - 1) / split : 1;
-  return rows * ms;
+// Workspace layout: the split partials (fp32 [rows * max_splits][BS][D] outputs, then
+// [rows * max_splits][BS] log2-sum-exps; only when a row can take more than one unit), then the
+// int32 arrival counters [rows], each region starting on a 256-byte boundary.
+int64_t partial_bytes(int64_t rows, int64_t max_splits, int64_t block_size, int64_t D) {
+  return max_splits > 1 ? (rows * max_splits * block_size * (D + 1) * 4 + 255) / 256 * 256 : 0;
 }
+
+int64_t max_splits_of(int64_t max_visits, int64_t split) {
+  return max_visits > 0 ? (max_visits + split - 1) / split : 1;
+}
+
+int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream);
 
 }  // namespace
 
 extern "C" int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t split, int64_t block_size,
                                               int64_t D) {
   if (split <= 0) split = WA_BSA_DEFAULT_SPLIT;
-  const int64_t slots = split_slots(rows, max_visits, split);
-  return ((slots * block_size * (D + 1)) * 4 + 255) / 256 * 256 + (rows * 4 + 255) / 256 * 256;
+  return partial_bytes(rows, max_splits_of(max_visits, split), block_size, D) + (rows * 4 + 255) / 256 * 256;
 }
 
 extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
   WA_CHECK_ARG(a != nullptr, "wa_bsa_fwd: null args");
+  return bsa_fwd_impl(a, a->workspace, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// wa_bsa_fwd_noalloc: the same launch with its workspace in a static device array of this library
+// (one copy per GPU, allocated when the library's code is loaded on that GPU), for callers that
+// cannot allocate device memory. The array's host-side name only stands for the symbol: its device
+// address is looked up once per device with hipGetSymbolAddress and used from then on.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[WA_BSA_FWD_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that runs `stream` (the current device for the null
+// stream), looked up on the first call for that device with the device current.
+int scratch_address(void* stream, void** out) {
+  int cur = 0;
+  WA_CHECK_HIP(hipGetDevice(&cur));
+  int dev = cur;
+  if (stream) WA_CHECK_HIP(hipStreamGetDevice((hipStream_t)stream, &dev));
+  WA_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "wa_bsa_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur) WA_CHECK_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) WA_CHECK_HIP(hipSetDevice(cur));
+    if (e != hipSuccess || p == nullptr)
+      return wa_fail(e != hipSuccess ? (int)e : WA_ERR_UNSUPPORTED, "wa_bsa_fwd_noalloc: hipGetSymbolAddress: %s",
+                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return WA_OK;
+}
+
+}  // namespace
+
+extern "C" int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* a, void* stream) {
+  WA_CHECK_ARG(a != nullptr, "wa_bsa_fwd_noalloc: null args");
+  WA_CHECK_ARG(a->workspace == nullptr && a->arrivals == nullptr,
+               "wa_bsa_fwd_noalloc: workspace and arrivals must be NULL (the static scratch array holds both)");
+  WA_CHECK_ARG(a->D > 0 && a->block_size > 0 && a->B >= 0 && a->H > 0 && a->Lq >= 0 && a->Lkv > 0,
+               "wa_bsa_fwd_noalloc: bad sizes");
+  const int64_t nq = (a->Lq + a->block_size - 1) / a->block_size;
+  const int64_t nkv = (a->Lkv + a->block_size - 1) / a->block_size;
+  const int64_t nh = a->heads ? a->n_heads : a->H;
+  const int64_t rows = a->B * nh * nq;
+  const int64_t split = a->split_visits > 0 ? a->split_visits : WA_BSA_DEFAULT_SPLIT;
+  const int64_t width = a->index ? a->index_width : nkv;
+  const int64_t max_visits = a->max_visits > 0 ? (a->max_visits < width ? a->max_visits : width) : width;
+  const int64_t need = wa_bsa_fwd_workspace_bytes(rows, max_visits, split, a->block_size, a->D);
+  WA_CHECK_ARG(need <= (int64_t)WA_BSA_FWD_NOALLOC_SCRATCH_BYTES,
+               "wa_bsa_fwd_noalloc: the launch needs %lld bytes of workspace, more than the %lld-byte static "
+               "scratch array; call wa_bsa_fwd with a workspace instead",
+               (long long)need, (long long)WA_BSA_FWD_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(stream, &ws);
+  if (rc != WA_OK) return rc;
+  // arrivals == NULL: the launch clears the counters in the scratch array with a fill kernel first
+  return bsa_fwd_impl(a, ws, stream);
+}
+
+namespace {
+
+int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream) {
   WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_bsa_fwd: head dim %lld not in {64, 128}", (long long)a->D);
   WA_CHECK_ARG(a->block_size == 64 || a->block_size == 128, "wa_bsa_fwd: block size %lld not in {64, 128}",
                (long long)a->block_size);
   WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->Lq >= 0 && a->Lkv > 0, "wa_bsa_fwd: bad sizes");
   WA_CHECK_ARG(a->q && a->k && a->v && a->o, "wa_bsa_fwd: null tensor");
-  WA_CHECK_ARG(a->workspace, "wa_bsa_fwd: workspace required (wa_bsa_fwd_workspace_bytes)");
-  WA_CHECK_ARG(wa_aligned16(a->q) && wa_aligned16(a->k) && wa_aligned16(a->v) && wa_aligned16(a->workspace),
+  WA_CHECK_ARG(workspace, "wa_bsa_fwd: workspace required (wa_bsa_fwd_workspace_bytes)");
+  WA_CHECK_ARG(wa_aligned16(a->q) && wa_aligned16(a->k) && wa_aligned16(a->v) && wa_aligned16(workspace),
                "wa_bsa_fwd: q/k/v/workspace must be 16-byte aligned");
   WA_CHECK_ARG(a->q_sb % 8 == 0 && a->q_st % 8 == 0 && a->q_sh % 8 == 0 && a->k_sb % 8 == 0 &&
                    a->k_st % 8 == 0 && a->k_sh % 8 == 0 && a->v_sb % 8 == 0 && a->v_st % 8 == 0 &&
@@ -776,11 +855,10 @@ extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
                "wa_bsa_fwd: one K/V head slab must span less than 2 GiB");
   fp.k_slab_bytes = (int)k_slab;
   fp.v_slab_bytes = (int)v_slab;
-  fp.part_o = (float*)a->workspace;
+  fp.part_o = (float*)workspace;
   fp.part_lse = fp.part_o + rows * max_splits * a->block_size * a->D;
   fp.arrivals = a->arrivals ? a->arrivals
-                            : (int*)((char*)a->workspace +
-                                     (rows * max_splits * a->block_size * (a->D + 1) * 4 + 255) / 256 * 256);
+                            : (int*)((char*)workspace + partial_bytes(rows, max_splits, a->block_size, a->D));
   const bool cleared = a->arrivals != nullptr;
   if (n_units == 0) fp.n_units = 0;
 
@@ -797,3 +875,5 @@ extern "C" int wa_bsa_fwd(const wa_bsa_fwd_args* a, void* stream) {
   if (a->D == 128 && a->block_size == 64) return launch<128, 64>(fp, rows, cleared, s);
   return launch<128, 128>(fp, rows, cleared, s);
 }
+
+}  // namespace

@@ -63,14 +63,16 @@ def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[
 def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=None, heads=None,
                 out=None, out_dtype=None, want_lse=False, epilogue=_lib.WA_EPI_PLAIN, x=None, gate_w=None,
                 gate_b=None, gate_pre_bf16=False, gate_out_bf16=False, attn_round_bf16=False, lq=None,
-                lkv=None, visits=None, split=None, arrivals=None):
+                lkv=None, visits=None, split=None, arrivals=None, noalloc=False):
     """Launch ``wa_bsa_fwd`` on bf16 q/k/v in ``layout`` ("bhld" = [B, H, L, D], "blhd" = [B, L, H, D]).
 
     ``index=None`` attends densely to every key block. ``visits`` (optional) gives each launched
     head's exact visit count ``min(num, width)`` when the host knows it (top-k routing): the launch
     then covers exactly the needed (row, split) units. ``arrivals`` (optional): an int32 tensor of
     at least ``B * n_heads * ceil(lq / block_size)`` zeros (left zero), which spares the launch
-    clearing its own. Returns ``(out, lse)``.
+    clearing its own. ``noalloc``: launch ``wa_bsa_fwd_noalloc`` instead, whose workspace is the
+    library's static device array (no workspace tensor; ``arrivals`` must be None). Returns
+    ``(out, lse)``.
     """
     dev = _lib.require_gpu(q, k, v)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -111,8 +113,13 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
     if arrivals is not None and (arrivals.dtype != torch.int32 or arrivals.numel() < rows
                                  or not arrivals.is_contiguous() or arrivals.device != dev):
         raise ValueError(f"arrivals must be a contiguous int32 tensor of >= {rows} elements on {dev}")
-    ws_bytes = _lib.lib().wa_bsa_fwd_workspace_bytes(rows, max_visits, split, block_size, d)
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    if noalloc:
+        if arrivals is not None:
+            raise ValueError("noalloc launches keep their arrival counters in the static scratch array")
+        ws = None
+    else:
+        ws_bytes = _lib.lib().wa_bsa_fwd_workspace_bytes(rows, max_visits, split, block_size, d)
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     args = _lib.BsaFwdArgs(
         qp, q_sb, q_st, q_sh, kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh,
         op, o_sb, o_st, o_sh, _lib.dtype_code(out), _lib.ptr(lse),
@@ -121,8 +128,8 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
         xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
         int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16),
-        ws.data_ptr(), _lib.ptr(units), n_units, max_visits, split, _lib.ptr(arrivals))
-    _lib.call("wa_bsa_fwd", args, _lib.stream_ptr(dev))
+        _lib.ptr(ws), _lib.ptr(units), n_units, max_visits, split, _lib.ptr(arrivals))
+    _lib.call("wa_bsa_fwd_noalloc" if noalloc else "wa_bsa_fwd", args, _lib.stream_ptr(dev))
     return out, lse
 
 
