@@ -119,6 +119,24 @@ __global__ void __launch_bounds__(256) summary_partial_kernel(SumParams p) {
   const bool band = p.factors != nullptr && d0 < 2 * p.nt;
   const T* base = (const T*)p.x + (int64_t)b * p.x_sb + c0;
 
+  // The de-rope factor row of a token is its frame (t / row_tokens). The factors of this thread's
+  // band pairs are held in registers and reloaded only when the frame changes, which a token run
+  // inside one frame (a page of whole frames) never does: no per-token division or table load.
+  constexpr int NP = VEC >= 2 ? VEC / 2 : 1;
+  float2 w[NP];
+  int row = -1, next = 0;  // current frame and the first token of the next one
+  auto set_row = [&](int t) {
+    row = min(t / p.row_tokens, p.n_rows - 1);
+    next = row == p.n_rows - 1 ? 0x7fffffff : (row + 1) * p.row_tokens;
+    const float2* frow = p.factors + (int64_t)row * p.nt;
+#pragma unroll
+    for (int e = 0; e < NP; ++e) {
+      const int pr = (d0 >> 1) + e;
+      w[e] = pr < p.nt ? frow[pr] : float2{1.f, 0.f};
+    }
+  };
+  if (band && ts < te) set_row(ts);
+
   float acc[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
@@ -135,8 +153,18 @@ __global__ void __launch_bounds__(256) summary_partial_kernel(SumParams p) {
       if (t + u < te) {
         if constexpr (VEC >= 2) {
           if (band) {
-            const int row = min((t + u) / p.row_tokens, p.n_rows - 1);
-            rotate_band<T, VEC>(f[u], d0, p.factors + (int64_t)row * p.nt, p.nt);
+            if (t + u >= next) set_row(t + u);
+            // complex pairs in the temporal band times the factor, in fp32, rounded to T
+#pragma unroll
+            for (int e = 0; e < VEC; e += 2) {
+              if (((d0 + e) >> 1) < p.nt) {
+                const float2 wv = w[e >> 1];
+                const float re = f[u][e] * wv.x - f[u][e + 1] * wv.y;
+                const float im = f[u][e] * wv.y + f[u][e + 1] * wv.x;
+                f[u][e] = round_to<T>(re);
+                f[u][e + 1] = round_to<T>(im);
+              }
+            }
           }
         }
 #pragma unroll
@@ -163,8 +191,24 @@ __global__ void __launch_bounds__(256) summary_reduce_kernel(SumParams p, float*
     float tot = 0.f;
     for (int b = 0; b < p.B; ++b) {
       const float* w = p.ws + ((int64_t)seg * p.B + b) * p.splits * (int64_t)p.C + c;
+      // the split partials are loaded 16 at a time (all in flight together) and added in split order
       float s = 0.f;
-      for (int sp = 0; sp < p.splits; ++sp) s += w[(int64_t)sp * p.C];
+      int sp = 0;
+      for (; sp + 16 <= p.splits; sp += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = w[(int64_t)(sp + j) * p.C];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += v[j];
+      }
+      if (sp < p.splits) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = sp + j < p.splits ? w[(int64_t)(sp + j) * p.C] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (sp + j < p.splits) s += v[j];
+      }
       tot += s / len;
     }
     const float v = tot / (float)p.B;
