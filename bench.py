@@ -183,6 +183,8 @@ def bench_cfg2(args, dev):
     # inputs are identical; the replay drops the per-call Python and launch overhead.
     ms_per_step = graph_time_ms(step, args.warmup, args.steps)
 
+    cached = bench_cfg2_cached_sums(args, cfg, kw, step)
+
     plan = WA.HeadPlan(q.shape[2], cfg["head_modes"], dev)
     out = torch.empty_like(q)
     nkv = -(-k.shape[1] // cfg["block_size"])
@@ -204,7 +206,46 @@ def bench_cfg2(args, dev):
         f"{achieved:.1f} TFLOP/s")
     hbm = memory_legs(cfg, plan, route, gate, dev, max(args.steps, 20))
     return cfg, proj, dict(ms_per_step=ms_per_step, eager_ms=eager_ms, useful_flop=useful_flop, tile_flop=tile_flop,
-                           sparse_ms=sparse_ms, achieved=achieved, hbm=hbm)
+                           sparse_ms=sparse_ms, achieved=achieved, hbm=hbm, cached=cached)
+
+
+def bench_cfg2_cached_sums(args, cfg, kw, step):
+    """The cfg 2 call as a decoding loop makes it: the 32,760-token window filled by seven
+    4,680-token appends (``kv_append``, which keeps the key block sums of the routed heads), then
+    the same HSA call reading the cached sums, so routing pools only the queries. Reports the
+    call's graph-replay time beside the headline's, the time of one chunk's append, and whether
+    the outputs are identical."""
+    from worldattention_amd.hsa import attention as WA
+    from worldattention_amd.hsa.kvcache import kv_append
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    bs, lkv = cfg["block_size"], k.shape[1]
+    sparse_heads = [h for h, m in enumerate(cfg["head_modes"]) if m != "linear"]
+    cache = {"k": torch.empty_like(k), "v": torch.empty_like(v)}
+    chunk = q.shape[1]
+    for s0 in range(0, lkv, chunk):
+        kv_append(cache, k[:, s0:s0 + chunk], v[:, s0:s0 + chunk], write_start=s0, block_size=bs,
+                  heads=sparse_heads)
+    sums = cache["k_block_sums"]
+
+    def cached_step():
+        with torch.no_grad():
+            return WA.hsa_forward(q, cache["k"], cache["v"], k_block_sums=sums, **kw)
+
+    identical = bool(torch.equal(cached_step(), step()))
+    ms = graph_time_ms(cached_step, args.warmup, args.steps)
+    s_last = (lkv - 1) // chunk * chunk
+
+    def append_last():
+        kv_append(cache, k[:, s_last:], v[:, s_last:], write_start=s_last, block_size=bs, heads=sparse_heads)
+
+    append_ms = graph_time_ms(append_last, args.warmup, max(args.steps, 20))
+    log(f"cfg2 with cached key block sums: {ms:.4f} ms/call (graph replay), identical output {identical}; "
+        f"one {lkv - s_last}-token append {append_ms * 1e3:.1f} us")
+    del cache
+    return {"ms_per_call": round(ms, 4), "identical_to_pooling_keys": identical,
+            "append_ms_per_chunk": round(append_ms, 4), "chunk_tokens": lkv - s_last,
+            "what": "hsa_forward over a cache filled by kv_append, routing from its cached key block sums "
+                    "(graph replay); append: one chunk's K/V copy + block sums of the routed heads (graph replay)"}
 
 
 def memory_legs(cfg, plan, route, gate, dev, iters):
@@ -668,6 +709,7 @@ def main():
         "hsa_fwd_ms_per_chunk_eager": round(c2["eager_ms"], 4),
         "timing": "ms_per_step: the hsa_forward call captured once in a HIP graph and replayed; "
                   "hsa_fwd_ms_per_chunk_eager: the same call launched eagerly from Python",
+        "hsa_fwd_ms_per_chunk_cached_key_sums": c2["cached"],
         "sparse_kernel_ms": round(c2["sparse_ms"], 4),
         "sparse_useful_gflop": round(c2["useful_flop"] / 1e9, 3),
         "sparse_tile_gflop": round(c2["tile_flop"] / 1e9, 3),

@@ -53,6 +53,13 @@ typedef struct wa_pool_args {
   const int32_t* heads; int64_t n_heads;
   float* out;
   int32_t emulate_rounding;
+  /* Block range and sums (no reference counterpart; the cache-write side of causal_model.py:286-327
+   * keeps them): blocks first_block .. first_block + num_blocks - 1 are written (L still counts
+   * tokens from token 0 of x), into an output of out_blocks blocks (0: first_block + num_blocks);
+   * with store_sums the fp32 block sums (in the order the means are formed from) are written
+   * instead of the means. */
+  int64_t first_block, out_blocks;
+  int32_t store_sums;
 } wa_pool_args;
 int wa_block_mean_pool(const wa_pool_args* args, void* stream);
 /* Several pooling jobs (e.g. the query and key tensors of one routing call) with as few launches
@@ -92,9 +99,38 @@ typedef struct wa_route_args {
   float* probs_out;
   void* workspace;
   int32_t* clear; int64_t n_clear;
+  /* k_sum_len > 0 (no reference counterpart): k_pooled holds the fp32 block sums that
+   * wa_block_mean_pool writes with store_sums for a key tensor of k_sum_len tokens in blocks of
+   * block_size (k_sum_bf16: the keys are bf16); the launch forms from them exactly the block means
+   * a pooling of those keys gives (routing.py:45-61 rounding), so the keys need no pooling pass.
+   * k_pooled_blocks: blocks per (batch, head) row of k_pooled (0: Nkv), so the sums of a cache
+   * longer than the routed keys are read in place. */
+  int64_t k_sum_len, block_size;
+  int32_t k_sum_bf16;
+  int64_t k_pooled_blocks;
 } wa_route_args;
 int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nkv);
 int wa_route(const wa_route_args* args, void* stream);
+
+/* Appends new tokens to a KV cache and keeps its key block sums current. Replaces the cache write
+ * of causal_model.py:286-327 (kv_cache["k"/"v"][:, start:end] = roped k / v): new_k / new_v
+ * [B, n, H, D] (BLHD strides, bf16 or fp32 like the cache) are copied to cache tokens
+ * [start, start + n) of cache_k / cache_v [B, cap, H, D]. With k_sums (optional, fp32
+ * [B, H, ceil(cap / block_size), D], no reference counterpart), the sums of every key block that
+ * holds a new token are recomputed over the cache tokens [0, start + n) (wa_block_mean_pool's
+ * store_sums, same order), for the heads listed in `heads` (NULL = all): a later routing call over
+ * the first start + n tokens reads them instead of pooling the keys (wa_route's k_sum_len). */
+typedef struct wa_kv_append_args {
+  void* cache_k; int64_t ck_sb, ck_st, ck_sh;
+  void* cache_v; int64_t cv_sb, cv_st, cv_sh;
+  const void* new_k; int64_t nk_sb, nk_st, nk_sh;
+  const void* new_v; int64_t nv_sb, nv_st, nv_sh;
+  int32_t dtype;
+  int64_t B, cap, H, D, start, n;
+  float* k_sums; int64_t block_size;
+  const int32_t* heads; int64_t n_heads;
+} wa_kv_append_args;
+int wa_kv_append(const wa_kv_append_args* args, void* stream);
 
 /* Boolean selection mask [rows, ncols] (uint8) -> ascending (index [rows, ncols], num [rows]),
  * index padded with -1. Replaces map_to_index, wan/modules/hsa/block_sparse_triton.py:20-57. */

@@ -32,6 +32,7 @@ PoolArgs = _struct("wa_pool_args", [
     ("B", c_int64), ("L", c_int64), ("H", c_int64), ("D", c_int64), ("block_size", c_int64),
     ("num_blocks", c_int64), ("heads", c_void_p), ("n_heads", c_int64), ("out", c_void_p),
     ("emulate_rounding", c_int32),
+    ("first_block", c_int64), ("out_blocks", c_int64), ("store_sums", c_int32),
 ])
 
 RouteArgs = _struct("wa_route_args", [
@@ -41,6 +42,19 @@ RouteArgs = _struct("wa_route_args", [
     ("head_k", c_void_p), ("heads", c_void_p), ("n_heads", c_int64),
     ("index", c_void_p), ("num", c_void_p), ("thresholds", c_void_p), ("mask", c_void_p),
     ("probs_out", c_void_p), ("workspace", c_void_p), ("clear", c_void_p), ("n_clear", c_int64),
+    ("k_sum_len", c_int64), ("block_size", c_int64), ("k_sum_bf16", c_int32),
+    ("k_pooled_blocks", c_int64),
+])
+
+KvAppendArgs = _struct("wa_kv_append_args", [
+    ("cache_k", c_void_p), ("ck_sb", c_int64), ("ck_st", c_int64), ("ck_sh", c_int64),
+    ("cache_v", c_void_p), ("cv_sb", c_int64), ("cv_st", c_int64), ("cv_sh", c_int64),
+    ("new_k", c_void_p), ("nk_sb", c_int64), ("nk_st", c_int64), ("nk_sh", c_int64),
+    ("new_v", c_void_p), ("nv_sb", c_int64), ("nv_st", c_int64), ("nv_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("cap", c_int64), ("H", c_int64), ("D", c_int64), ("start", c_int64), ("n", c_int64),
+    ("k_sums", c_void_p), ("block_size", c_int64),
+    ("heads", c_void_p), ("n_heads", c_int64),
 ])
 
 BsaFwdArgs = _struct("wa_bsa_fwd_args", [
@@ -190,6 +204,7 @@ SIGNATURES = {
     "wa_route_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_route": (c_int, [POINTER(RouteArgs), c_void_p]),
     "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "wa_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
     "wa_bsa_fwd_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_bsa_fwd_noalloc": (c_int, [POINTER(BsaFwdArgs), c_void_p]),

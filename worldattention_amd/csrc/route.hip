@@ -19,6 +19,7 @@ struct PoolParams {
   float* out;
   int emulate;
   int nh;  // head slots (heads listed, or H)
+  int blk0, n_out, sums;  // first block of the launch, blocks of the output, write sums
 };
 
 // Several pooling jobs (e.g. the query and key tensors of one call) in one launch: job j takes
@@ -30,6 +31,17 @@ struct PoolJobs {
   int n;
 };
 
+// The block mean of routing.py:45-61 from the fp32 sum of the block's `real` tokens of a tensor of
+// L tokens: with L a multiple of the block size, the mean in the input dtype (a bf16 input rounds
+// it), otherwise the sum in the input dtype divided by the real count in fp32.
+__device__ __forceinline__ float block_mean_from_sum(float s, int L, int Bs, int real, bool bf) {
+  if (L % Bs == 0) {
+    const float m = s / (float)Bs;
+    return bf ? wa_bf16_round(m) : m;
+  }
+  return (bf ? wa_bf16_round(s) : s) / (float)real;
+}
+
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) pool_kernel(PoolJobs pj) {
   extern __shared__ float red[];  // [rows_per_pass][D + 4]
@@ -40,7 +52,8 @@ __global__ void __launch_bounds__(256) pool_kernel(PoolJobs pj) {
   // consecutive workgroups take the heads of one token block: they read neighbouring chunks of the
   // same token rows
   const int64_t local = id - pj.start[j];
-  const int hs = (int)(local % p.nh), blk = (int)((local / p.nh) % p.N), b = (int)(local / ((int64_t)p.nh * p.N));
+  const int hs = (int)(local % p.nh), blk = p.blk0 + (int)((local / p.nh) % p.N),
+            b = (int)(local / ((int64_t)p.nh * p.N));
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tpr = p.D / VEC;             // threads per token row
@@ -80,16 +93,9 @@ __global__ void __launch_bounds__(256) pool_kernel(PoolJobs pj) {
   for (int d = tid; d < p.D; d += 256) {
     float s = 0.f;
     for (int r = 0; r < rpp; ++r) s += red[r * (p.D + 4) + d];
-    float m;
-    const bool bf = p.emulate && p.dtype == WA_BF16;
-    if (p.L % p.Bs == 0) {
-      m = s / (float)p.Bs;
-      if (bf) m = wa_bf16_round(m);
-    } else {
-      if (bf) s = wa_bf16_round(s);
-      m = s / (float)real;
-    }
-    p.out[(((int64_t)b * p.H + h) * p.N + blk) * p.D + d] = m;
+    float m = s;
+    if (!p.sums) m = block_mean_from_sum(s, p.L, p.Bs, real, p.emulate && p.dtype == WA_BF16);
+    p.out[(((int64_t)b * p.H + h) * p.n_out + blk) * p.D + d] = m;
   }
 }
 
@@ -107,7 +113,16 @@ struct RouteParams {
   int32_t* index; int32_t* num; float* thresholds; uint8_t* mask; float* probs_out;
   float* ws_sorted; float* ws_gini;
   int32_t* clear; int64_t n_clear;
+  int k_sum_len, Bs, k_sum_bf16;  // k_pooled holds block sums of k_sum_len tokens (0: means)
+  int kp_blocks;                  // blocks per (batch, head) row of k_pooled (>= Nkv)
 };
+
+// Pooled key element d of block j: the stored mean, or the mean formed from the stored sum.
+__device__ __forceinline__ float pooled_key(const RouteParams& p, float x, int j) {
+  if (p.k_sum_len <= 0) return x;
+  const int real = max(1, min(p.Bs, p.k_sum_len - j * p.Bs));
+  return block_mean_from_sum(x, p.k_sum_len, p.Bs, real, p.k_sum_bf16 != 0);
+}
 
 __device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
   v = wa_wave_max(v);
@@ -257,7 +272,7 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
     for (int d = tid; d < p.D; d += 256) qrow[d] = qsrc[d];
     __syncthreads();
     // 8 threads per key row: thread tg of the group reads d = 32k + 4tg .. +3 (coalesced float4).
-    const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * p.D;
+    const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)p.kp_blocks * p.D;
     const int grp = tid >> 3, tg = tid & 7;
     const bool vec = (p.D & 31) == 0;
     for (int j0 = 0; j0 < N; j0 += 32) {
@@ -268,13 +283,13 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
         if (vec) {
           for (int d = 4 * tg; d < p.D; d += 32) {
             const f32x4 kv = *(const f32x4*)(kr + d);
-            s = fmaf(qrow[d], kv[0], s);
-            s = fmaf(qrow[d + 1], kv[1], s);
-            s = fmaf(qrow[d + 2], kv[2], s);
-            s = fmaf(qrow[d + 3], kv[3], s);
+            s = fmaf(qrow[d], pooled_key(p, kv[0], j), s);
+            s = fmaf(qrow[d + 1], pooled_key(p, kv[1], j), s);
+            s = fmaf(qrow[d + 2], pooled_key(p, kv[2], j), s);
+            s = fmaf(qrow[d + 3], pooled_key(p, kv[3], j), s);
           }
         } else {
-          for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], kr[d], s);
+          for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], pooled_key(p, kr[d], j), s);
         }
       }
       s += __shfl_xor(s, 1, 64);
@@ -399,16 +414,24 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   if (h < 0 || h >= p.H) return;  // uniform per workgroup
   const int N = p.Nkv, D = DK ? DK : p.D;
   const int64_t row0 = ((int64_t)b * p.H + h) * p.Nq;
-  const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)N * D;
+  const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)p.kp_blocks * D;
 
   // 1. scores of the four rows. With the head dim known at compile time (and N <= 256: one key
   // block per thread), this thread's pooled key row is loaded whole before the pooled queries are
   // staged, so both latencies overlap.
   f32x4 kv[DK ? DK / 4 : 1];
   auto load_key = [&](int j) {
-    const float* kr = kbase + (int64_t)min(j, N - 1) * D;
+    const int jj = min(j, N - 1);
+    const float* kr = kbase + (int64_t)jj * D;
 #pragma unroll
     for (int c = 0; c < (DK ? DK / 4 : 1); ++c) kv[c] = *(const f32x4*)(kr + 4 * c);
+    if (p.k_sum_len > 0) {
+#pragma unroll
+      for (int c = 0; c < (DK ? DK / 4 : 1); ++c) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kv[c][e] = pooled_key(p, kv[c][e], jj);
+      }
+    }
   };
   if (DK) load_key(tid);
   for (int u = tid; u < R * D; u += 256) {
@@ -444,7 +467,11 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
         for (int d0 = 0; d0 < D; d0 += 32) {
           f32x4 kc[8];
 #pragma unroll
-          for (int c = 0; c < 8; ++c) kc[c] = *(const f32x4*)(kr + d0 + 4 * c);
+          for (int c = 0; c < 8; ++c) {
+            kc[c] = *(const f32x4*)(kr + d0 + 4 * c);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kc[c][e] = pooled_key(p, kc[c][e], j);
+          }
 #pragma unroll
           for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -459,7 +486,7 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
         }
       } else {
         for (int d = 0; d < D; ++d) {
-          const float kd = kr[d];
+          const float kd = pooled_key(p, kr[d], j);
 #pragma unroll
           for (int r = 0; r < R; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
         }
@@ -635,9 +662,12 @@ int pool_check(const wa_pool_args* a) {
   WA_CHECK_ARG(a->x_dtype == WA_F32 || a->x_dtype == WA_BF16, "wa_block_mean_pool: bad dtype");
   WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->D > 0 && a->D <= 1024 && a->block_size > 0 && a->num_blocks >= 0,
                "wa_block_mean_pool: bad sizes");
-  WA_CHECK_ARG(a->L <= a->num_blocks * a->block_size && a->L > (a->num_blocks - 1) * a->block_size,
-               "wa_block_mean_pool: L=%lld does not fill %lld blocks of %lld", (long long)a->L,
-               (long long)a->num_blocks, (long long)a->block_size);
+  WA_CHECK_ARG(a->first_block >= 0 && a->out_blocks >= 0, "wa_block_mean_pool: bad block range");
+  const int64_t end_block = a->first_block + a->num_blocks;
+  WA_CHECK_ARG(a->L <= end_block * a->block_size && a->L > (end_block - 1) * a->block_size,
+               "wa_block_mean_pool: L=%lld does not end in block %lld of %lld tokens", (long long)a->L,
+               (long long)(end_block - 1), (long long)a->block_size);
+  WA_CHECK_ARG(a->out_blocks == 0 || a->out_blocks >= end_block, "wa_block_mean_pool: out_blocks < last block");
   WA_CHECK_ARG(pool_variant(a) >= 0, "wa_block_mean_pool: an unaligned input needs D <= 256");
   return WA_OK;
 }
@@ -653,7 +683,10 @@ int pool_launch(const wa_pool_args* const* jobs, int n, int variant, hipStream_t
     const int64_t nh = a->heads ? a->n_heads : a->H;
     if (a->B == 0 || nh == 0 || a->num_blocks == 0) continue;
     pj.job[pj.n] = PoolParams{a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype, (int)a->L, (int)a->H, (int)a->D,
-                              (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding, (int)nh};
+                              (int)a->block_size, (int)a->num_blocks, a->heads, a->out, a->emulate_rounding, (int)nh,
+                              (int)a->first_block,
+                              (int)(a->out_blocks > 0 ? a->out_blocks : a->first_block + a->num_blocks),
+                              a->store_sums};
     pj.start[pj.n] = total;
     total += nh * a->num_blocks * a->B;
     const int vec = variant == 0 ? 8 : variant == 2 ? 4 : 1;
@@ -740,6 +773,15 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.probs_out = a->probs_out;
   WA_CHECK_ARG(a->n_clear >= 0 && (a->n_clear == 0 || a->clear), "wa_route: clear is NULL with n_clear > 0");
   rp.clear = a->clear; rp.n_clear = a->n_clear;
+  WA_CHECK_ARG(a->k_sum_len <= 0 || (a->block_size > 0 && a->k_sum_len > (a->Nkv - 1) * a->block_size &&
+                                     a->k_sum_len <= a->Nkv * a->block_size && a->k_sum_len < ((int64_t)1 << 30)),
+               "wa_route: k_sum_len %lld does not end in key block %lld of %lld tokens", (long long)a->k_sum_len,
+               (long long)(a->Nkv - 1), (long long)a->block_size);
+  rp.k_sum_len = a->k_sum_len > 0 ? (int)a->k_sum_len : 0;
+  rp.Bs = (int)(a->block_size > 0 ? a->block_size : 1);
+  rp.k_sum_bf16 = a->k_sum_bf16;
+  WA_CHECK_ARG(a->k_pooled_blocks == 0 || a->k_pooled_blocks >= a->Nkv, "wa_route: k_pooled_blocks < Nkv");
+  rp.kp_blocks = (int)(a->k_pooled_blocks > 0 ? a->k_pooled_blocks : a->Nkv);
   const int64_t rows = a->B * a->H * a->Nq;
   rp.ws_sorted = (float*)a->workspace;
   rp.ws_gini = a->workspace ? (float*)a->workspace + rows * a->Nkv : nullptr;
@@ -765,6 +807,95 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipLaunchKernelGGL(gini_count_kernel, dim3((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B), dim3(64),
                      (size_t)a->Nkv * sizeof(float), s, rp);
   return wa_launch_status("route_gini_count");
+}
+
+namespace {
+
+// Copy of a [B, n, H, D] BLHD tensor into another, 16 bytes per thread (VEC elements of T).
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) kv_copy_kernel(const T* src, int64_t s_sb, int64_t s_st, int64_t s_sh, T* dst,
+                                                      int64_t d_sb, int64_t d_st, int64_t d_sh, int B, int n, int H,
+                                                      int D) {
+  const int64_t cpr = D / VEC;  // chunks per head row
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)B * n * H * cpr;
+  if (i >= total) return;
+  const int c = (int)(i % cpr);
+  const int64_t r = i / cpr;
+  const int h = (int)(r % H), t = (int)((r / H) % n), b = (int)(r / ((int64_t)H * n));
+  const T* sp = src + b * s_sb + t * s_st + h * s_sh + c * VEC;
+  T* dp = dst + b * d_sb + t * d_st + h * d_sh + c * VEC;
+  if constexpr (VEC * sizeof(T) == 16) {
+    *(u32x4*)dp = *(const u32x4*)sp;
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dp[e] = sp[e];
+  }
+}
+
+int kv_copy(const void* src, int64_t s_sb, int64_t s_st, int64_t s_sh, void* dst, int64_t d_sb, int64_t d_st,
+            int64_t d_sh, int dtype, int64_t B, int64_t n, int64_t H, int64_t D, hipStream_t s) {
+  const int es = dtype == WA_BF16 ? 2 : 4;
+  const int vec = 16 / es;
+  const bool v16 = wa_aligned16(src) && wa_aligned16(dst) && D % vec == 0 && s_sb % vec == 0 && s_st % vec == 0 &&
+                   s_sh % vec == 0 && d_sb % vec == 0 && d_st % vec == 0 && d_sh % vec == 0;
+  const int64_t total = B * n * H * (v16 ? D / vec : D);
+  if (total == 0) return WA_OK;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (dtype == WA_BF16) {
+    if (v16)
+      hipLaunchKernelGGL((kv_copy_kernel<bf16_t, 8>), grid, dim3(256), 0, s, (const bf16_t*)src, s_sb, s_st, s_sh,
+                         (bf16_t*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
+    else
+      hipLaunchKernelGGL((kv_copy_kernel<bf16_t, 1>), grid, dim3(256), 0, s, (const bf16_t*)src, s_sb, s_st, s_sh,
+                         (bf16_t*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
+  } else {
+    if (v16)
+      hipLaunchKernelGGL((kv_copy_kernel<float, 4>), grid, dim3(256), 0, s, (const float*)src, s_sb, s_st, s_sh,
+                         (float*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
+    else
+      hipLaunchKernelGGL((kv_copy_kernel<float, 1>), grid, dim3(256), 0, s, (const float*)src, s_sb, s_st, s_sh,
+                         (float*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
+  }
+  return wa_launch_status("kv_append_copy");
+}
+
+}  // namespace
+
+extern "C" int wa_kv_append(const wa_kv_append_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->cache_k && a->cache_v && a->new_k && a->new_v, "wa_kv_append: null argument");
+  WA_CHECK_ARG(a->dtype == WA_BF16 || a->dtype == WA_F32, "wa_kv_append: dtype must be bf16 or fp32");
+  WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->D > 0 && a->cap > 0 && a->n >= 0 && a->start >= 0 &&
+                   a->start + a->n <= a->cap,
+               "wa_kv_append: tokens [%lld, %lld) do not fit a cache of %lld", (long long)a->start,
+               (long long)(a->start + a->n), (long long)a->cap);
+  WA_CHECK_ARG(a->B < (1 << 20) && a->cap < ((int64_t)1 << 30) && a->H < (1 << 16) && a->D <= 1024,
+               "wa_kv_append: sizes too large");
+  if (a->B == 0 || a->n == 0) return WA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t es = a->dtype == WA_BF16 ? 2 : 4;
+  void* dk = (char*)a->cache_k + a->start * a->ck_st * es;  // token `start` of the cache
+  void* dv = (char*)a->cache_v + a->start * a->cv_st * es;
+  int rc = kv_copy(a->new_k, a->nk_sb, a->nk_st, a->nk_sh, dk, a->ck_sb, a->ck_st, a->ck_sh, a->dtype, a->B, a->n,
+                   a->H, a->D, s);
+  if (rc != WA_OK) return rc;
+  rc = kv_copy(a->new_v, a->nv_sb, a->nv_st, a->nv_sh, dv, a->cv_sb, a->cv_st, a->cv_sh, a->dtype, a->B, a->n, a->H,
+               a->D, s);
+  if (rc != WA_OK || !a->k_sums) return rc;
+  WA_CHECK_ARG(a->block_size > 0, "wa_kv_append: k_sums needs a block size");
+  // sums of the key blocks that hold a new token, over the cache's tokens [0, start + n)
+  wa_pool_args pa{};
+  pa.x = a->cache_k; pa.x_sb = a->ck_sb; pa.x_st = a->ck_st; pa.x_sh = a->ck_sh; pa.x_dtype = a->dtype;
+  pa.B = a->B; pa.L = a->start + a->n; pa.H = a->H; pa.D = a->D; pa.block_size = a->block_size;
+  pa.first_block = a->start / a->block_size;
+  pa.num_blocks = (a->start + a->n + a->block_size - 1) / a->block_size - pa.first_block;
+  pa.heads = a->heads; pa.n_heads = a->n_heads;
+  pa.out = a->k_sums; pa.out_blocks = (a->cap + a->block_size - 1) / a->block_size;
+  pa.emulate_rounding = 1; pa.store_sums = 1;
+  rc = pool_check(&pa);
+  if (rc != WA_OK) return rc;
+  const wa_pool_args* job = &pa;
+  return pool_launch(&job, 1, pool_variant(&pa), s);
 }
 
 extern "C" int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* index,

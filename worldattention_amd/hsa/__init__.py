@@ -8,6 +8,7 @@ from .attention import (
     require_trained_hsa,
     resolve_backend,
 )
+from .kvcache import kv_append, new_block_sums
 from .block_sparse import block_sparse_attention, block_sparse_attention_reference, map_to_index
 from .routing import (
     BlockRouting,
@@ -32,4 +33,6 @@ __all__ = [
     "build_topk_routing",
     "block_attention_map",
     "block_mean_pool",
+    "kv_append",
+    "new_block_sums",
 ]

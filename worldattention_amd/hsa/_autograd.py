@@ -16,7 +16,7 @@ import torch
 from .. import _lib
 from ._bwd import bsa_backward
 from .block_sparse import bsa_forward
-from .routing import _route, block_counts, pool_blhd
+from .routing import _route, block_counts, pool_for_routing
 
 __all__ = ["hsa_attention_autograd", "compress_autograd", "elu1_backward", "fuse_forward", "fuse_backward"]
 
@@ -188,15 +188,15 @@ class _HSA(torch.autograd.Function):
         if plan.sparse:
             _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
             st = plan.t["sparse"]
-            qp = pool_blhd(q, q_len, nq, block_size, heads=st)
-            kp = pool_blhd(k, kv_len, nkv, block_size, heads=st)
+            qp, kp, key_args = pool_for_routing(q, k, q_len, kv_len, block_size, st,
+                                                k_block_sums=cfg["k_block_sums"], k_pooled=cfg["k_pooled"])
             visits = None
             if routing == "gini":
                 route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=cfg["tau_min"],
-                                  tau_max=cfg["tau_max"], heads=st)
+                                  tau_max=cfg["tau_max"], heads=st, **key_args)
             else:
                 ks = _per_head_k(topk, heads)
-                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st)
+                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st, **key_args)
                 visits = [min(ks[h], nkv) for h in plan.sparse]
             _, lse_s = bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size,
                                    layout="blhd", heads=st, out=sparse, lq=q_len, lkv=kv_len, want_lse=True,
@@ -274,12 +274,14 @@ class _HSA(torch.autograd.Function):
 
 
 def hsa_attention_autograd(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
-                           tau_max, proj_segment_len, routing, topk, head_modes, linear_mode):
+                           tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, k_block_sums=None,
+                           k_pooled=None):
     """Differentiable :func:`hsa_attention` (q, k, v, coarse caches, projections and gate)."""
     if block_size not in (64, 128) or q.shape[-1] not in (64, 128):
         raise ValueError("block_size and head_dim must each be 64 or 128 for the gfx950 kernels")
     gate_w = gate_lin.weight if gate_lin is not None else None
     gate_b = getattr(gate_lin, "bias", None) if gate_lin is not None else None
     cfg = dict(block_size=block_size, tau_min=tau_min, tau_max=tau_max, proj_segment_len=proj_segment_len,
-               routing=routing, topk=topk, head_modes=head_modes, linear_mode=linear_mode)
+               routing=routing, topk=topk, head_modes=head_modes, linear_mode=linear_mode,
+               k_block_sums=k_block_sums, k_pooled=k_pooled)
     return _HSA.apply(q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b, cfg)

@@ -30,7 +30,7 @@ import torch.nn as nn
 from .. import _lib
 from . import distill
 from .block_sparse import bsa_forward
-from .routing import _route, block_counts, pool_blhd_many
+from .routing import _route, block_counts, pool_for_routing
 
 __all__ = [
     "HSAAttention",
@@ -77,7 +77,10 @@ def coarse_length(kv_len: int, segment_len: int, proj_rank: int, block_size: int
     return total
 
 
-def _compress(x: torch.Tensor, proj: torch.Tensor, *, segment_len: int, block_size: int, layout: str) -> torch.Tensor:
+def _compress(x: torch.Tensor, proj: torch.Tensor, *, segment_len: int, block_size: int, layout: str,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``out`` (optional): a view of the destination rows (same layout, dtype of ``x``), e.g. slots
+    of a compressed cache, written in place."""
     dev = _lib.require_gpu(x, proj)
     if layout == "bhld":
         bsz, heads, length, d = x.shape
@@ -96,12 +99,16 @@ def _compress(x: torch.Tensor, proj: torch.Tensor, *, segment_len: int, block_si
         src = src.contiguous()
     pj = proj if proj.dtype in (torch.float32, torch.bfloat16) else proj.float()
     pj = pj.contiguous()
+    shape = (bsz, heads, lc, d) if layout == "bhld" else (bsz, lc, heads, d)
+    if out is None:
+        out = torch.empty(shape, dtype=x.dtype, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != x.dtype or out.stride(-1) != 1:
+        raise ValueError(f"compress output must be {x.dtype} {shape} with unit last stride, got "
+                         f"{out.dtype} {tuple(out.shape)}")
     if layout == "bhld":
-        out = torch.empty((bsz, heads, lc, d), dtype=x.dtype, device=dev)
         xp, x_sb, x_st, x_sh = _lib.bhld(src)
         op, o_sb, o_st, o_sh = _lib.bhld(out)
     else:
-        out = torch.empty((bsz, lc, heads, d), dtype=x.dtype, device=dev)
         xp, x_sb, x_st, x_sh = _lib.blhd(src)
         op, o_sb, o_st, o_sh = _lib.blhd(out)
     args = _lib.CompressArgs(xp, x_sb, x_st, x_sh, _lib.dtype_code(src), pj.data_ptr(), _lib.dtype_code(pj),
@@ -256,7 +263,8 @@ def _per_head_k(topk, heads: int):
 
 
 def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
-                tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, save=None):
+                tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, k_block_sums=None,
+                k_pooled=None, save=None):
     """Forward of HSA on the GPU; ``save`` (a dict) receives what the backward needs."""
     bsz, q_len, heads, head_dim = q.shape
     kv_len = k.shape[1]
@@ -305,7 +313,8 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     if plan.sparse:
         _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
         sp_t = plan.t["sparse"]
-        qp, kp = pool_blhd_many([(q, q_len, nq), (k, kv_len, nkv)], block_size, heads=sp_t)
+        qp, kp, key_args = pool_for_routing(q, k, q_len, kv_len, block_size, sp_t, k_block_sums=k_block_sums,
+                                            k_pooled=k_pooled)
 
     # ---- sparse branch: routing and attention ----------------------------------------------
     if plan.sparse:
@@ -315,10 +324,11 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
         arrivals = torch.empty((rows_only + rows_both,), dtype=torch.int32, device=dev)
         if routing == "gini":
             route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t,
-                              clear=arrivals)
+                              clear=arrivals, **key_args)
         else:
             ks = _per_head_k(topk, heads)
-            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t, clear=arrivals)
+            route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t, clear=arrivals,
+                              **key_args)
         if save is not None:
             save.update(route=route)
         # top-k routing fixes every row's visit count on the host: launch exactly those units
@@ -401,14 +411,24 @@ def hsa_attention(
     topk=None,
     head_modes: Optional[Sequence[str]] = None,
     linear_mode: str = "lowrank",
+    k_block_sums: Optional[torch.Tensor] = None,
+    k_pooled: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Run HSA over ``[B, L, H, D]`` queries, keys and values (``attention.py:153-259``).
 
     ``k_coarse`` / ``v_coarse`` supply an already-compressed view of the same KV range (the
     decoding loop's compressed cache); when omitted the compression runs here.
+
+    ``k_block_sums`` (no reference counterpart): the fp32 key block sums that
+    :func:`worldattention_amd.hsa.kvcache.kv_append` keeps beside a KV cache whose first
+    ``k.shape[1]`` tokens are ``k``; ``k_pooled``: fp32 block means of exactly ``k`` (the routing
+    pool of ``routing.py:45-61``). With either, routing pools only the queries; the result is
+    identical to pooling ``k``.
     """
     if (k_coarse is None) != (v_coarse is None):
         raise ValueError("k_coarse and v_coarse must be provided together")
+    if k_block_sums is not None and k_pooled is not None:
+        raise ValueError("pass k_block_sums or k_pooled, not both")
     bsz, q_len, heads, head_dim = q.shape
     kv_len = k.shape[1]
     if q_len <= 0 or kv_len <= 0:
@@ -423,7 +443,7 @@ def hsa_attention(
     cfg = dict(k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=k_proj_mat, v_proj_mat=v_proj_mat,
                gate_lin=gate_lin, block_size=block_size, tau_min=tau_min, tau_max=tau_max,
                proj_segment_len=proj_segment_len, routing=routing, topk=topk, head_modes=head_modes,
-               linear_mode=linear_mode)
+               linear_mode=linear_mode, k_block_sums=k_block_sums, k_pooled=k_pooled)
     needs_grad = torch.is_grad_enabled() and (
         any(t is not None and t.requires_grad for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat))
         or (gate_lin is not None and any(p.requires_grad for p in gate_lin.parameters())))
@@ -518,10 +538,10 @@ class HSAAttention(nn.Module):
                 _compress(v, self.v_proj_mat, segment_len=self.proj_segment_len, block_size=self.block_size,
                           layout="blhd"))
 
-    def forward(self, q, k, v, k_coarse=None, v_coarse=None) -> torch.Tensor:
+    def forward(self, q, k, v, k_coarse=None, v_coarse=None, *, k_block_sums=None, k_pooled=None) -> torch.Tensor:
         return hsa_attention(
             q, k, v, k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=self.k_proj_mat,
             v_proj_mat=self.v_proj_mat, gate_lin=self.gate_lin, block_size=self.block_size,
             tau_min=self.tau_min, tau_max=self.tau_max, proj_segment_len=self.proj_segment_len,
             backend=self.backend, routing=self.routing, topk=self.topk, head_modes=self.head_modes,
-            linear_mode=self.linear_mode)
+            linear_mode=self.linear_mode, k_block_sums=k_block_sums, k_pooled=k_pooled)

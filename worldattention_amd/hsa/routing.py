@@ -137,10 +137,42 @@ def block_mean_pool(x: torch.Tensor, logical_len: int, num_blocks: int, block_si
     return out
 
 
+def pool_for_routing(q, k, q_len: int, kv_len: int, block_size: int, heads=None, *, k_block_sums=None,
+                     k_pooled=None):
+    """Pooled queries and keys of one routing call, and the key arguments of :func:`_route`.
+
+    The keys are pooled here unless the caller holds them: ``k_pooled`` (fp32 ``[B, H, >= Nkv, D]``
+    block means of exactly these ``kv_len`` keys, e.g. :func:`pool_blhd`'s output) or
+    ``k_block_sums`` (fp32 ``[B, H, >= Nkv, D]`` block sums, as :func:`worldattention_amd.hsa.kvcache.kv_append`
+    keeps them for a cache; routing forms from them the means of the first ``kv_len`` tokens).
+    Either way only the queries are pooled.
+    """
+    _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+    if k_block_sums is not None and k_pooled is not None:
+        raise ValueError("pass k_block_sums or k_pooled, not both")
+    held = k_block_sums if k_block_sums is not None else k_pooled
+    if held is None:
+        qp, kp = pool_blhd_many([(q, q_len, nq), (k, kv_len, nkv)], block_size, heads=heads)
+        return qp, kp, {}
+    b, _, h, d = k.shape
+    if (held.dtype != torch.float32 or held.dim() != 4 or held.shape[0] != b or held.shape[1] != h
+            or held.shape[3] != d or held.shape[2] < nkv or not held.is_contiguous()):
+        raise ValueError(f"cached key blocks must be contiguous fp32 [{b}, {h}, >= {nkv}, {d}], got "
+                         f"{held.dtype} {tuple(held.shape)}")
+    _lib.require_gpu(held, q)
+    (qp,) = pool_blhd_many([(q, q_len, nq)], block_size, heads=heads)
+    key_args = dict(nkv=nkv, k_pooled_blocks=held.shape[2])
+    if k_block_sums is not None:
+        key_args.update(k_sum_len=kv_len, block_size=block_size, k_sum_bf16=k.dtype == torch.bfloat16)
+    return qp, held, key_args
+
+
 def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=None,
-           return_mask=False, want_probs=False, clear=None):
+           return_mask=False, want_probs=False, clear=None, nkv=None, k_pooled_blocks=0, k_sum_len=0,
+           block_size=0, k_sum_bf16=False):
     """``clear`` (optional): a contiguous int32 device tensor the launch zeroes (the arrivals of
-    the block-sparse launch that follows)."""
+    the block-sparse launch that follows). ``nkv`` / ``k_pooled_blocks`` / ``k_sum_len`` /
+    ``block_size`` / ``k_sum_bf16``: cached key blocks (:func:`pool_for_routing`)."""
     src = probs if probs is not None else qp
     dev = _lib.require_gpu(src, kp)
     if probs is not None:
@@ -151,7 +183,7 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
         qp = qp.float().contiguous()
         kp = kp.float().contiguous()
         bsz, nheads, nq, d = qp.shape
-        nkv = kp.shape[2]
+        nkv = kp.shape[2] if nkv is None else nkv
     index = torch.empty((bsz, nheads, nq, nkv), dtype=torch.int32, device=dev)
     # the kernel writes num of unrouted heads (0) and every threshold: no fill needed
     num = torch.empty((bsz, nheads, nq), dtype=torch.int32, device=dev)
@@ -171,7 +203,8 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
                           float(tau_min), float(tau_max - tau_min), _lib.ptr(head_k_t), _lib.ptr(heads),
                           0 if heads is None else heads.numel(), index.data_ptr(), num.data_ptr(),
                           thresholds.data_ptr(), _lib.ptr(mask), _lib.ptr(probs_out), _lib.ptr(ws),
-                          _lib.ptr(clear), 0 if clear is None else clear.numel())
+                          _lib.ptr(clear), 0 if clear is None else clear.numel(), int(k_sum_len),
+                          int(block_size), int(bool(k_sum_bf16)), int(k_pooled_blocks))
     _lib.call("wa_route", args, _lib.stream_ptr(dev))
     return BlockRouting(index=index, num=num, mask=mask, thresholds=thresholds), probs_out
 
