@@ -132,6 +132,60 @@ typedef struct wa_kv_append_args {
 } wa_kv_append_args;
 int wa_kv_append(const wa_kv_append_args* args, void* stream);
 
+/* QKV epilogue of one cached causal attention step (after the q / k / v projections). Replaces
+ * norm_q / norm_k (WanRMSNorm, wan/modules/model.py:70-86, applied at causal_model.py:166-169),
+ * causal_rope_apply of q and k (causal_model.py:34-62, called at :275-281) and the cache write of
+ * the roped keys and the values (causal_model.py:358-365 / :393-400, committed at :1089-1113):
+ *   q_out[b, s]              = rope(norm_q(q[b, s]))            s < n
+ *   cache_k[b, ws + t]       = rope(norm_k(k[b, so + t]))       t < write_len
+ *   cache_v[b, ws + t]       = v[b, so + t]
+ * (ws = write_start, so = src_offset). q, k, v, q_out and the caches are [B, *, H, D] BLHD of one
+ * dtype (bf16 or fp32). rope: the 3-D RoPE of token s's position (frame start_frame + s / (gh*gw),
+ * row, column) in the grid_f x grid_h x grid_w grid, from `freqs` = the model's complex128 table
+ * [f_rows, D / 2] as fp64 (re, im) pairs; products in fp64, rounded to fp32, then to the dtype.
+ * Tokens s >= grid_f * grid_h * grid_w pass through unrotated. norm (q_norm_w and k_norm_w [H * D],
+ * w_dtype bf16 or fp32; both NULL: no norm): x * rsqrt(mean(x^2) + eps) over a token's H * D
+ * channels in fp32, summed in torch's CPU order, rounded to the dtype, times the weight in the wider
+ * of the two dtypes. With k_sums (fp32 [B, H, ceil(cap / block_size), D], no reference
+ * counterpart) the key block sums of the written blocks are then refreshed as wa_kv_append does. */
+typedef struct wa_qkv_epilogue_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  int32_t dtype;
+  int64_t B, n, H, D;
+  void* q_out; int64_t qo_sb, qo_st, qo_sh;
+  void* cache_k; int64_t ck_sb, ck_st, ck_sh;
+  void* cache_v; int64_t cv_sb, cv_st, cv_sh;
+  int64_t cap, write_start, src_offset, write_len;
+  const double* freqs; int64_t f_rows;
+  int64_t grid_f, grid_h, grid_w, start_frame;
+  const void* q_norm_w; const void* k_norm_w; int32_t w_dtype; float eps;
+  float* k_sums; int64_t block_size;
+} wa_qkv_epilogue_args;
+int wa_qkv_epilogue(const wa_qkv_epilogue_args* args, void* stream);
+
+/* Sliding-window roll of a KV cache, in place. Replaces the clone-and-shift of
+ * causal_model.py:326-356 (and its commit, :1034-1087): tokens [sink + evicted,
+ * sink + evicted + rolled) of cache_k / cache_v move to [sink, sink + rolled); with k_coarse /
+ * v_coarse (same dtype, [B, coarse_cap, H, D]) coarse rows [c_src, c_src + c_rows) move to
+ * [c_dst, c_dst + c_rows). No copy of the cache is made: the move runs in launches of at most
+ * `evicted` tokens, each of which overwrites only tokens earlier launches have read. With k_sums,
+ * the key block sums over [sink, sink + rolled) are recomputed (heads as in wa_kv_append). */
+typedef struct wa_kv_roll_args {
+  void* cache_k; int64_t ck_sb, ck_st, ck_sh;
+  void* cache_v; int64_t cv_sb, cv_st, cv_sh;
+  int32_t dtype;
+  int64_t B, cap, H, D;
+  int64_t sink, evicted, rolled;
+  float* k_sums; int64_t block_size;
+  const int32_t* heads; int64_t n_heads;
+  void* k_coarse; int64_t kc_sb, kc_st, kc_sh;
+  void* v_coarse; int64_t vc_sb, vc_st, vc_sh;
+  int64_t coarse_cap, c_dst, c_src, c_rows;
+} wa_kv_roll_args;
+int wa_kv_roll(const wa_kv_roll_args* args, void* stream);
+
 /* Boolean selection mask [rows, ncols] (uint8) -> ascending (index [rows, ncols], num [rows]),
  * index padded with -1. Replaces map_to_index, wan/modules/hsa/block_sparse_triton.py:20-57. */
 int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* index,

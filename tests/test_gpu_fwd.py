@@ -191,6 +191,34 @@ def test_compress_kv_matches_oracle(dtype):
     assert_close(gv, wv, max_abs=1e-2, mean_abs=1e-3, what="compress v")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_dense_distillation_teacher_matches_oracle(d):
+    """The distillation teacher (the dense flash kernel) against fp32 softmax attention (the
+    oracle's dense attention, pinned by SDPA in fp64), and the recorded loss against the MSE to it."""
+    from worldattention_amd.hsa import distill
+    torch.manual_seed(d)
+    q, k, v = torch.randn(2, 700, 3, d), torch.randn(2, 2000, 3, d), torch.randn(2, 2000, 3, d)
+    want = O.linear_branch_lowrank(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)).transpose(1, 2)
+    qg, kg, vg = (t.to(DEV).bfloat16() for t in (q, k, v))
+    got = distill.dense_attention(qg, kg, vg)
+    assert got.dtype == torch.bfloat16
+    assert_close(got, want, what="dense teacher")
+    got32 = distill.dense_attention(qg.float(), kg.float(), vg.float())
+    assert got32.dtype == torch.float32
+    assert_close(got32, want, what="dense teacher, fp32 result")
+    hsa_out = (want + 0.05 * torch.randn_like(want)).to(DEV).requires_grad_(True)
+    distill.enable_distill(True)
+    try:
+        distill.record_against_dense(hsa_out, qg.float(), kg.float(), vg.float())
+        (loss,) = distill.pop_distill_losses()
+    finally:
+        distill.enable_distill(False)
+    want_loss = ((hsa_out.detach().cpu() - want) ** 2).mean()
+    assert abs(loss.item() - want_loss.item()) <= 2e-2 * want_loss.item()
+    loss.backward()
+    assert hsa_out.grad is not None and torch.isfinite(hsa_out.grad).all()
+
+
 def test_lowrank_linear_branch_matches_oracle():
     torch.manual_seed(3)
     q, kc, vc = torch.randn(1, 2, 300, 64), torch.randn(1, 2, 77, 64), torch.randn(1, 2, 77, 64)

@@ -57,6 +57,35 @@ KvAppendArgs = _struct("wa_kv_append_args", [
     ("heads", c_void_p), ("n_heads", c_int64),
 ])
 
+QkvEpilogueArgs = _struct("wa_qkv_epilogue_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("n", c_int64), ("H", c_int64), ("D", c_int64),
+    ("q_out", c_void_p), ("qo_sb", c_int64), ("qo_st", c_int64), ("qo_sh", c_int64),
+    ("cache_k", c_void_p), ("ck_sb", c_int64), ("ck_st", c_int64), ("ck_sh", c_int64),
+    ("cache_v", c_void_p), ("cv_sb", c_int64), ("cv_st", c_int64), ("cv_sh", c_int64),
+    ("cap", c_int64), ("write_start", c_int64), ("src_offset", c_int64), ("write_len", c_int64),
+    ("freqs", c_void_p), ("f_rows", c_int64),
+    ("grid_f", c_int64), ("grid_h", c_int64), ("grid_w", c_int64), ("start_frame", c_int64),
+    ("q_norm_w", c_void_p), ("k_norm_w", c_void_p), ("w_dtype", c_int32), ("eps", c_float),
+    ("k_sums", c_void_p), ("block_size", c_int64),
+])
+
+KvRollArgs = _struct("wa_kv_roll_args", [
+    ("cache_k", c_void_p), ("ck_sb", c_int64), ("ck_st", c_int64), ("ck_sh", c_int64),
+    ("cache_v", c_void_p), ("cv_sb", c_int64), ("cv_st", c_int64), ("cv_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("cap", c_int64), ("H", c_int64), ("D", c_int64),
+    ("sink", c_int64), ("evicted", c_int64), ("rolled", c_int64),
+    ("k_sums", c_void_p), ("block_size", c_int64),
+    ("heads", c_void_p), ("n_heads", c_int64),
+    ("k_coarse", c_void_p), ("kc_sb", c_int64), ("kc_st", c_int64), ("kc_sh", c_int64),
+    ("v_coarse", c_void_p), ("vc_sb", c_int64), ("vc_st", c_int64), ("vc_sh", c_int64),
+    ("coarse_cap", c_int64), ("c_dst", c_int64), ("c_src", c_int64), ("c_rows", c_int64),
+])
+
 BsaFwdArgs = _struct("wa_bsa_fwd_args", [
     ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
     ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
@@ -205,6 +234,8 @@ SIGNATURES = {
     "wa_route": (c_int, [POINTER(RouteArgs), c_void_p]),
     "wa_map_to_index": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "wa_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
+    "wa_qkv_epilogue": (c_int, [POINTER(QkvEpilogueArgs), c_void_p]),
+    "wa_kv_roll": (c_int, [POINTER(KvRollArgs), c_void_p]),
     "wa_bsa_fwd_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_bsa_fwd_noalloc": (c_int, [POINTER(BsaFwdArgs), c_void_p]),

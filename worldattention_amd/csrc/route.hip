@@ -5,6 +5,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "torch_order.h"
 
 namespace {
 
@@ -115,13 +116,44 @@ struct RouteParams {
   int32_t* clear; int64_t n_clear;
   int k_sum_len, Bs, k_sum_bf16;  // k_pooled holds block sums of k_sum_len tokens (0: means)
   int kp_blocks;                  // blocks per (batch, head) row of k_pooled (>= Nkv)
+  float inv_bs;                   // 1 / Bs when Bs is a power of two (exact), else 0
+  int k_sum_div;                  // k_sum_len % Bs == 0
 };
 
-// Pooled key element d of block j: the stored mean, or the mean formed from the stored sum.
+// Pooled key element of block j: the stored mean, or the mean formed from the stored sum
+// (block_mean_from_sum). Used by the loops that visit a key row element by element.
 __device__ __forceinline__ float pooled_key(const RouteParams& p, float x, int j) {
   if (p.k_sum_len <= 0) return x;
   const int real = max(1, min(p.Bs, p.k_sum_len - j * p.Bs));
   return block_mean_from_sum(x, p.k_sum_len, p.Bs, real, p.k_sum_bf16 != 0);
+}
+
+// A whole key row held in registers, sums -> means. For a power-of-two block size a full block's
+// division is a multiply by the exact reciprocal (the same correctly rounded result), so one branch
+// per row picks the multiply for every block but a partial last one, which divides.
+template <int NC>
+__device__ __forceinline__ void pooled_key_row(const RouteParams& p, f32x4 (&kv)[NC], int j) {
+  if (p.k_sum_len <= 0) return;
+  const bool bf = p.k_sum_bf16 != 0;
+  if (p.inv_bs != 0.f && (j < p.Nkv - 1 || p.k_sum_div)) {
+    const bool pre = bf && !p.k_sum_div, post = bf && p.k_sum_div;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = pre ? wa_bf16_round(kv[c][e]) : kv[c][e];
+        const float m = x * p.inv_bs;
+        kv[c][e] = post ? wa_bf16_round(m) : m;
+      }
+    }
+  } else {
+    const float real = (float)max(1, min(p.Bs, p.k_sum_len - j * p.Bs));
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kv[c][e] = (bf ? wa_bf16_round(kv[c][e]) : kv[c][e]) / real;
+    }
+  }
 }
 
 __device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
@@ -167,64 +199,6 @@ __device__ bool clear_unrouted(const RouteParams& p) {
       if (!routed((int)((u / p.Nq) % p.H))) p.num[u] = 0;
   for (int64_t u = threadIdx.x; u < p.n_clear; u += blockDim.x) p.clear[u] = 0;
   return true;
-}
-
-// ---------------------------------------------------------------------------------------------
-// fp32 sums in the order of torch's CPU reduction kernel (aten/src/ATen/native/cpu/SumKernel.cpp,
-// cascade_sum), which computes the reference's Gini sums and head means (routing.py:99-101):
-//   * cascade: one accumulator chain over n elements, pushed up a 4-level cascade every 2^p
-//     elements (p = max(4, ceil(log2 n) / 4)) and folded at the end (multi_row_sum);
-//   * row_sum: 4 interleaved cascades over n / 4 groups, the tail added to the first, then the
-//     four folded in order;
-//   * inner_sum: a contiguous run of n >= 8 is summed as 8 lanes (lane l = row_sum of elements
-//     l, l + 8, ...), then the scalar tail and the 8 lanes are added one by one to 0; n < 8 uses
-//     row_sum directly.
-// One thread evaluates these sequentially with round-to-nearest adds (no contraction or
-// reassociation), so the result is bit-identical to the reference's fp32 value.
-// ---------------------------------------------------------------------------------------------
-__device__ int tc_ceil_log2(int n) {
-  if (n <= 2) return 1;
-  return 32 - __clz((unsigned)(n - 1));
-}
-
-template <typename Load>
-__device__ float tc_cascade(const Load& x, int start, int stride, int n) {
-  const int power = max(4, tc_ceil_log2(n) / 4);
-  const int step = 1 << power, mask = step - 1;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int i = 0;
-  while (i + step <= n) {
-    for (int j = 0; j < step; ++j, ++i) acc[0] = wa_add_rn(acc[0], x(start + i * stride));
-    for (int j = 1; j < 4; ++j) {
-      acc[j] = wa_add_rn(acc[j], acc[j - 1]);
-      acc[j - 1] = 0.f;
-      if ((i & (mask << (j * power))) != 0) break;
-    }
-  }
-  for (; i < n; ++i) acc[0] = wa_add_rn(acc[0], x(start + i * stride));
-  for (int j = 1; j < 4; ++j) acc[0] = wa_add_rn(acc[0], acc[j]);
-  return acc[0];
-}
-
-template <typename Load>
-__device__ float tc_row_sum(const Load& x, int start, int stride, int n) {
-  const int groups = n / 4;
-  float part[4];
-  for (int k = 0; k < 4; ++k) part[k] = tc_cascade(x, start + k * stride, 4 * stride, groups);
-  for (int i = groups * 4; i < n; ++i) part[0] = wa_add_rn(part[0], x(start + i * stride));
-  for (int k = 1; k < 4; ++k) part[0] = wa_add_rn(part[0], part[k]);
-  return part[0];
-}
-
-template <typename Load>
-__device__ float tc_inner_sum(const Load& x, int start, int n) {
-  constexpr int L = 8;
-  if (n < L) return tc_row_sum(x, start, 1, n);
-  const int nv = n / L;
-  float fin = 0.f;
-  for (int k = nv * L; k < n; ++k) fin = wa_add_rn(fin, x(start + k));
-  for (int l = 0; l < L; ++l) fin = wa_add_rn(fin, tc_row_sum(x, start + l, L, nv));
-  return fin;
 }
 
 // Sum over (batch, query block) of one head's row Ginis g[(b * H + h) * Nq + i], as torch sums
@@ -282,11 +256,12 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
         const float* kr = kbase + (int64_t)j * p.D;
         if (vec) {
           for (int d = 4 * tg; d < p.D; d += 32) {
-            const f32x4 kv = *(const f32x4*)(kr + d);
-            s = fmaf(qrow[d], pooled_key(p, kv[0], j), s);
-            s = fmaf(qrow[d + 1], pooled_key(p, kv[1], j), s);
-            s = fmaf(qrow[d + 2], pooled_key(p, kv[2], j), s);
-            s = fmaf(qrow[d + 3], pooled_key(p, kv[3], j), s);
+            f32x4 kv[1] = {*(const f32x4*)(kr + d)};
+            pooled_key_row(p, kv, j);
+            s = fmaf(qrow[d], kv[0][0], s);
+            s = fmaf(qrow[d + 1], kv[0][1], s);
+            s = fmaf(qrow[d + 2], kv[0][2], s);
+            s = fmaf(qrow[d + 3], kv[0][3], s);
           }
         } else {
           for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], pooled_key(p, kr[d], j), s);
@@ -402,11 +377,12 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return ((uint64_t)hi << 32) | lo;
 }
 
-template <int KPL, int DK, int R>
+template <int KPL, int DK, int R, bool SUMS>
 __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   constexpr int NP = 64 * KPL;
   __shared__ __attribute__((aligned(16))) float q_sh[R][256];
   __shared__ float s_sh[R][NP];
+  __shared__ __attribute__((aligned(16))) float last_sh[SUMS ? 256 : 4];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
   if (clear_unrouted(p)) return;
   const int i0 = blockIdx.x * R, hs = blockIdx.y, b = blockIdx.z;
@@ -419,26 +395,38 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   // 1. scores of the four rows. With the head dim known at compile time (and N <= 256: one key
   // block per thread), this thread's pooled key row is loaded whole before the pooled queries are
   // staged, so both latencies overlap.
+  // With cached sums and a power-of-two block size, a partial last block is the only row whose
+  // means divide: the workgroup converts it once into LDS instead of one thread dividing D times.
+  const bool last_in_lds = SUMS && p.inv_bs != 0.f && !p.k_sum_div;
   f32x4 kv[DK ? DK / 4 : 1];
   auto load_key = [&](int j) {
     const int jj = min(j, N - 1);
     const float* kr = kbase + (int64_t)jj * D;
 #pragma unroll
     for (int c = 0; c < (DK ? DK / 4 : 1); ++c) kv[c] = *(const f32x4*)(kr + 4 * c);
-    if (p.k_sum_len > 0) {
-#pragma unroll
-      for (int c = 0; c < (DK ? DK / 4 : 1); ++c) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) kv[c][e] = pooled_key(p, kv[c][e], jj);
-      }
+    if constexpr (SUMS) {
+      if (!(last_in_lds && jj == N - 1)) pooled_key_row(p, kv, jj);
     }
   };
   if (DK) load_key(tid);
+  if constexpr (SUMS) {
+    if (last_in_lds) {
+      const float* kr = kbase + (int64_t)(N - 1) * D;
+      const float real = (float)(p.k_sum_len - (N - 1) * p.Bs);
+      for (int d = tid; d < D; d += 256) last_sh[d] = (p.k_sum_bf16 ? wa_bf16_round(kr[d]) : kr[d]) / real;
+    }
+  }
   for (int u = tid; u < R * D; u += 256) {
     const int r = u / D, d = u % D;
     q_sh[r][d] = i0 + r < p.Nq ? p.qp[(row0 + i0 + r) * D + d] : 0.f;
   }
   __syncthreads();
+  if constexpr (SUMS && DK != 0) {
+    if (last_in_lds && tid == N - 1) {
+#pragma unroll
+      for (int c = 0; c < DK / 4; ++c) kv[c] = *(const f32x4*)(&last_sh[4 * c]);
+    }
+  }
   for (int j = tid; j < N; j += 256) {
     float acc[R];
 #pragma unroll
@@ -469,8 +457,14 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
 #pragma unroll
           for (int c = 0; c < 8; ++c) {
             kc[c] = *(const f32x4*)(kr + d0 + 4 * c);
+          }
+          if constexpr (SUMS) {
+            if (last_in_lds && j == N - 1) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) kc[c][e] = pooled_key(p, kc[c][e], j);
+              for (int c = 0; c < 8; ++c) kc[c] = *(const f32x4*)(&last_sh[d0 + 4 * c]);
+            } else {
+              pooled_key_row(p, kc, j);
+            }
           }
 #pragma unroll
           for (int r = 0; r < R; ++r) {
@@ -486,7 +480,7 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
         }
       } else {
         for (int d = 0; d < D; ++d) {
-          const float kd = pooled_key(p, kr[d], j);
+          const float kd = SUMS ? (last_in_lds && j == N - 1 ? last_sh[d] : pooled_key(p, kr[d], j)) : kr[d];
 #pragma unroll
           for (int r = 0; r < R; ++r) acc[r] = fmaf(q_sh[r][d], kd, acc[r]);
         }
@@ -752,6 +746,22 @@ extern "C" int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, in
   return ((rows * Nkv + rows) * 4 + 255) / 256 * 256;
 }
 
+namespace {
+template <bool SUMS>
+void route_wave_launch(const RouteParams& rp, int64_t D, int64_t Nkv, dim3 wgrid, hipStream_t s) {
+  if (D == 128 && Nkv <= 256) {
+    if (Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 128, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+    else if (Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 128, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+    else hipLaunchKernelGGL((route_wave_kernel<4, 128, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+  } else {
+    if (Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 0, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+    else if (Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 0, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+    else if (Nkv <= 256) hipLaunchKernelGGL((route_wave_kernel<4, 0, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+    else hipLaunchKernelGGL((route_wave_kernel<8, 0, 2, SUMS>), wgrid, dim3(256), 0, s, rp);
+  }
+}
+}  // namespace
+
 extern "C" int wa_route(const wa_route_args* a, void* stream) {
   WA_CHECK_ARG(a && a->index && a->num, "wa_route: null output");
   WA_CHECK_ARG(a->probs || (a->q_pooled && a->k_pooled), "wa_route: need probs or pooled q/k");
@@ -780,6 +790,8 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.k_sum_len = a->k_sum_len > 0 ? (int)a->k_sum_len : 0;
   rp.Bs = (int)(a->block_size > 0 ? a->block_size : 1);
   rp.k_sum_bf16 = a->k_sum_bf16;
+  rp.inv_bs = (rp.Bs & (rp.Bs - 1)) == 0 ? 1.0f / (float)rp.Bs : 0.f;
+  rp.k_sum_div = rp.k_sum_len > 0 && rp.k_sum_len % rp.Bs == 0;
   WA_CHECK_ARG(a->k_pooled_blocks == 0 || a->k_pooled_blocks >= a->Nkv, "wa_route: k_pooled_blocks < Nkv");
   rp.kp_blocks = (int)(a->k_pooled_blocks > 0 ? a->k_pooled_blocks : a->Nkv);
   const int64_t rows = a->B * a->H * a->Nq;
@@ -789,16 +801,8 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (a->mode == WA_ROUTE_TOPK && !a->probs && !a->probs_out && a->Nkv <= 512) {
     const dim3 wgrid((unsigned)((a->Nq + 1) / 2) + 1, (unsigned)nh, (unsigned)a->B);
-    if (a->D == 128 && a->Nkv <= 256) {
-      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 128, 2>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 128, 2>), wgrid, dim3(256), 0, s, rp);
-      else hipLaunchKernelGGL((route_wave_kernel<4, 128, 2>), wgrid, dim3(256), 0, s, rp);
-    } else {
-      if (a->Nkv <= 64) hipLaunchKernelGGL((route_wave_kernel<1, 0, 2>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 128) hipLaunchKernelGGL((route_wave_kernel<2, 0, 2>), wgrid, dim3(256), 0, s, rp);
-      else if (a->Nkv <= 256) hipLaunchKernelGGL((route_wave_kernel<4, 0, 2>), wgrid, dim3(256), 0, s, rp);
-      else hipLaunchKernelGGL((route_wave_kernel<8, 0, 2>), wgrid, dim3(256), 0, s, rp);
-    }
+    if (rp.k_sum_len > 0) route_wave_launch<true>(rp, a->D, a->Nkv, wgrid, s);
+    else route_wave_launch<false>(rp, a->D, a->Nkv, wgrid, s);
     return wa_launch_status("route_wave");
   }
   hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);
@@ -807,95 +811,6 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipLaunchKernelGGL(gini_count_kernel, dim3((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B), dim3(64),
                      (size_t)a->Nkv * sizeof(float), s, rp);
   return wa_launch_status("route_gini_count");
-}
-
-namespace {
-
-// Copy of a [B, n, H, D] BLHD tensor into another, 16 bytes per thread (VEC elements of T).
-template <typename T, int VEC>
-__global__ void __launch_bounds__(256) kv_copy_kernel(const T* src, int64_t s_sb, int64_t s_st, int64_t s_sh, T* dst,
-                                                      int64_t d_sb, int64_t d_st, int64_t d_sh, int B, int n, int H,
-                                                      int D) {
-  const int64_t cpr = D / VEC;  // chunks per head row
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)B * n * H * cpr;
-  if (i >= total) return;
-  const int c = (int)(i % cpr);
-  const int64_t r = i / cpr;
-  const int h = (int)(r % H), t = (int)((r / H) % n), b = (int)(r / ((int64_t)H * n));
-  const T* sp = src + b * s_sb + t * s_st + h * s_sh + c * VEC;
-  T* dp = dst + b * d_sb + t * d_st + h * d_sh + c * VEC;
-  if constexpr (VEC * sizeof(T) == 16) {
-    *(u32x4*)dp = *(const u32x4*)sp;
-  } else {
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) dp[e] = sp[e];
-  }
-}
-
-int kv_copy(const void* src, int64_t s_sb, int64_t s_st, int64_t s_sh, void* dst, int64_t d_sb, int64_t d_st,
-            int64_t d_sh, int dtype, int64_t B, int64_t n, int64_t H, int64_t D, hipStream_t s) {
-  const int es = dtype == WA_BF16 ? 2 : 4;
-  const int vec = 16 / es;
-  const bool v16 = wa_aligned16(src) && wa_aligned16(dst) && D % vec == 0 && s_sb % vec == 0 && s_st % vec == 0 &&
-                   s_sh % vec == 0 && d_sb % vec == 0 && d_st % vec == 0 && d_sh % vec == 0;
-  const int64_t total = B * n * H * (v16 ? D / vec : D);
-  if (total == 0) return WA_OK;
-  const dim3 grid((unsigned)((total + 255) / 256));
-  if (dtype == WA_BF16) {
-    if (v16)
-      hipLaunchKernelGGL((kv_copy_kernel<bf16_t, 8>), grid, dim3(256), 0, s, (const bf16_t*)src, s_sb, s_st, s_sh,
-                         (bf16_t*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
-    else
-      hipLaunchKernelGGL((kv_copy_kernel<bf16_t, 1>), grid, dim3(256), 0, s, (const bf16_t*)src, s_sb, s_st, s_sh,
-                         (bf16_t*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
-  } else {
-    if (v16)
-      hipLaunchKernelGGL((kv_copy_kernel<float, 4>), grid, dim3(256), 0, s, (const float*)src, s_sb, s_st, s_sh,
-                         (float*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
-    else
-      hipLaunchKernelGGL((kv_copy_kernel<float, 1>), grid, dim3(256), 0, s, (const float*)src, s_sb, s_st, s_sh,
-                         (float*)dst, d_sb, d_st, d_sh, (int)B, (int)n, (int)H, (int)D);
-  }
-  return wa_launch_status("kv_append_copy");
-}
-
-}  // namespace
-
-extern "C" int wa_kv_append(const wa_kv_append_args* a, void* stream) {
-  WA_CHECK_ARG(a && a->cache_k && a->cache_v && a->new_k && a->new_v, "wa_kv_append: null argument");
-  WA_CHECK_ARG(a->dtype == WA_BF16 || a->dtype == WA_F32, "wa_kv_append: dtype must be bf16 or fp32");
-  WA_CHECK_ARG(a->B >= 0 && a->H > 0 && a->D > 0 && a->cap > 0 && a->n >= 0 && a->start >= 0 &&
-                   a->start + a->n <= a->cap,
-               "wa_kv_append: tokens [%lld, %lld) do not fit a cache of %lld", (long long)a->start,
-               (long long)(a->start + a->n), (long long)a->cap);
-  WA_CHECK_ARG(a->B < (1 << 20) && a->cap < ((int64_t)1 << 30) && a->H < (1 << 16) && a->D <= 1024,
-               "wa_kv_append: sizes too large");
-  if (a->B == 0 || a->n == 0) return WA_OK;
-  hipStream_t s = (hipStream_t)stream;
-  const int64_t es = a->dtype == WA_BF16 ? 2 : 4;
-  void* dk = (char*)a->cache_k + a->start * a->ck_st * es;  // token `start` of the cache
-  void* dv = (char*)a->cache_v + a->start * a->cv_st * es;
-  int rc = kv_copy(a->new_k, a->nk_sb, a->nk_st, a->nk_sh, dk, a->ck_sb, a->ck_st, a->ck_sh, a->dtype, a->B, a->n,
-                   a->H, a->D, s);
-  if (rc != WA_OK) return rc;
-  rc = kv_copy(a->new_v, a->nv_sb, a->nv_st, a->nv_sh, dv, a->cv_sb, a->cv_st, a->cv_sh, a->dtype, a->B, a->n, a->H,
-               a->D, s);
-  if (rc != WA_OK || !a->k_sums) return rc;
-  WA_CHECK_ARG(a->block_size > 0, "wa_kv_append: k_sums needs a block size");
-  // sums of the key blocks that hold a new token, over the cache's tokens [0, start + n)
-  wa_pool_args pa{};
-  pa.x = a->cache_k; pa.x_sb = a->ck_sb; pa.x_st = a->ck_st; pa.x_sh = a->ck_sh; pa.x_dtype = a->dtype;
-  pa.B = a->B; pa.L = a->start + a->n; pa.H = a->H; pa.D = a->D; pa.block_size = a->block_size;
-  pa.first_block = a->start / a->block_size;
-  pa.num_blocks = (a->start + a->n + a->block_size - 1) / a->block_size - pa.first_block;
-  pa.heads = a->heads; pa.n_heads = a->n_heads;
-  pa.out = a->k_sums; pa.out_blocks = (a->cap + a->block_size - 1) / a->block_size;
-  pa.emulate_rounding = 1; pa.store_sums = 1;
-  rc = pool_check(&pa);
-  if (rc != WA_OK) return rc;
-  const wa_pool_args* job = &pa;
-  return pool_launch(&job, 1, pool_variant(&pa), s);
 }
 
 extern "C" int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* index,

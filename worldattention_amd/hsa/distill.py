@@ -1,7 +1,13 @@
-"""Attention self-distillation registry (``wan/modules/hsa/distill.py:22-71``).
+"""Per-layer self-distillation of HSA towards dense attention (``wan/modules/hsa/distill.py:22-71``).
 
-Every HSA forward under grad records ``MSE(hsa_out, dense_out.detach())`` when collection is on.
-The dense teacher is torch SDPA — a training signal outside the accelerated attention path.
+While collection is switched on, each HSA forward that runs under autograd adds one scalar,
+``MSE(hsa_out, dense_out)`` with the dense output detached, to a process-wide list; the trainer
+takes the list, sums it and backpropagates into the gate and the low-rank projections
+(``trainer/hsa_stage.py:149-165``). Switching collection off empties the list.
+
+The dense teacher is this library's flash kernel (``wa_bsa_fwd`` over every key block, bf16
+operands, fp32 softmax and accumulation), not torch SDPA: it reads ``[B, L, H, D]`` q/k/v in place
+and never materialises the ``L x L`` scores.
 """
 from __future__ import annotations
 
@@ -10,44 +16,69 @@ from typing import List
 import torch
 import torch.nn.functional as F
 
+from .. import _lib
+from .block_sparse import bsa_forward
+
 __all__ = ["enable_distill", "distill_enabled", "pop_distill_losses", "record_distill_loss",
            "dense_attention", "record_against_dense"]
 
-_ENABLED = False
-_LOSSES: List[torch.Tensor] = []
+
+class _Collector:
+    """The on/off switch and the losses gathered since the trainer last took them."""
+
+    def __init__(self) -> None:
+        self.on = False
+        self.items: List[torch.Tensor] = []
+
+    def switch(self, on: bool) -> None:
+        self.on = bool(on)
+        if not self.on:
+            self.items = []
+
+    def take(self) -> List[torch.Tensor]:
+        got, self.items = self.items, []
+        return got
+
+
+_COLLECTOR = _Collector()
 
 
 def enable_distill(flag: bool = True) -> None:
-    """Turn collection on or off; turning it off clears the registry."""
-    global _ENABLED
-    _ENABLED = bool(flag)
-    if not _ENABLED:
-        _LOSSES.clear()
+    """Switch collection on (``True``) or off (``False``, which also drops what was gathered)."""
+    _COLLECTOR.switch(flag)
 
 
 def distill_enabled() -> bool:
-    return _ENABLED
+    return _COLLECTOR.on
 
 
 def pop_distill_losses() -> List[torch.Tensor]:
-    """Return the losses recorded since the last pop and clear the registry."""
-    global _LOSSES
-    losses, _LOSSES = _LOSSES, []
-    return losses
+    """The losses gathered since the previous call; the registry is left empty."""
+    return _COLLECTOR.take()
 
 
 def record_distill_loss(loss: torch.Tensor) -> None:
-    _LOSSES.append(loss)
+    _COLLECTOR.items.append(loss)
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-    """Full attention over ``[B, L, H, D]`` tensors (the distillation target)."""
-    query, key, value = (t.transpose(1, 2) for t in (q, k, v))
-    return F.scaled_dot_product_attention(query, key, value).transpose(1, 2)
+    """Softmax attention of ``[B, Lq, H, D]`` queries over all ``[B, Lkv, H, D]`` keys, scale
+    ``D ** -0.5``, no mask: the target HSA is distilled towards. Runs the dense flash kernel on
+    bf16 copies of the operands (head dim 64 or 128); the result has ``q``'s dtype."""
+    d = q.shape[-1]
+    if d not in (64, 128):
+        raise ValueError(f"the dense teacher kernel needs head dim 64 or 128, got {d}")
+    if k.shape != v.shape or k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)} and v {tuple(v.shape)} do not match")
+    block = 128 if d == 128 else 64
+    qb, kb, vb = (_lib.kernel_ready(t.detach()) for t in (q, k, v))
+    out, _ = bsa_forward(qb, kb, vb, index=None, num=None, block_size=block, layout="blhd",
+                         out_dtype=q.dtype if q.dtype in (torch.float32, torch.bfloat16) else torch.float32)
+    return out if out.dtype == q.dtype else out.to(q.dtype)
 
 
 def record_against_dense(hsa_out: torch.Tensor, q, k, v) -> None:
-    """Record the MSE between an HSA output and dense attention over the same window."""
+    """Gather ``MSE(hsa_out, dense_attention(q, k, v))``; gradients reach ``hsa_out`` only."""
     with torch.no_grad():
-        teacher = dense_attention(q, k, v).to(hsa_out.dtype)
-    record_distill_loss(F.mse_loss(hsa_out.float(), teacher.float().detach()))
+        teacher = dense_attention(q, k, v).to(hsa_out.dtype).float()
+    record_distill_loss(F.mse_loss(hsa_out.float(), teacher))

@@ -27,7 +27,7 @@ import torch
 from .. import _lib
 from .attention import _compress
 
-__all__ = ["kv_append", "new_block_sums"]
+__all__ = ["kv_append", "new_block_sums", "qkv_epilogue", "kv_roll", "cache_step"]
 
 
 def new_block_sums(k_cache: torch.Tensor, block_size: int) -> torch.Tensor:
@@ -116,3 +116,222 @@ def kv_append(kv_cache: dict, k_new: torch.Tensor, v_new: torch.Tensor, *, write
         "new_k_coarse": new_kc,
         "new_v_coarse": new_vc,
     }
+
+
+def _grid3(grid_sizes):
+    """``(f, h, w)`` from a ``[B, 3]`` tensor / nested list / triple; every sample must share it."""
+    if isinstance(grid_sizes, torch.Tensor):
+        rows = grid_sizes.reshape(-1, 3).tolist()
+    elif len(grid_sizes) and isinstance(grid_sizes[0], (list, tuple)):
+        rows = [list(r) for r in grid_sizes]
+    else:
+        rows = [list(grid_sizes)]
+    if any(r != rows[0] for r in rows):
+        raise ValueError(f"the fused epilogue needs one grid for the whole batch, got {rows}")
+    return tuple(int(x) for x in rows[0])
+
+
+def _table(freqs: torch.Tensor, dev) -> torch.Tensor:
+    """The RoPE table as device fp64 (re, im) pairs ``[rows, D/2, 2]``."""
+    t = torch.view_as_real(freqs) if freqs.is_complex() else freqs
+    if t.dtype != torch.float64:
+        raise ValueError(f"freqs must be the complex128 RoPE table, got {freqs.dtype}")
+    return t.to(dev).contiguous()
+
+
+def qkv_epilogue(q, k, v, kv_cache: dict, *, grid_sizes, freqs, start_frame: int, write_start: int,
+                 src_offset: int = 0, write_len: Optional[int] = None, norm_q=None, norm_k=None, eps: float = 1e-6,
+                 block_size: Optional[int] = None) -> torch.Tensor:
+    """One launch for a layer's q / k / v projections ``[B, n, H, D]``: returns ``rope(norm_q(q))``
+    and writes ``rope(norm_k(k))`` / ``v`` tokens ``[src_offset, src_offset + write_len)`` to cache
+    tokens ``[write_start, ...)`` (``wa_qkv_epilogue``). ``norm_q`` / ``norm_k``: the RMSNorm
+    weights ``[H * D]`` (or None: no norm); ``freqs``: the model's complex128 RoPE table. With
+    ``block_size``, ``kv_cache["k_block_sums"]`` is kept as :func:`kv_append` keeps it."""
+    kc, vc = kv_cache["k"], kv_cache["v"]
+    dev = _lib.require_gpu(q, k, v, kc, vc)
+    if not (q.shape == k.shape == v.shape) or q.dim() != 4:
+        raise ValueError(f"q, k, v must be matching [B, n, H, D], got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    bsz, n, heads, d = q.shape
+    if kc.shape[0] != bsz or tuple(kc.shape[2:]) != (heads, d) or vc.shape != kc.shape:
+        raise ValueError(f"cache {tuple(kc.shape)} does not hold [B={bsz}, cap, H={heads}, D={d}] tokens")
+    dtype = kc.dtype
+    if dtype not in (torch.bfloat16, torch.float32) or vc.dtype != dtype:
+        raise ValueError(f"cache dtype must be bf16 or fp32, got {kc.dtype} / {vc.dtype}")
+    if (norm_q is None) != (norm_k is None):
+        raise ValueError("give both RMSNorm weights or neither")
+    ready = [_lib.kernel_ready(t, dtype) for t in (q, k, v)]
+    q_out = torch.empty((bsz, n, heads, d), dtype=dtype, device=dev)
+    table = _table(freqs, dev)
+    f, gh, gw = _grid3(grid_sizes)
+    wlen = n - src_offset if write_len is None else int(write_len)
+    sums = None
+    if block_size is not None:
+        sums = kv_cache.get("k_block_sums")
+        if sums is None:
+            sums = new_block_sums(kc, block_size)
+            kv_cache["k_block_sums"] = sums
+    wq = wk = None
+    w_dtype = 0
+    if norm_q is not None:
+        if norm_q.numel() != heads * d or norm_k.numel() != heads * d:
+            raise ValueError(f"RMSNorm weights must hold H * D = {heads * d} values")
+        wdt = norm_q.dtype if norm_q.dtype in (torch.bfloat16, torch.float32) else torch.float32
+        wq = norm_q.detach().to(dev, wdt).contiguous()
+        wk = norm_k.detach().to(dev, wdt).contiguous()
+        w_dtype = _lib.dtype_code(wq)
+    qq, kk, vv = (_lib.blhd(t) for t in ready)
+    qo, ck, cv = _lib.blhd(q_out), _lib.blhd(kc), _lib.blhd(vc)
+    args = _lib.QkvEpilogueArgs(*qq, *kk, *vv, _lib.dtype_code(kc), bsz, n, heads, d, *qo, *ck, *cv,
+                                kc.shape[1], int(write_start), int(src_offset), wlen, table.data_ptr(),
+                                table.shape[0], f, gh, gw, int(start_frame), _lib.ptr(wq), _lib.ptr(wk), w_dtype,
+                                float(eps), _lib.ptr(sums), int(block_size or 0))
+    _lib.call("wa_qkv_epilogue", args, _lib.stream_ptr(dev))
+    return q_out
+
+
+def kv_roll(kv_cache: dict, *, sink_tokens: int, num_evicted: int, num_rolled: int,
+            block_size: Optional[int] = None, hsa_module=None, heads: Optional[Sequence[int]] = None) -> None:
+    """Move cache tokens ``[sink + evicted, sink + evicted + rolled)`` to ``[sink, sink + rolled)``
+    in place (``wa_kv_roll``), with the coarse rows of those segments when the cache has a coarse
+    tier and ``hsa_module`` is given (``causal_model.py:326-356``), and the key block sums."""
+    kc, vc = kv_cache["k"], kv_cache["v"]
+    dev = _lib.require_gpu(kc, vc)
+    bsz, cap, heads_n, d = kc.shape
+    sums = kv_cache.get("k_block_sums")
+    if sums is not None and block_size is None:
+        raise ValueError("kv_cache holds k_block_sums: pass the block_size they were made with")
+    heads_t = _lib.head_list(heads, dev) if heads is not None else None
+    coarse = hsa_module is not None and "k_coarse" in kv_cache and "v_coarse" in kv_cache
+    c_dst = c_src = c_rows = 0
+    kcc = vcc = None
+    if coarse:
+        _, c_dst = hsa_module.token_range_to_coarse(0, int(sink_tokens))
+        c_src, c_end = hsa_module.token_range_to_coarse(int(sink_tokens + num_evicted),
+                                                        int(sink_tokens + num_evicted + num_rolled))
+        c_rows = max(0, c_end - c_src)
+        kcc, vcc = kv_cache["k_coarse"], kv_cache["v_coarse"]
+        if kcc.dtype != kc.dtype or vcc.dtype != kc.dtype:
+            raise ValueError("the coarse tier must have the cache dtype")
+    kp, vp = _lib.blhd(kc), _lib.blhd(vc)
+    kcp = _lib.blhd(kcc) if coarse else (None, 0, 0, 0)
+    vcp = _lib.blhd(vcc) if coarse else (None, 0, 0, 0)
+    args = _lib.KvRollArgs(*kp, *vp, _lib.dtype_code(kc), bsz, cap, heads_n, d, int(sink_tokens), int(num_evicted),
+                           int(num_rolled), _lib.ptr(sums), int(block_size or 0), _lib.ptr(heads_t),
+                           0 if heads_t is None else heads_t.numel(), *kcp, *vcp,
+                           kcc.shape[1] if coarse else 0, c_dst, c_src, c_rows)
+    _lib.call("wa_kv_roll", args, _lib.stream_ptr(dev))
+
+
+def _index(kv_cache: dict, key: str) -> int:
+    t = kv_cache[key]
+    return int(t.item()) if isinstance(t, torch.Tensor) else int(t)
+
+
+def cache_step(kv_cache: dict, q, k, v, *, grid_sizes, freqs, current_start: int, sink_size: int,
+               local_attn_size: int, max_attention_size: int, norm_q=None, norm_k=None, eps: float = 1e-6,
+               hsa_module=None, block_size: Optional[int] = None, sink_recache_after_switch: bool = False):
+    """The cache side of one ``CausalWanSelfAttention.forward`` call with a KV cache
+    (``causal_model.py:268-437`` and the commit ``:1016-1119``), in place on the GPU.
+
+    ``q``, ``k``, ``v``: the layer's projections ``[B, n, H, D]`` before the RMSNorm (weights
+    ``norm_q`` / ``norm_k``, or None) and RoPE. The roll (when the window is full) is
+    :func:`kv_roll`, the norm + RoPE + insert one :func:`qkv_epilogue` launch, and a coarse tier
+    (``kv_cache["k_coarse"/"v_coarse"]`` with ``hsa_module``) gets the written segments compressed
+    into its slots. ``kv_cache["global_end_index"]`` / ``["local_end_index"]`` move as the
+    reference's commit moves them (not for a recompute). With ``block_size`` the key block sums are
+    kept for routing (``hsa_attention(..., k_block_sums=...)``).
+
+    Returns ``(roped_q, attn_k, attn_v, attn_kc, attn_vc, info)``: the attention inputs of
+    ``run_hsa_core_attn`` (views of the cache where the window is one contiguous range; the
+    reference's ``torch.cat`` of sink and local range otherwise) and the update record, whose
+    ``"k_block_sums"`` is the tensor to pass to ``hsa_attention`` (None unless the window is the
+    cache's first tokens and sums are kept).
+    """
+    f, gh, gw = _grid3(grid_sizes)
+    frame_seqlen = gh * gw
+    start_frame = current_start // frame_seqlen
+    n = q.shape[1]
+    current_end = current_start + n
+    sink = sink_size * frame_seqlen
+    cap = kv_cache["k"].shape[1]
+    global_end = _index(kv_cache, "global_end_index")
+    local_end = _index(kv_cache, "local_end_index")
+    coarse = hsa_module is not None and "k_coarse" in kv_cache and "v_coarse" in kv_cache
+    recompute = current_end <= global_end and current_start > 0
+    roll = local_attn_size != -1 and current_end > global_end and n + local_end > cap
+    evicted = rolled = 0
+    if roll:
+        evicted = n + local_end - cap
+        rolled = local_end - evicted - sink
+        new_local_end = local_end + current_end - global_end - evicted
+    else:
+        new_local_end = local_end + current_end - global_end
+    local_start = new_local_end - n
+    write_start = max(local_start, sink) if recompute else local_start
+    if not roll and sink_recache_after_switch:
+        write_start = local_start
+    offset = max(0, write_start - local_start)
+    write_len = max(0, new_local_end - write_start)
+    if coarse and write_len > 0:  # refused before anything is written, as the reference's step refuses
+        c0, c1 = hsa_module.token_range_to_coarse(write_start, new_local_end)
+    if roll:
+        kv_roll(kv_cache, sink_tokens=sink, num_evicted=evicted, num_rolled=rolled, block_size=block_size,
+                hsa_module=hsa_module if coarse else None)
+    roped_q = qkv_epilogue(q, k, v, kv_cache, grid_sizes=(f, gh, gw), freqs=freqs, start_frame=start_frame,
+                           write_start=write_start, src_offset=offset, write_len=write_len, norm_q=norm_q,
+                           norm_k=norm_k, eps=eps, block_size=block_size)
+    kc, vc = kv_cache["k"], kv_cache["v"]
+    new_kc = new_vc = None
+    if coarse and write_len > 0:
+        new_kc, new_vc = kv_cache["k_coarse"][:, c0:c1], kv_cache["v_coarse"][:, c0:c1]
+        seg, bsm = hsa_module.proj_segment_len, hsa_module.block_size
+        with torch.no_grad():
+            _compress(kc[:, write_start:new_local_end], hsa_module.k_proj_mat, segment_len=seg, block_size=bsm,
+                      layout="blhd", out=new_kc)
+            _compress(vc[:, write_start:new_local_end], hsa_module.v_proj_mat, segment_len=seg, block_size=bsm,
+                      layout="blhd", out=new_vc)
+
+    def coarse_slice(a, b):
+        if not coarse:
+            return None, None
+        s0, s1 = hsa_module.token_range_to_coarse(a, b)
+        return kv_cache["k_coarse"][:, s0:s1], kv_cache["v_coarse"][:, s0:s1]
+
+    if sink > 0:
+        budget = max_attention_size - sink
+        if budget > 0:
+            lsw = max(sink, new_local_end - budget)
+            if lsw == sink:  # sink and local range are one contiguous run: views, no copy
+                attn_k, attn_v = kc[:, :new_local_end], vc[:, :new_local_end]
+                attn_kc, attn_vc = coarse_slice(0, new_local_end)
+            else:
+                attn_k = torch.cat([kc[:, :sink], kc[:, lsw:new_local_end]], dim=1)
+                attn_v = torch.cat([vc[:, :sink], vc[:, lsw:new_local_end]], dim=1)
+                attn_kc = attn_vc = None
+                if coarse:
+                    ks, vs = coarse_slice(0, sink)
+                    kl, vl = coarse_slice(lsw, new_local_end)
+                    attn_kc, attn_vc = torch.cat([ks, kl], dim=1), torch.cat([vs, vl], dim=1)
+        else:
+            attn_k, attn_v = kc[:, :sink], vc[:, :sink]
+            attn_kc, attn_vc = coarse_slice(0, sink)
+    else:
+        ws = max(0, new_local_end - max_attention_size)
+        attn_k, attn_v = kc[:, ws:new_local_end], vc[:, ws:new_local_end]
+        attn_kc, attn_vc = coarse_slice(ws, new_local_end)
+    if not recompute:
+        for key, val in (("global_end_index", current_end), ("local_end_index", new_local_end)):
+            if isinstance(kv_cache[key], torch.Tensor):
+                kv_cache[key].fill_(val)
+            else:
+                kv_cache[key] = val
+    info = {"action": "roll_and_insert" if roll else "direct_insert", "sink_tokens": sink,
+            "num_rolled_tokens": rolled, "num_evicted_tokens": evicted, "local_start_index": local_start,
+            "local_end_index": new_local_end, "write_start_index": write_start, "write_end_index": new_local_end,
+            "new_k": kc[:, write_start:new_local_end], "new_v": vc[:, write_start:new_local_end],
+            "new_k_coarse": new_kc, "new_v_coarse": new_vc, "current_end": current_end, "is_recompute": recompute}
+    # the cached key sums describe the window only when it is the cache's first tokens
+    prefix = attn_k.data_ptr() == kc.data_ptr() and attn_k.shape[1] == new_local_end
+    info["k_block_sums"] = kv_cache.get("k_block_sums") if prefix and block_size is not None else None
+    return roped_q, attn_k, attn_v, attn_kc, attn_vc, info
