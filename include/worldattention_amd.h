@@ -28,6 +28,7 @@ extern "C" {
 #define WA_OK 0
 #define WA_ERR_ARG (-1)
 #define WA_ERR_UNSUPPORTED (-2)
+#define WA_ERR_IO (-3)
 
 enum { WA_F32 = 0, WA_BF16 = 1 };
 enum { WA_ROUTE_GINI = 0, WA_ROUTE_TOPK = 1 };
@@ -473,6 +474,44 @@ typedef struct wa_hkv_copy {
 } wa_hkv_copy;
 int wa_hkv_gather_async(const wa_hkv_copy* copies, int64_t n, void* stream, void* done);
 int wa_hkv_store_async(const wa_hkv_copy* copies, int64_t n, void* stream, void* done);
+
+/* Asynchronous file I/O of the HKV NVMe tier: replaces the synchronous torch.save / torch.load of a
+ * spilled chunk (pipeline/hkv/tiering.py:89-105). wa_io_write_async / wa_io_read_async move the n
+ * host buffers (bufs[i], sizes[i] bytes) to / from the file at `path`, buffer i at the 4 KiB-aligned
+ * offset sum(round_up(sizes[j], 4096), j < i), on a worker thread, with O_DIRECT when `direct` is
+ * set and the file system takes it (buffered I/O otherwise; page-aligned buffers go to the device
+ * directly, the rest through an aligned bounce buffer). The file is opened (created, for a write)
+ * before the call returns; the buffers must stay valid until wa_io_wait. Returns a handle > 0, or
+ * a negative status. wa_io_done: 1 when the transfer has finished, 0 while it runs;
+ * wa_io_direct: 1 if O_DIRECT is in use; wa_io_wait: joins the transfer and releases the handle
+ * (WA_OK, or WA_ERR_IO with the reason in wa_last_error). No reference counterpart beyond the
+ * tier's spill / reload. */
+int64_t wa_io_write_async(const char* path, const void* const* bufs, const int64_t* sizes, int64_t n, int32_t direct);
+int64_t wa_io_read_async(const char* path, void* const* bufs, const int64_t* sizes, int64_t n, int32_t direct);
+int wa_io_done(int64_t handle);
+int wa_io_direct(int64_t handle);
+int wa_io_wait(int64_t handle);
+
+/* Page install with the re-rope fused in: replaces the page-by-page install + rotation of
+ * HKVCache.apply (pipeline/hkv/cache.py:229-246, shift_temporal_rope per page at :233-238). Each
+ * page (a pinned host [B, tokens, H, D] view, element strides) is read by a kernel through its
+ * device mapping and written to cache tokens [dst_token, dst_token + tokens) of `dst`
+ * ([B, cap, H, D] on the device), its temporal band (complex pairs < n_temporal) multiplied by
+ * factor row i of `factors` ([n_pages, n_temporal] complex fp32 as (re, im) pairs, device; NULL:
+ * plain copy) as wa_rerope does, so the installed keys need no second pass over HBM. Pages must
+ * stay alive until the stream passes the launch. */
+typedef struct wa_hkv_page {
+  const void* src; int64_t s_sb, s_st, s_sh;
+  int64_t tokens, dst_token;
+} wa_hkv_page;
+typedef struct wa_hkv_gather_rotate_args {
+  const wa_hkv_page* pages; int64_t n_pages;
+  void* dst; int64_t d_sb, d_st, d_sh;
+  int32_t dtype;
+  int64_t B, cap, H, D;
+  const float* factors; int64_t n_temporal;
+} wa_hkv_gather_rotate_args;
+int wa_hkv_gather_rotate(const wa_hkv_gather_rotate_args* args, void* stream);
 
 #ifdef __cplusplus
 }

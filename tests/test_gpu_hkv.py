@@ -195,6 +195,42 @@ def test_in_place_rotation_by_rows_touches_only_the_range():
     assert torch.equal(kd.cpu()[:, :5], k[:, :5]) and torch.equal(kd.cpu()[:, 30:], k[:, 30:])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gather_rotate_equals_copy_then_rerope(dtype):
+    """The fused install (pinned pages read by the kernel, re-rope on the way) against DMA copies
+    followed by the in-place rotation: bit-identical keys, 40 pages (two launches), pages of
+    unequal length out of order, and untouched tokens outside the pages; without factors it is
+    a plain copy. Pageable pages are refused."""
+    torch.manual_seed(3)
+    d, h, b = 128, 3, 2
+    nt = O.temporal_complex_dims(d)
+    band = O.temporal_band(O.rope_freqs(128, d), d)
+    blob = torch.randn(b, 900, h, d).to(dtype).pin_memory()
+    spans = [(i * 20 + (i % 3), i * 20 + (i % 3) + 7 + (i % 5)) for i in range(40)]
+    spans.reverse()
+    pages, off = [], 0
+    for s0, s1 in spans:
+        pages.append((blob[:, s0:s1], off))
+        off += s1 - s0
+    factors = _ops.factor_table(band, torch.arange(40) + 50, torch.arange(40), torch.device(DEV))
+    cap = off + 9
+    got = torch.full((b, cap, h, d), 3.0, dtype=dtype, device=DEV)
+    _ops.gather_rotate(pages, got, factors)
+    want = torch.full((b, cap, h, d), 3.0, dtype=dtype, device=DEV)
+    rows = []
+    for i, (src, o) in enumerate(pages):
+        want[:, o:o + src.shape[1]] = src.to(DEV)
+        rows += [i] * src.shape[1]
+    _ops.rotate_temporal(want, factors, rows=torch.tensor(rows, dtype=torch.int32, device=DEV), t0=0, t1=off)
+    assert torch.equal(got.cpu(), want.cpu())
+    plain = torch.zeros_like(got)
+    _ops.gather_rotate(pages, plain, None)
+    for src, o in pages:
+        assert torch.equal(plain[:, o:o + src.shape[1]].cpu(), src)
+    with pytest.raises(ValueError, match="pinned"):
+        _ops.gather_rotate([(blob[:, :4].clone(), 0)], got, None)
+
+
 # ---------------------------------------------------------------------------------------------
 # host-tier copies
 # ---------------------------------------------------------------------------------------------

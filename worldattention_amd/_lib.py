@@ -17,7 +17,7 @@ import torch
 LIB_PATH = os.environ.get("WORLDATTENTION_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
                                                                    "libworldattention_amd.so")
 
-WA_OK, WA_ERR_ARG, WA_ERR_UNSUPPORTED = 0, -1, -2
+WA_OK, WA_ERR_ARG, WA_ERR_UNSUPPORTED, WA_ERR_IO = 0, -1, -2, -3
 WA_F32, WA_BF16 = 0, 1
 WA_ROUTE_GINI, WA_ROUTE_TOPK = 0, 1
 WA_EPI_PLAIN, WA_EPI_FUSE, WA_EPI_GATED = 0, 1, 2
@@ -84,6 +84,19 @@ KvRollArgs = _struct("wa_kv_roll_args", [
     ("k_coarse", c_void_p), ("kc_sb", c_int64), ("kc_st", c_int64), ("kc_sh", c_int64),
     ("v_coarse", c_void_p), ("vc_sb", c_int64), ("vc_st", c_int64), ("vc_sh", c_int64),
     ("coarse_cap", c_int64), ("c_dst", c_int64), ("c_src", c_int64), ("c_rows", c_int64),
+])
+
+HkvPage = _struct("wa_hkv_page", [
+    ("src", c_void_p), ("s_sb", c_int64), ("s_st", c_int64), ("s_sh", c_int64),
+    ("tokens", c_int64), ("dst_token", c_int64),
+])
+
+HkvGatherRotateArgs = _struct("wa_hkv_gather_rotate_args", [
+    ("pages", c_void_p), ("n_pages", c_int64),
+    ("dst", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64),
+    ("dtype", c_int32),
+    ("B", c_int64), ("cap", c_int64), ("H", c_int64), ("D", c_int64),
+    ("factors", c_void_p), ("n_temporal", c_int64),
 ])
 
 BsaFwdArgs = _struct("wa_bsa_fwd_args", [
@@ -236,6 +249,12 @@ SIGNATURES = {
     "wa_kv_append": (c_int, [POINTER(KvAppendArgs), c_void_p]),
     "wa_qkv_epilogue": (c_int, [POINTER(QkvEpilogueArgs), c_void_p]),
     "wa_kv_roll": (c_int, [POINTER(KvRollArgs), c_void_p]),
+    "wa_hkv_gather_rotate": (c_int, [POINTER(HkvGatherRotateArgs), c_void_p]),
+    "wa_io_write_async": (c_int64, [c_char_p, POINTER(c_void_p), POINTER(c_int64), c_int64, c_int32]),
+    "wa_io_read_async": (c_int64, [c_char_p, POINTER(c_void_p), POINTER(c_int64), c_int64, c_int32]),
+    "wa_io_done": (c_int, [c_int64]),
+    "wa_io_direct": (c_int, [c_int64]),
+    "wa_io_wait": (c_int, [c_int64]),
     "wa_bsa_fwd_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_bsa_fwd_noalloc": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
@@ -278,6 +297,8 @@ def call(name: str, *args) -> None:
     rc = getattr(lib(), name)(*args)
     if rc != 0:
         msg = lib().wa_last_error().decode(errors="replace")
+        if rc == WA_ERR_IO:
+            raise OSError(f"{name}: {msg}")
         if rc < 0:
             raise ValueError(f"{name}: {msg}")
         raise RuntimeError(f"{name} failed (hip error {rc}): {msg}")

@@ -9,6 +9,8 @@
 
 #include <algorithm>
 
+#include <vector>
+
 #include "common.h"
 
 namespace {
@@ -323,6 +325,48 @@ __global__ void __launch_bounds__(256) rerope_kernel(RopeParams p) {
   store_vec<T, VEC>((T*)p.dst + (int64_t)b * p.d_sb + t * p.d_st + (int64_t)h * p.d_sh + d0, f);
 }
 
+// =============================================================================================
+// Gather + rotate: key pages read straight from pinned host memory (through the device mapping)
+// into the cache, the temporal band rotated on the way; one factor row per page. One thread per
+// VEC-channel run of one (b, token, head); up to GR_MAX pages per launch.
+// =============================================================================================
+constexpr int GR_MAX = 32;
+struct GRPage {
+  const void* src; int64_t s_sb, s_st, s_sh;
+  int tokens, dst_token;
+  int64_t start;  // first thread id of the page
+};
+struct GatherRotParams {
+  GRPage pg[GR_MAX];
+  int n;
+  void* dst; int64_t d_sb, d_st, d_sh;
+  int B, H, D, runs;
+  const float2* factors; int nt;
+  int64_t total;
+};
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256) gather_rotate_kernel(GatherRotParams p) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= p.total) return;
+  int j = 0;
+  while (j + 1 < p.n && gid >= p.pg[j + 1].start) ++j;
+  const GRPage& g = p.pg[j];
+  int64_t r = gid - g.start;
+  const int run = (int)(r % p.runs);
+  r /= p.runs;
+  const int h = (int)(r % p.H);
+  r /= p.H;
+  const int tl = (int)(r % g.tokens);
+  const int b = (int)(r / g.tokens);
+  const int d0 = run * VEC;
+  float f[VEC];
+  load_vec<T, VEC>((const T*)g.src + (int64_t)b * g.s_sb + (int64_t)tl * g.s_st + (int64_t)h * g.s_sh + d0, f);
+  if (p.factors && d0 < 2 * p.nt) rotate_band<T, VEC>(f, d0, p.factors + (int64_t)j * p.nt, p.nt);
+  store_vec<T, VEC>((T*)p.dst + (int64_t)b * p.d_sb + (int64_t)(g.dst_token + tl) * p.d_st + (int64_t)h * p.d_sh + d0,
+                    f);
+}
+
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)0x7fffffff; }
 
 int hkv_copies(const wa_hkv_copy* c, int64_t n, hipMemcpyKind kind, void* stream, void* done, const char* what) {
@@ -456,6 +500,72 @@ extern "C" int wa_rerope(const wa_rerope_args* a, void* stream) {
     else rerope_kernel<float, 2><<<(unsigned)blocks, 256, 0, s>>>(p);
   }
   return wa_launch_status("rerope_kernel");
+}
+
+extern "C" int wa_hkv_gather_rotate(const wa_hkv_gather_rotate_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->dst && (a->n_pages == 0 || a->pages), "wa_hkv_gather_rotate: null argument");
+  WA_CHECK_ARG(a->dtype == WA_BF16 || a->dtype == WA_F32, "wa_hkv_gather_rotate: dtype must be bf16 or fp32");
+  WA_CHECK_ARG(a->B >= 1 && a->H >= 1 && a->D >= 2 && a->D % 2 == 0 && a->cap >= 1 && a->n_pages >= 0,
+               "wa_hkv_gather_rotate: bad shape");
+  WA_CHECK_ARG(!a->factors || (a->n_temporal >= 1 && 2 * a->n_temporal <= a->D),
+               "wa_hkv_gather_rotate: bad factor table (n_temporal=%lld)", (long long)a->n_temporal);
+  WA_CHECK_ARG(fits_int(a->B * a->cap) && fits_int(a->H) && fits_int(a->D), "wa_hkv_gather_rotate: sizes exceed int32");
+  const bool vec_dst = a->D % 8 == 0 && a->d_sb % 8 == 0 && a->d_st % 8 == 0 && a->d_sh % 8 == 0 && wa_aligned16(a->dst);
+  bool vec8 = vec_dst;
+  // every page: pinned host memory with a device mapping, inside the cache
+  std::vector<const void*> dev_src((size_t)a->n_pages);
+  for (int64_t i = 0; i < a->n_pages; ++i) {
+    const wa_hkv_page& g = a->pages[i];
+    WA_CHECK_ARG(g.src && g.tokens >= 0 && g.dst_token >= 0 && g.dst_token + g.tokens <= a->cap,
+                 "wa_hkv_gather_rotate: page %lld: tokens [%lld, %lld) outside a cache of %lld", (long long)i,
+                 (long long)g.dst_token, (long long)(g.dst_token + g.tokens), (long long)a->cap);
+    hipPointerAttribute_t attr;
+    const hipError_t e = hipPointerGetAttributes(&attr, g.src);
+    if (e != hipSuccess) (void)hipGetLastError();
+    WA_CHECK_ARG(e == hipSuccess && attr.type == hipMemoryTypeHost && attr.devicePointer != nullptr,
+                 "wa_hkv_gather_rotate: page %lld is not pinned host memory with a device mapping", (long long)i);
+    dev_src[(size_t)i] = attr.devicePointer;
+    vec8 = vec8 && g.s_sb % 8 == 0 && g.s_st % 8 == 0 && g.s_sh % 8 == 0 && wa_aligned16(attr.devicePointer);
+  }
+  const int vec = vec8 ? 8 : 2;
+  const int64_t runs = a->D / vec;
+  hipStream_t s = (hipStream_t)stream;
+  for (int64_t p0 = 0; p0 < a->n_pages; p0 += GR_MAX) {
+    GatherRotParams p{};
+    p.n = 0;
+    int64_t total = 0;
+    for (int64_t i = p0; i < std::min<int64_t>(a->n_pages, p0 + GR_MAX); ++i) {
+      const wa_hkv_page& g = a->pages[i];
+      if (g.tokens == 0) continue;
+      p.pg[p.n] = GRPage{dev_src[(size_t)i], g.s_sb, g.s_st, g.s_sh, (int)g.tokens, (int)g.dst_token, total};
+      total += a->B * g.tokens * a->H * runs;
+      ++p.n;
+    }
+    if (p.n == 0) continue;
+    p.dst = a->dst; p.d_sb = a->d_sb; p.d_st = a->d_st; p.d_sh = a->d_sh;
+    p.B = (int)a->B; p.H = (int)a->H; p.D = (int)a->D; p.runs = (int)runs;
+    p.factors = (const float2*)a->factors;
+    p.nt = (int)a->n_temporal;
+    p.total = total;
+    // factor row j of the launch is the caller's row p0 + j, so no page may be skipped then
+    if (a->factors) {
+      WA_CHECK_ARG(p.n == std::min<int64_t>(a->n_pages, p0 + GR_MAX) - p0,
+                   "wa_hkv_gather_rotate: empty pages are not allowed with a factor table");
+      p.factors = (const float2*)a->factors + p0 * a->n_temporal;
+    }
+    const int64_t blocks = (total + 255) / 256;
+    WA_CHECK_ARG(blocks <= 0x7fffffff, "wa_hkv_gather_rotate: grid too large");
+    if (a->dtype == WA_BF16) {
+      if (vec8) gather_rotate_kernel<bf16_t, 8><<<(unsigned)blocks, 256, 0, s>>>(p);
+      else gather_rotate_kernel<bf16_t, 2><<<(unsigned)blocks, 256, 0, s>>>(p);
+    } else {
+      if (vec8) gather_rotate_kernel<float, 8><<<(unsigned)blocks, 256, 0, s>>>(p);
+      else gather_rotate_kernel<float, 2><<<(unsigned)blocks, 256, 0, s>>>(p);
+    }
+    const int rc = wa_launch_status("gather_rotate_kernel");
+    if (rc != WA_OK) return rc;
+  }
+  return WA_OK;
 }
 
 extern "C" int wa_hkv_gather_async(const wa_hkv_copy* copies, int64_t n, void* stream, void* done) {

@@ -138,6 +138,38 @@ def rotate_temporal(src: torch.Tensor, factors: torch.Tensor, *, dst: Optional[t
     return dst
 
 
+def gather_rotate(pages, dst: torch.Tensor, factors: Optional[torch.Tensor] = None, *, stream=None) -> None:
+    """Install pinned host pages into ``dst`` ``[B, cap, H, D]`` (device) with one kernel launch per
+    32 pages (``wa_hkv_gather_rotate``): ``pages`` is a list of ``(src, dst_token)`` with ``src`` a
+    pinned ``[B, tokens, H, D]`` view; page i's temporal band is multiplied by ``factors[i]``
+    (``[n_pages, n_temporal, 2]`` fp32, device) on the way, or copied as is when ``factors`` is None."""
+    dev = _lib.require_gpu(dst, factors)
+    d4 = _as_blhd(dst)
+    bsz, cap, heads, hd = d4.shape
+    arr = (_lib.HkvPage * max(len(pages), 1))()
+    for i, (src, dst_token) in enumerate(pages):
+        if src.is_cuda or not src.is_pinned():
+            raise ValueError("gather_rotate reads pinned host pages")
+        if src.dtype != dst.dtype:
+            raise ValueError(f"page dtype {src.dtype} differs from the cache's {dst.dtype}")
+        s4 = _as_blhd(src)
+        if s4.shape[0] != bsz or tuple(s4.shape[2:]) != (heads, hd):
+            raise ValueError(f"page {tuple(src.shape)} does not fit a [B={bsz}, *, H={heads}, D={hd}] cache")
+        p, sb, st, sh = _lib.blhd(s4)
+        arr[i] = _lib.HkvPage(p, sb, st, sh, s4.shape[1], int(dst_token))
+    nt = 0
+    if factors is not None:
+        factors = factors.to(torch.float32).contiguous()
+        if factors.shape[0] != len(pages):
+            raise ValueError("one factor row per page")
+        nt = factors.shape[1]
+    pd, db, dt, dh = _lib.blhd(d4)
+    args = _lib.HkvGatherRotateArgs(ctypes.cast(arr, ctypes.c_void_p), len(pages), pd, db, dt, dh,
+                                    _lib.dtype_code(dst), bsz, cap, heads, hd, _lib.ptr(factors), nt)
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    _lib.call("wa_hkv_gather_rotate", ctypes.byref(args), s.cuda_stream)
+
+
 class PageCopy:
     """One 2-D copy: ``rows`` rows of ``width`` bytes (pitches in bytes)."""
 

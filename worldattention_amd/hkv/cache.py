@@ -10,10 +10,11 @@ optional ``k_coarse`` / ``v_coarse``). What moves to the GPU path:
   keys; every layer's valid tokens copied into pinned host blobs on a side stream
   (``wa_hkv_store_async``) instead of synchronous pageable ``.to("cpu")``.
 * ``retrieve``: stage-1 and stage-2 scoring + top-k in ``wa_hkv_score_topk``.
-* ``apply``: per layer, the selected pages are gathered from the pinned tier into the online cache
-  on the side stream (``wa_hkv_gather_async``, adjacent pages of a chunk merged into one copy),
-  re-rotated in place (``wa_rerope``, one factor per page from the reference's move plan), the
-  compressed tier rebuilt (``wa_compress_kv``) and a per-layer event recorded; the caller's stream
+* ``apply``: per layer, on the side stream, the selected key pages are read from the pinned tier
+  by one kernel that writes them into the online cache already re-rotated
+  (``wa_hkv_gather_rotate``, one factor per page from the reference's move plan), the value pages
+  are DMA copies (``wa_hkv_gather_async``, adjacent pages of a chunk merged into one copy), the
+  compressed tier is rebuilt (``wa_compress_kv``) and a per-layer event recorded; the caller's stream
   waits for the last one (or, with ``wait=False``, per layer through :meth:`wait_layer`, so layer
   l's attention overlaps the gather of the layers after it).
 """
@@ -24,7 +25,7 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from .. import _lib
-from ._ops import PageCopy, copy_pages, factor_table, rotate_temporal
+from ._ops import PageCopy, copy_pages, factor_table, gather_rotate, rotate_temporal
 from .retrieval import page_key_index, prompt_index, select_pages, select_top_chunks
 from .rope import temporal_complex_dims
 from .tiering import HKVTierManager
@@ -69,6 +70,8 @@ class HKVCache:
         self.topk_pages = int(topk_pages)
         self.stage1_topk_chunks = int(stage1_topk_chunks)
         self.rerope = bool(rerope)
+        # keys installed by the gather + re-rope kernel (False: DMA copies, then the rotation pass)
+        self.fused_install = True
         self._tier_kwargs = dict(cpu_max_chunks=cpu_max_chunks, nvme_enabled=nvme_enabled, nvme_dir=nvme_dir)
         self._side_stream: Optional[torch.cuda.Stream] = None
         self._inflight: list = []   # (event, objects) kept alive until the event completes
@@ -181,6 +184,7 @@ class HKVCache:
     # -- apply ---------------------------------------------------------------------------------
     def _resolve_pages(self, selected_pairs, side):
         entries, blobs = [], {}
+        self.tier.prefetch(sorted({cid for cid, _ in selected_pairs}))  # spilled chunks read in parallel
         for chunk_id, page_id in selected_pairs:
             if not 0 <= chunk_id < len(self.chunks):
                 continue
@@ -262,8 +266,8 @@ class HKVCache:
                     block["k_coarse"].zero_()
                     block["v_coarse"].zero_()
                 if total > 0:
-                    self._gather_layer(block_idx, installed, blobs, kc, vc, total, keep)
-                    if factors is not None:
+                    fused = self._gather_layer(block_idx, installed, blobs, kc, vc, total, keep, factors)
+                    if factors is not None and not fused:
                         rotate_temporal(kc, factors, rows=rows, t0=0, t1=total)
                     if has_coarse:
                         self._write_coarse(block, hsa_modules[block_idx], kc[:, :total], vc[:, :total])
@@ -277,11 +281,21 @@ class HKVCache:
             main.wait_event(self.layer_events[-1])
         return total
 
-    def _gather_layer(self, block_idx, installed, blobs, kc, vc, total, keep) -> None:
-        """Pinned-tier pages of one layer -> cache tokens [0, total) (K copies, then V copies, so
-        neighbouring pages of a chunk coalesce)."""
+    def _gather_layer(self, block_idx, installed, blobs, kc, vc, total, keep, factors=None) -> bool:
+        """Pinned-tier pages of one layer -> cache tokens [0, total). Keys of the cache's dtype are
+        read by one kernel that also applies each page's re-rope factors (returns True); otherwise
+        they are DMA copies like the values (neighbouring pages of a chunk coalesce) and the caller
+        rotates afterwards."""
+        k_srcs = [blobs[cid]["k"][block_idx] for cid, _, _ in installed]
+        fused = self.fused_install and all(src.dtype == kc.dtype for src in k_srcs)
+        if fused:
+            pages, off = [], 0
+            for (cid, s, e), src in zip(installed, k_srcs):
+                pages.append((src[:, s:e], off))
+                off += e - s
+            gather_rotate(pages, kc, factors, stream=torch.cuda.current_stream(kc.device))
         plans = []
-        for name, dst in (("k", kc), ("v", vc)):
+        for name, dst in ((("v", vc),) if fused else (("k", kc), ("v", vc))):
             srcs = [blobs[cid][name][block_idx] for cid, _, _ in installed]
             direct = all(s.dtype == dst.dtype for s in srcs) and _slab(dst[:, :total]) is not None
             stage = dst[:, :total] if direct else torch.empty((dst.shape[0], total) + tuple(srcs[0].shape[2:]),
@@ -293,11 +307,13 @@ class HKVCache:
                 copies.append(_copy(src[:, s:e], stage[:, off:off + e - s]))
                 off += e - s
             plans.append((copies, stage, dst, direct))
-        copy_pages(plans[0][0] + plans[1][0], to_device=True, stream=torch.cuda.current_stream(kc.device))
+        copy_pages([c for plan in plans for c in plan[0]], to_device=True,
+                   stream=torch.cuda.current_stream(kc.device))
         for _, stage, dst, direct in plans:
             if not direct:
                 dst[:, :total].copy_(stage)
                 keep.append(stage)
+        return fused
 
     @staticmethod
     def _write_coarse(block: dict, hsa, loaded_k: torch.Tensor, loaded_v: torch.Tensor) -> None:

@@ -5,31 +5,78 @@ tests depend on it: ``put`` / ``get`` / ``location`` / ``stats`` / ``cleanup``; 
 host chunks leave first; with NVMe a spilled chunk keeps its file as a backup, so spilling it again
 writes nothing; without NVMe it is dropped. Additions for the GPU path: a blob may carry the event
 of the device->host copy that fills it (``put(..., ready=event)``); host readers and spills wait
-for it. Spill files are written by ``torch.save`` and read with ``torch.load(weights_only=True)``
-(dicts / lists of tensors), then re-pinned when a GPU is present so page gathers stay asynchronous.
+for it.
+
+The NVMe tier replaces the reference's synchronous ``torch.save`` / ``torch.load`` with
+asynchronous direct I/O (``wa_io_*``): a spill starts writing the blob's tensors (raw bytes, one
+4 KiB-aligned region each, O_DIRECT where the file system takes it) on a worker thread and returns;
+the blob is released when the write completes. A reload reads into freshly allocated (pinned, when
+a GPU is present) tensors of the recorded shapes; :meth:`HKVTierManager.prefetch` starts reloads
+ahead of their ``get``. A chunk requested while its spill is still being written is served from
+memory.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 from collections import OrderedDict
-from typing import Dict, Optional
+from typing import Dict, Iterable, List, Optional
 
 import torch
+
+from .. import _lib
 
 __all__ = ["HKVTierManager"]
 
 _HOST, _DISK = "cpu", "nvme"
 
 
-def _pinned(obj):
-    """``obj`` with every tensor in page-locked host memory."""
+def _leaves(obj, out: List[torch.Tensor]) -> List[torch.Tensor]:
+    """The tensors of a blob (dicts in key order, lists in order)."""
     if isinstance(obj, torch.Tensor):
-        return obj if obj.is_pinned() else obj.pin_memory()
+        out.append(obj)
+    elif isinstance(obj, dict):
+        for key in sorted(obj):
+            _leaves(obj[key], out)
+    elif isinstance(obj, (list, tuple)):
+        for val in obj:
+            _leaves(val, out)
+    return out
+
+
+def _spec(obj):
+    """The blob's structure with each tensor replaced by its (shape, dtype)."""
+    if isinstance(obj, torch.Tensor):
+        return ("t", tuple(obj.shape), obj.dtype)
     if isinstance(obj, dict):
-        return {key: _pinned(val) for key, val in obj.items()}
+        return ("d", {key: _spec(val) for key, val in obj.items()})
     if isinstance(obj, (list, tuple)):
-        return type(obj)(_pinned(val) for val in obj)
-    return obj
+        return ("l", type(obj), [_spec(val) for val in obj])
+    return ("o", obj)
+
+
+def _build(spec, pin: bool):
+    """Empty tensors (pinned when ``pin``) in the structure of ``spec``."""
+    kind = spec[0]
+    if kind == "t":
+        return torch.empty(spec[1], dtype=spec[2], pin_memory=pin)
+    if kind == "d":
+        return {key: _build(val, pin) for key, val in spec[1].items()}
+    if kind == "l":
+        return spec[1](_build(val, pin) for val in spec[2])
+    return spec[1]
+
+
+def _start_io(write: bool, path: str, tensors: List[torch.Tensor], direct: bool) -> int:
+    n = len(tensors)
+    bufs = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in tensors])
+    sizes = (ctypes.c_int64 * max(n, 1))(*[t.numel() * t.element_size() for t in tensors])
+    fn = "wa_io_write_async" if write else "wa_io_read_async"
+    handle = getattr(_lib.lib(), fn)(os.fsencode(path), bufs, sizes, n, int(direct))
+    if handle <= 0:
+        msg = _lib.lib().wa_last_error().decode(errors="replace")
+        raise (OSError if handle == _lib.WA_ERR_IO else ValueError)(f"{fn}: {msg}")
+    return handle
 
 
 class HKVTierManager:
@@ -54,6 +101,10 @@ class HKVTierManager:
         self._blobs: Dict[int, dict] = {}            # host-resident blobs
         self._files: Dict[int, str] = {}             # spill file (backup) per chunk ever spilled
         self._pending: Dict[int, object] = {}        # fill event per host blob
+        self._specs: Dict[int, tuple] = {}           # structure of each spilled blob
+        self._writes: Dict[int, tuple] = {}          # spill in flight: (handle, blob, tensors)
+        self._reads: Dict[int, tuple] = {}           # reload in flight: (handle, blob)
+        self.direct_io = True
         self.n_spills = self.n_loads = self.n_drops = 0
 
     # -- residency -------------------------------------------------------------------------
@@ -80,11 +131,40 @@ class HKVTierManager:
                 self.n_drops += 1
                 continue
             if victim not in self._files:
-                path = os.path.join(self.nvme_dir, f"hkv_chunk_{victim}.pt")
-                torch.save(blob, path)
+                path = os.path.join(self.nvme_dir, f"hkv_chunk_{victim}.bin")
+                tensors = [t if t.is_contiguous() else t.contiguous() for t in _leaves(blob, [])]
+                self._specs[victim] = _spec(blob)
+                self._writes[victim] = (_start_io(True, path, tensors, self.direct_io), blob, tensors)
                 self._files[victim] = path
             self._where[victim] = _DISK
             self.n_spills += 1
+        self._reap()
+
+    def _reap(self) -> None:
+        """Finish the spills whose writes have completed (releasing their blobs)."""
+        for cid in [c for c, (h, _, _) in self._writes.items() if _lib.lib().wa_io_done(h) == 1]:
+            handle, _, _ = self._writes.pop(cid)
+            _lib.call("wa_io_wait", handle)
+
+    def _read(self, chunk_id: int) -> dict:
+        """Reload a spilled chunk: the blob still in memory if its spill is being written, else the
+        prefetched or a fresh read of its file."""
+        if chunk_id in self._writes:
+            return self._writes[chunk_id][1]
+        if chunk_id in self._reads:
+            handle, blob = self._reads.pop(chunk_id)
+        else:
+            blob = _build(self._specs[chunk_id], torch.cuda.is_available())
+            handle = _start_io(False, self._files[chunk_id], _leaves(blob, []), self.direct_io)
+        _lib.call("wa_io_wait", handle)
+        return blob
+
+    def prefetch(self, chunk_ids: Iterable[int]) -> None:
+        """Start reading spilled chunks back so later ``get`` calls only wait for them."""
+        for cid in chunk_ids:
+            if self._where.get(cid) == _DISK and cid not in self._reads and cid not in self._writes:
+                blob = _build(self._specs[cid], torch.cuda.is_available())
+                self._reads[cid] = (_start_io(False, self._files[cid], _leaves(blob, []), self.direct_io), blob)
 
     # -- API -------------------------------------------------------------------------------
     def put(self, chunk_id: int, blob: dict, ready=None) -> None:
@@ -106,9 +186,7 @@ class HKVTierManager:
         if tier is None:
             return None
         if tier == _DISK:
-            blob = torch.load(self._files[chunk_id], map_location="cpu", weights_only=True)
-            if torch.cuda.is_available():
-                blob = _pinned(blob)
+            blob = self._read(chunk_id)
             self.n_loads += 1
             self._blobs[chunk_id] = blob
             self._where[chunk_id] = _HOST
@@ -137,6 +215,15 @@ class HKVTierManager:
         """Delete spill files and forget every chunk."""
         for cid in list(self._pending):
             self._wait_filled(cid)
+        errors = []
+        for table in (self._writes, self._reads):
+            for handle, *_ in table.values():
+                try:
+                    _lib.call("wa_io_wait", handle)
+                except OSError as exc:  # the files go anyway
+                    errors.append(exc)
+            table.clear()
+        self._specs.clear()
         for path in set(self._files.values()):
             try:
                 os.remove(path)
@@ -146,3 +233,5 @@ class HKVTierManager:
         self._recency.clear()
         self._blobs.clear()
         self._files.clear()
+        if errors:
+            raise errors[0]
