@@ -390,6 +390,24 @@ def test_apply_installs_pages_verbatim_and_sets_end_indices():
         assert int(blk["local_end_index"]) == PAGE_TOKENS and int(blk["global_end_index"]) == 30 * FRAME_TOKENS
 
 
+def test_apply_refreshes_kept_key_block_sums():
+    """A cache that keeps key block sums for routing gets them recomputed for the installed pages."""
+    from worldattention_amd.hsa.kvcache import kv_append
+    mods = hsa_modules()
+    bk = seed_chunks(bank(topk_pages=1), mods)
+    c = make_cache(mods)
+    torch.manual_seed(4)
+    for blk in c:
+        x = torch.randn(1, CAPACITY, HEADS, HEAD_DIM, device=DEV)
+        kv_append(blk, x, x, write_start=0, block_size=4)
+    n = bk.apply(c, [(1, 1)], current_start_frame=30, temporal_freqs=FREQS, hsa_modules=mods)
+    for blk in c:
+        k = blk["k"][0, :n, 0].cpu().double()
+        want = k.reshape(n // 4, 4, HEAD_DIM).sum(1)
+        got = blk["k_block_sums"][0, 0, : n // 4].cpu().double()
+        assert torch.allclose(got, want, rtol=1e-6, atol=1e-4)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_apply_reropes_keys_like_the_oracle(dtype):
     mods = hsa_modules()

@@ -25,6 +25,7 @@ from typing import List, Optional, Sequence, Tuple
 import torch
 
 from .. import _lib
+from ..hsa.kvcache import refresh_block_sums
 from ._ops import PageCopy, copy_pages, factor_table, gather_rotate, rotate_temporal
 from .retrieval import page_key_index, prompt_index, select_pages, select_top_chunks
 from .rope import temporal_complex_dims
@@ -271,6 +272,7 @@ class HKVCache:
                         rotate_temporal(kc, factors, rows=rows, t0=0, t1=total)
                     if has_coarse:
                         self._write_coarse(block, hsa_modules[block_idx], kc[:, :total], vc[:, :total])
+                    refresh_block_sums(block, total)  # key block sums kept for routing, if any
                 block["global_end_index"].fill_(current_start_frame * self.frame_seq_length)
                 block["local_end_index"].fill_(total)
                 ev = torch.cuda.Event()

@@ -27,13 +27,30 @@ import torch
 from .. import _lib
 from .attention import _compress
 
-__all__ = ["kv_append", "new_block_sums", "qkv_epilogue", "kv_roll", "cache_step"]
+__all__ = ["kv_append", "new_block_sums", "refresh_block_sums", "qkv_epilogue", "kv_roll", "cache_step"]
 
 
 def new_block_sums(k_cache: torch.Tensor, block_size: int) -> torch.Tensor:
     """Zeroed fp32 key block sums ``[B, H, ceil(cap / block_size), D]`` for a ``[B, cap, H, D]`` cache."""
     bsz, cap, heads, d = k_cache.shape
     return torch.zeros((bsz, heads, math.ceil(cap / block_size), d), dtype=torch.float32, device=k_cache.device)
+
+
+def refresh_block_sums(kv_cache: dict, length: int) -> None:
+    """Recompute ``kv_cache["k_block_sums"]`` (if kept) for the first ``length`` cache tokens, e.g.
+    after something other than these functions rewrote the keys (an HKV page install)."""
+    sums = kv_cache.get("k_block_sums")
+    if sums is None or length <= 0:
+        return
+    bs = int(kv_cache["k_block_sums_block_size"])
+    kc = kv_cache["k"]
+    dev = _lib.require_gpu(kc, sums)
+    bsz, cap, heads_n, d = kc.shape
+    p, sb, st, sh = _lib.blhd(kc)
+    nblk = -(-int(length) // bs)
+    args = _lib.PoolArgs(p, sb, st, sh, _lib.dtype_code(kc), bsz, int(length), heads_n, d, bs, nblk, None, 0,
+                         sums.data_ptr(), 1, 0, sums.shape[2], 1)
+    _lib.call("wa_block_mean_pool", args, _lib.stream_ptr(dev))
 
 
 def kv_append(kv_cache: dict, k_new: torch.Tensor, v_new: torch.Tensor, *, write_start: int,
@@ -78,6 +95,7 @@ def kv_append(kv_cache: dict, k_new: torch.Tensor, v_new: torch.Tensor, *, write
     if sums is None and block_size is not None:
         sums = new_block_sums(kc, block_size)
         kv_cache["k_block_sums"] = sums
+        kv_cache["k_block_sums_block_size"] = int(block_size)
     bs = 0
     if sums is not None:
         if block_size is None:
@@ -171,6 +189,7 @@ def qkv_epilogue(q, k, v, kv_cache: dict, *, grid_sizes, freqs, start_frame: int
         if sums is None:
             sums = new_block_sums(kc, block_size)
             kv_cache["k_block_sums"] = sums
+            kv_cache["k_block_sums_block_size"] = int(block_size)
     wq = wk = None
     w_dtype = 0
     if norm_q is not None:
