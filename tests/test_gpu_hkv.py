@@ -116,6 +116,27 @@ def test_score_topk_matches_oracle(pages, dim, k):
     assert sel.cpu().tolist() == O.stable_topk(O.score_pages(q, index), k)   # tie-free data
 
 
+def test_selection_beyond_one_launch_matches_the_oracle():
+    """More rows than one selection launch takes: runs of 4096 rows merged, ties across runs to
+    the lowest row, masked rows skipped, the full score vector returned."""
+    torch.manual_seed(9)
+    n, dim, k = 9000, 64, 12
+    index = torch.randn(n, dim)
+    index[8100] = index[100]          # exact ties in different runs
+    index[5000] = index[100]
+    q = torch.randn(dim)
+    mask = torch.zeros(n, dtype=torch.uint8)
+    mask[7:40] = 1
+    sel, vals, scores = _ops.score_topk(index.to(DEV), q.to(DEV), k, scale=8.0, mask=mask.to(DEV), want_scores=True)
+    want_scores = O.score_pages(q, index, scale=8.0)
+    close(scores, want_scores, what="scores")
+    masked = scores.cpu().clone()
+    masked[mask.bool()] = -float("inf")
+    order = torch.sort(masked, descending=True, stable=True).indices[:k]
+    assert sel.cpu().tolist() == order.tolist()
+    close(vals, masked[order], what="selected scores")
+
+
 def test_selection_ties_mask_and_empty_slots():
     torch.manual_seed(0)
     base = torch.randn(6, 64)

@@ -69,19 +69,45 @@ def segment_means(x: torch.Tensor, *, heads: int, head_dim: int, seg_tokens: Opt
     return out
 
 
+def _score_topk_chunked(index, query, k, *, scale, mask, want_scores):
+    """:func:`score_topk` over more rows than one selection launch takes: each run of
+    ``HKV_MAX_PAGES`` rows selects its own top-k, then the candidates (in row order, each run's
+    best first) are ordered by a stable descending sort of their scores, which keeps the lowest
+    row first among equal scores."""
+    n_pages = index.shape[0]
+    dev = index.device
+    sels, vals, parts = [], [], []
+    for r0 in range(0, n_pages, _lib.HKV_MAX_PAGES):
+        r1 = min(n_pages, r0 + _lib.HKV_MAX_PAGES)
+        kk = min(k, r1 - r0)
+        sel, val, sc = score_topk(index[r0:r1], query, kk, scale=scale,
+                                  mask=None if mask is None else mask[r0:r1], want_scores=want_scores)
+        sels.append(torch.where(sel >= 0, sel + r0, sel))
+        vals.append(val)
+        if want_scores:
+            parts.append(sc)
+    cand, cval = torch.cat(sels), torch.cat(vals)
+    order = torch.sort(cval, descending=True, stable=True).indices[:k]
+    sel, sel_scores = cand[order].to(torch.int32).contiguous(), cval[order].contiguous()
+    return sel, sel_scores, torch.cat(parts) if want_scores else None
+
+
 def score_topk(index: torch.Tensor, query: torch.Tensor, k: int, *, scale: float = 0.0,
                mask: Optional[torch.Tensor] = None, want_scores: bool = False):
     """Device ``(sel int32 [k], sel_scores fp32 [k], scores fp32 [P] or None)``: the ``k`` highest
     of ``index @ query / scale`` (no division for ``scale <= 0``), lowest page index first among
-    equal scores; masked pages are skipped and empty slots hold -1 / -inf."""
+    equal scores; masked pages are skipped and empty slots hold -1 / -inf. More rows than one
+    selection launch takes (``HKV_MAX_PAGES``) are selected in runs and merged."""
     dev = _lib.require_gpu(index, query, mask)
     if index.dim() != 2:
         raise ValueError(f"page index must be [P, dim], got {tuple(index.shape)}")
     n_pages, dim = index.shape
-    if not 1 <= n_pages <= _lib.HKV_MAX_PAGES:
-        raise ValueError(f"{n_pages} pages; the selection kernel handles 1..{_lib.HKV_MAX_PAGES}")
+    if n_pages < 1:
+        raise ValueError("no pages to select from")
     if not 1 <= k <= n_pages:
         raise ValueError(f"k={k} outside [1, {n_pages}]")
+    if n_pages > _lib.HKV_MAX_PAGES:
+        return _score_topk_chunked(index, query, k, scale=scale, mask=mask, want_scores=want_scores)
     index = index.to(torch.float32)
     if index.stride(-1) != 1:
         index = index.contiguous()
