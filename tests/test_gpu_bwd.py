@@ -192,14 +192,17 @@ def test_cfg5_wan_chunk_fwd_bwd_matches_oracle(keep_dtype):
         assert_close(gg, r, what=f"cfg5 {name}")
 
 
-def test_bf16_dk_dv_are_the_fp32_gradients_rounded():
+@pytest.mark.parametrize("d", [64, 128])
+def test_bf16_dk_dv_are_the_fp32_gradients_rounded(d):
     """dkv_dtype = WA_BF16: the sparse and elu1 backward kernels write dK / dV once in bf16; the
-    values are the fp32 path's, rounded to nearest even (bit-exact)."""
+    values are the fp32 path's, rounded to nearest even (bit-exact). At D = 64 this also pins the
+    bf16 elu1 key side against the fp32 kernel on every token (the elu1 gradients are ~1e-3, below
+    what the oracle tolerances resolve)."""
     from worldattention_amd.hsa._autograd import elu1_backward
     from worldattention_amd.hsa._bwd import bsa_backward
     from worldattention_amd.hsa.block_sparse import bsa_forward
     torch.manual_seed(21)
-    b, h, d, bs, nq, nkv = 1, 2, 128, 128, 3, 9
+    b, h, bs, nq, nkv = 1, 2, 128, 3, 9
     lkv = nkv * bs - 40
     q = torch.randn(b, nq * bs, h, d, device=DEV).bfloat16()
     k = torch.randn(b, lkv, h, d, device=DEV).bfloat16()

@@ -520,8 +520,7 @@ struct Elu1BwdParams {
   void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
-  int kv_tiles_per_wg;  // 128-token tiles per workgroup of the bf16 key-side kernel
-  int64_t k_slab, v_slab;  // bytes of one (batch, head) K / V slab, first row to last row's end
+  int kv_groups_per_wg;  // 32-token groups per workgroup of the bf16 key-side kernel
   const int32_t* heads; int n_heads, H, B, Lq, Lkv, n_qt;
   float* part;    // [n_qt][B][n_heads][D*D + D]
   float* dstate;  // [B][n_heads][D*D]
@@ -548,19 +547,19 @@ __device__ __forceinline__ void load8_any(const void* base, int64_t i, int dtype
 }
 
 // Stages an fp32 [D][D] matrix as bf16 hi + lo dual-swizzled tiles (rows = first index).
-template <int D>
+template <int D, int NT = 256>
 __device__ __forceinline__ void stage_hilo(const float* S, bf16_t* hi_t, bf16_t* lo_t, int tid) {
-  constexpr int CPR = D / 8, SU = D * CPR / 256;
+  constexpr int CPR = D / 8, SU = D * CPR / NT;
   f32x4 x0[SU], x1[SU];
 #pragma unroll
   for (int k = 0; k < SU; ++k) {
-    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    const int u = tid + NT * k, d = u / CPR, cc = u % CPR;
     x0[k] = *(const f32x4*)(S + d * D + cc * 8);
     x1[k] = *(const f32x4*)(S + d * D + cc * 8 + 4);
   }
 #pragma unroll
   for (int k = 0; k < SU; ++k) {
-    const int u = tid + 256 * k, d = u / CPR, cc = u % CPR;
+    const int u = tid + NT * k, d = u / CPR, cc = u % CPR;
     bf16x8 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -574,25 +573,28 @@ __device__ __forceinline__ void stage_hilo(const float* S, bf16_t* hi_t, bf16_t*
   }
 }
 
-// Query side: one workgroup per (128-query tile, head slot, batch), wave w = queries 32w..
+// Query side: one workgroup of 8 waves per (128-query tile, head slot, batch), two waves per
+// SIMD. Wave w owns queries 32 (w & 3).. and the channel half w >> 2 of each product's output; both
+// halves form phi(q) and the denominator of their queries (the contraction runs over all channels).
 template <int D>
-__global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
-  constexpr int DC = D / 16, DT = D / 32;
+__global__ void __launch_bounds__(512) elu1_bwd_q_kernel(Elu1BwdParams p) {
+  constexpr int DC = D / 16, DT = D / 32, TTW = DT / 2;
   __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t t_dn[128 * D];
   __shared__ __attribute__((aligned(1024))) bf16_t t_ph[128 * D];
-  __shared__ float s_z[D], s_dd[128];
+  __shared__ float s_z[D], s_dd[128], s_go[2][128], s_dz[4][D];
   const int tile = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
+  const int half = w >> 2;
   const int64_t bh = (int64_t)b * p.n_heads + hs;
-  stage_hilo<D>(p.state + bh * D * D, s_hi, s_lo, tid);
-  for (int e = tid; e < D; e += 256) s_z[e] = p.zsum[bh * D + e];
+  stage_hilo<D, 512>(p.state + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 512) s_z[e] = p.zsum[bh * D + e];
   __syncthreads();
 
-  const int ql = w * 32 + l32, qi = tile * 128 + ql;
+  const int ql = (w & 3) * 32 + l32, qi = tile * 128 + ql;
   const bool q_ok = qi < p.Lq;
   const int64_t qoff = (int64_t)b * p.q_sb + (int64_t)(q_ok ? qi : 0) * p.q_st + (int64_t)h * p.q_sh;
   const int64_t goff = (int64_t)b * p.g_sb + (int64_t)(q_ok ? qi : 0) * p.g_st + (int64_t)h * p.g_sh;
@@ -608,38 +610,39 @@ __global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
       phf[c][e] = (bf16_t)ph;
       den = fmaf(ph, s_z[c * 16 + g * 8 + e], den);
     }
-    tile_put8<D>(t_ph, ql, 2 * c + g, phf[c]);
+    if (c / (DC / 2) == half) tile_put8<D>(t_ph, ql, 2 * c + g, phf[c]);
   }
   den += __shfl_xor(den, 32, 64);
   const float inv = q_ok && den > 0.f ? 1.f / den : 0.f;
 
-  // n^T = S^T phi(q)^T, then o, dden, dn (accumulator layout: lane q, d = 32t + 8(r/4) + 4g + r%4)
-  f32x16 acc[DT];
+  // n^T = S^T phi(q)^T for this half's output tiles, then o, (g . o), dn (accumulator layout:
+  // lane q, d = 32t + 8(r/4) + 4g + r%4)
+  f32x16 acc[TTW];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    acc[t] = f32x16{};
+  for (int k = 0; k < TTW; ++k) {
+    const int t = half * TTW + k;
+    acc[k] = f32x16{};
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      acc[t] = wa_mfma32(tile_row8<D>(s_hi, 32 * t + l32, 2 * c + g), phf[c], acc[t]);
-      acc[t] = wa_mfma32(tile_row8<D>(s_lo, 32 * t + l32, 2 * c + g), phf[c], acc[t]);
+      acc[k] = wa_mfma32(tile_row8<D>(s_hi, 32 * t + l32, 2 * c + g), phf[c], acc[k]);
+      acc[k] = wa_mfma32(tile_row8<D>(s_lo, 32 * t + l32, 2 * c + g), phf[c], acc[k]);
     }
   }
   float go = 0.f;
-  bf16x8 dnb[DC];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
+  for (int k = 0; k < TTW; ++k) {
+    const int t = half * TTW + k;
+    float gv[4][4];
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) load4_any(p.g, goff + 32 * t + 8 * rq + 4 * g, p.g_dtype, gv[rq]);
 #pragma unroll
     for (int rq = 0; rq < 4; ++rq) {
-      float gv[4];
-      load4_any(p.g, goff + 32 * t + 8 * rq + 4 * g, p.g_dtype, gv);
       bf16x4 dn4;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float gg = q_ok ? gv[i] : 0.f;
-        go = fmaf(gg, acc[t][rq * 4 + i] * inv, go);
-        const float dn = gg * inv;
-        dnb[2 * t + (rq >> 1)][(rq & 1) * 4 + i] = (bf16_t)dn;
-        dn4[i] = (bf16_t)dn;
+        const float gg = q_ok ? gv[rq][i] : 0.f;
+        go = fmaf(gg, acc[k][rq * 4 + i] * inv, go);
+        dn4[i] = (bf16_t)(gg * inv);
       }
       // t_dn[q][d]: 4 consecutive channels of one 16-byte chunk
       const int d0 = 32 * t + 8 * rq + 4 * g;
@@ -647,17 +650,21 @@ __global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
     }
   }
   go += __shfl_xor(go, 32, 64);
-  const float dden = -go * inv;
-  if (g == 0) s_dd[ql] = q_ok ? dden : 0.f;
+  if (g == 0) s_go[half][ql] = go;
+  __syncthreads();  // t_dn, t_ph and both halves of (g . o) complete
+  const float dden = -(s_go[0][ql] + s_go[1][ql]) * inv;
+  if (g == 0 && half == 0) s_dd[ql] = q_ok ? dden : 0.f;
 
-  // dphi(q)^T[e, q] = sum_d S^T[d, e] dn[q, d] (+ dden z[e]); contraction in accumulator order
+  // dphi(q)^T[e, q] = sum_d S^T[d, e] dn[q, d] (+ dden z[e]) for this half's channels e
 #pragma unroll
-  for (int et = 0; et < DT; ++et) {
+  for (int k = 0; k < TTW; ++k) {
+    const int et = half * TTW + k;
     f32x16 da = f32x16{};
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      da = wa_mfma32(tile_tr8<D>(s_hi, c, 32 * et, lane), dnb[c], da);
-      da = wa_mfma32(tile_tr8<D>(s_lo, c, 32 * et, lane), dnb[c], da);
+      const bf16x8 dn8 = tile_row8<D>(t_dn, ql, 2 * c + g);
+      da = wa_mfma32(tile_tr8n<D>(s_hi, c, 32 * et, lane), dn8, da);
+      da = wa_mfma32(tile_tr8n<D>(s_lo, c, 32 * et, lane), dn8, da);
     }
     if (q_ok) {
       // all reads (q and, when accumulating, the previous dq) before any store
@@ -679,15 +686,13 @@ __global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
       }
     }
   }
-  __syncthreads();  // t_dn, t_ph, s_dd complete
+  __syncthreads();  // s_dd complete
 
-  // partial dS^T[d, e] = sum_q dn[q, d] phi(q)[q, e] over this tile (both operands transposed)
+  // partial dS^T[d, e] = sum_q dn[q, d] phi(q)[q, e] over this tile (both operands transposed):
+  // DT x DT output tiles spread over the 8 waves
   float* part = p.part + (((int64_t)tile * p.B + b) * p.n_heads + hs) * (int64_t)(D * D + D);
-  constexpr int TPW = DT * DT / 4;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int dt = D == 128 ? w : (w >> 1);
-    const int et = D == 128 ? i : (w & 1);
+  for (int i = w; i < DT * DT; i += 8) {
+    const int dt = i / DT, et = i % DT;
     f32x16 pa = f32x16{};
 #pragma unroll
     for (int c = 0; c < 8; ++c) pa = wa_mfma32(tile_tr8<D>(t_dn, c, 32 * dt, lane), tile_tr8<D>(t_ph, c, 32 * et, lane), pa);
@@ -697,13 +702,18 @@ __global__ void __launch_bounds__(256) elu1_bwd_q_kernel(Elu1BwdParams p) {
       part[d * D + 32 * et + l32] = pa[r];
     }
   }
-  // dz partial: thread per channel e, fixed query order
-  for (int e = tid; e < D; e += 256) {
+  // dz partial: per channel e four 32-query chains in fixed order, added in order
+  if (tid < 4 * D) {
+    const int e = tid % D, q4 = tid / D;
     float sz = 0.f;
-    for (int qq = 0; qq < 128; ++qq)
+    for (int k = 0; k < 32; ++k) {
+      const int qq = q4 * 32 + k;
       sz = fmaf(s_dd[qq], (float)t_ph[qq * D + (((e >> 3) ^ dual_swizzle<D>(qq)) * 8) + (e & 7)], sz);
-    part[D * D + e] = sz;
+    }
+    s_dz[q4][e] = sz;
   }
+  __syncthreads();
+  if (tid < D) part[D * D + tid] = ((s_dz[0][tid] + s_dz[1][tid]) + s_dz[2][tid]) + s_dz[3][tid];
 }
 
 // Key side: one workgroup per (128-token tile, head slot, batch), wave w = tokens 32w..
@@ -786,118 +796,108 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
 }
 
 // Key side, bf16 K / V in and bf16 dK / dV out (written once): the same products as
-// elu1_bwd_kv_kernel with every global access coalesced. A workgroup stages the state gradient
-// once and then walks a run of 128-token tiles (about one workgroup per CU): each tile's K and V
-// stream into LDS by direct-to-LDS loads, chunk-swizzled by token (chunk ^ (token & 15)), and give
-// the A fragments; per 32-channel column tile the results go through an LDS staging tile, from
-// which each thread forms 8 consecutive channels of a token (the dK factor elu1'(k) read from the
-// K tile) and writes them with one 16-byte store.
+// elu1_bwd_kv_kernel, transposed so that a lane owns a token (accumulator layout: lane = token,
+// registers = channels): dK^T[e, t] = sum_d dS^T[d, e] v[t, d], dV^T[d, t] = sum_e dS^T[d, e]
+// phi(k)[t, e]. A workgroup stages the state gradient once (bf16 hi + lo: 64 KB at D = 128, two
+// workgroups per CU) and its waves then walk 32-token groups of the workgroup's token run on their
+// own, without barriers: K and V rows load straight into MFMA fragments, the next group's loads
+// go out once the last column tile's products have read the fragments (before that tile's stores:
+// on gfx9 loads and stores share one counter, so a load issued after a store waits for it), and
+// each lane writes 4 channels of its token per store. The dK factor elu1'(k) comes from the K
+// fragments: the two lanes of a token exchange the halves of their 16-byte chunks. (Holding the
+// next group's fragments in registers for the whole group needs ~320 registers: one wave per
+// SIMD, slower.)
 template <int D>
 __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
-  constexpr int DC = D / 16, DT = D / 32, CPR = D / 8;
+  constexpr int DC = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(1024))) bf16_t s_hi[D * D];
   __shared__ __attribute__((aligned(1024))) bf16_t s_lo[D * D];
-  __shared__ __attribute__((aligned(1024))) bf16_t s_k[128 * D];
-  __shared__ __attribute__((aligned(1024))) bf16_t s_v[128 * D];
-  // staging of one column tile, [2][128][32] floats: in s_v once the fragments are read (D = 128),
-  // else its own array
-  __shared__ __attribute__((aligned(1024))) float s_stage[D == 128 ? 4 : 2 * 128 * 32];
   __shared__ float s_z[D];
   const int hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int64_t bh = (int64_t)b * p.n_heads + hs;
-  // this workgroup's run of 128-token tiles: the state gradient is staged once for all of them
-  const int n_tiles = (p.Lkv + 127) / 128;
-  const int tile_beg = blockIdx.x * p.kv_tiles_per_wg, tile_end = min(n_tiles, tile_beg + p.kv_tiles_per_wg);
-  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
-  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
-#pragma unroll 1
-  for (int tile = tile_beg; tile < tile_end; ++tile) {
-  const int t0 = tile * 128;
-
-  // K / V tiles: wave instruction q (i-th of wave w) moves RPI rows, 64 lanes x 16 bytes
-  {
-    constexpr int RPI = 64 / CPR, NQ = 128 / RPI;
-    const int64_t ko = ((int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)t0 * p.k_st) * 2;
-    const int64_t vo = ((int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)t0 * p.v_st) * 2;
-    const int64_t kslab0 = ((int64_t)b * p.k_sb + (int64_t)h * p.k_sh) * 2;
-    const int64_t vslab0 = ((int64_t)b * p.v_sb + (int64_t)h * p.v_sh) * 2;
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const char*)p.k + ko), (short)0, (int)(p.k_slab - (ko - kslab0)), WA_BUF_DWORD3);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)((const char*)p.v + vo), (short)0, (int)(p.v_slab - (vo - vslab0)), WA_BUF_DWORD3);
-#pragma unroll
-    for (int i = 0; i < NQ / 4; ++i) {
-      const int q = i * 4 + w, r = q * RPI + lane / CPR, slot = lane % CPR;
-      const int ch = slot ^ (r & 15);
-      lds_dma16(krs, s_k + q * RPI * D, (int)((r * p.k_st + ch * 8) * 2));
-      lds_dma16(vrs, s_v + q * RPI * D, (int)((r * p.v_st + ch * 8) * 2));
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  const int tr = w * 32 + l32;  // this lane's token (A-operand row) within the tile
-  const bool t_ok = t0 + tr < p.Lkv;
-  bf16x8 vf[DC], pk[DC];
-#pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    const int slot = (2 * c + g) ^ (tr & 15);
-    const bf16x8 kk = *(const bf16x8*)(s_k + tr * D + slot * 8);
-    const bf16x8 vv = *(const bf16x8*)(s_v + tr * D + slot * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      pk[c][e] = (bf16_t)(t_ok ? elu1f((float)kk[e]) : 0.f);
-      vf[c][e] = t_ok ? vv[e] : (bf16_t)0.f;
-    }
-  }
-  // staging row r sits at physical row r ^ ((r >> 2) & 1): the two rows a wave writes per
-  // register (r and r + 4) then fall in different halves of the banks
-  float* stk = D == 128 ? (float*)s_v : s_stage;  // dK before the elu1' factor
-  float* stv = stk + 128 * 32;                    // dV
-#pragma unroll 1
-  for (int jt = 0; jt < DT; ++jt) {
-    f32x16 dk = f32x16{}, dv = f32x16{};
+  const int n_groups = (p.Lkv + 31) / 32;
+  const int g_end = min(n_groups, (blockIdx.x + 1) * p.kv_groups_per_wg);
+  const bf16_t* kbase = (const bf16_t*)p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + g * 8;
+  const bf16_t* vbase = (const bf16_t*)p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + g * 8;
+  bf16x8 kf[DC], vf[DC];
+  auto load_group = [&](int gi, bf16x8(&kd)[DC], bf16x8(&vd)[DC]) {
+    const int t = gi * 32 + l32;
+    const int64_t tr = t < p.Lkv ? t : 0;  // rows past the end re-read row 0; nothing is stored for them
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_hi, c, 32 * jt, lane), dk);
-      dk = wa_mfma32(vf[c], tile_tr8n<D>(s_lo, c, 32 * jt, lane), dk);
-      dv = wa_mfma32(pk[c], tile_row8<D>(s_hi, 32 * jt + l32, 2 * c + g), dv);
-      dv = wa_mfma32(pk[c], tile_row8<D>(s_lo, 32 * jt + l32, 2 * c + g), dv);
+      kd[c] = *(const bf16x8*)(kbase + tr * p.k_st + c * 16);
+      vd[c] = *(const bf16x8*)(vbase + tr * p.v_st + c * 16);
     }
-    __syncthreads();  // the previous column tile's staging has been read (and, first, the fragments)
-    const float zc = s_z[32 * jt + l32];
+  };
+  int gi = blockIdx.x * p.kv_groups_per_wg + w;
+  if (gi < g_end) load_group(gi, kf, vf);  // in flight while the state gradient is staged
+  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
+  for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
+  __syncthreads();
+  bf16_t* dkb = (bf16_t*)p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + 4 * g;
+  bf16_t* dvb = (bf16_t*)p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + 4 * g;
+#pragma unroll 1
+  for (; gi < g_end; gi += 4) {
+    const int t = gi * 32 + l32;
+    const bool ok = t < p.Lkv;
+    bf16x8 pk[DC];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3), pr = row ^ ((row >> 2) & 1);
-      stk[pr * 32 + l32] = dk[r] + zc;
-      stv[pr * 32 + l32] = dv[r];
+    for (int c = 0; c < DC; ++c) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pk[c][e] = (bf16_t)elu1f((float)kf[c][e]);
     }
-    __syncthreads();
+    // k at this lane's epilogue channels 32 jt + 8 rq + 4 g + i lies in chunk 4 jt + rq, elements
+    // 4g..: fragment c = 2 jt + rq / 2 of the lane half rq & 1. The two lanes of a token swap the
+    // halves the other needs; afterwards kf[c] holds elements 4g.. of chunk 2c, then of chunk 2c + 1.
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i, row = u >> 2, cc = u & 3, pr = row ^ ((row >> 2) & 1);
-      if (t0 + row >= p.Lkv) continue;
-      const f32x4 a0 = *(const f32x4*)(stk + pr * 32 + cc * 8), a1 = *(const f32x4*)(stk + pr * 32 + cc * 8 + 4);
-      const f32x4 b0 = *(const f32x4*)(stv + pr * 32 + cc * 8), b1 = *(const f32x4*)(stv + pr * 32 + cc * 8 + 4);
-      const bf16x8 kk = *(const bf16x8*)(s_k + row * D + (((4 * jt + cc) ^ (row & 15)) * 8));
-      bf16x8 ok, ov;
+    for (int c = 0; c < DC; ++c) {
+      const u32x4 u = __builtin_bit_cast(u32x4, kf[c]);
+      const uint32_t m0 = g ? u[2] : u[0], m1 = g ? u[3] : u[1];  // own elements 4g..
+      const uint32_t s0 = g ? u[0] : u[2], s1 = g ? u[1] : u[3];  // the partner's elements
+      const uint32_t r0 = (uint32_t)__shfl_xor((int)s0, 32, 64), r1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+      kf[c] = __builtin_bit_cast(bf16x8, g ? u32x4{r0, r1, m0, m1} : u32x4{m0, m1, r0, r1});
+    }
+#pragma unroll 1
+    for (int jt = 0; jt < DT; ++jt) {
+      f32x16 dk = f32x16{}, dv = f32x16{};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ok[e] = (bf16_t)(a0[e] * elu1_grad((float)kk[e]));
-        ok[e + 4] = (bf16_t)(a1[e] * elu1_grad((float)kk[e + 4]));
-        ov[e] = (bf16_t)b0[e];
-        ov[e + 4] = (bf16_t)b1[e];
+      for (int c = 0; c < DC; ++c) {
+        dk = wa_mfma32(tile_tr8n<D>(s_hi, c, 32 * jt, lane), vf[c], dk);
+        dk = wa_mfma32(tile_tr8n<D>(s_lo, c, 32 * jt, lane), vf[c], dk);
+        dv = wa_mfma32(tile_row8<D>(s_hi, 32 * jt + l32, 2 * c + g), pk[c], dv);
+        dv = wa_mfma32(tile_row8<D>(s_lo, 32 * jt + l32, 2 * c + g), pk[c], dv);
       }
-      const int64_t t = t0 + row;
-      *(bf16x8*)((bf16_t*)p.dk + (int64_t)b * p.dk_sb + t * p.dk_st + (int64_t)h * p.dk_sh + 32 * jt + cc * 8) = ok;
-      *(bf16x8*)((bf16_t*)p.dv + (int64_t)b * p.dv_sb + t * p.dv_st + (int64_t)h * p.dv_sh + 32 * jt + cc * 8) = ov;
+      const bf16x8 k01[2] = {kf[0], kf[1]};  // this tile's K values (the array rotates below)
+      // after the last column tile's products the fragments are dead: the next group's loads go out
+      // before this tile's stores
+      if (jt == DT - 1 && gi + 4 < g_end) load_group(gi + 4, kf, vf);
+      if (ok) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int e0 = 32 * jt + 8 * rq + 4 * g;
+          const f32x4 z4 = *(const f32x4*)(s_z + e0);
+          const bf16x8 kc = k01[rq >> 1];  // fragments 2 jt, 2 jt + 1
+          bf16x4 ok4, ov4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float kv = (float)kc[4 * (rq & 1) + i];
+            ok4[i] = (bf16_t)((dk[rq * 4 + i] + z4[i]) * elu1_grad(kv));
+            ov4[i] = (bf16_t)dv[rq * 4 + i];
+          }
+          *(bf16x4*)(dkb + (int64_t)t * p.dk_st + 32 * jt + 8 * rq) = ok4;
+          *(bf16x4*)(dvb + (int64_t)t * p.dv_st + 32 * jt + 8 * rq) = ov4;
+        }
+      }
+      // rotate so the next column tile's fragments sit at 0 and 1 (static register indices: a
+      // runtime index into the array compiles to select chains)
+      if (jt < DT - 1) {
+#pragma unroll
+        for (int c = 0; c + 2 < DC; ++c) kf[c] = kf[c + 2];
+      }
     }
-  }
-  __syncthreads();  // every read of this tile's K (and of the staging) before the next tile's loads
   }
 }
 
@@ -1041,8 +1041,6 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
   bp.dkv_bf16 = a->dkv_dtype == WA_BF16;
-  bp.k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2;
-  bp.v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
   bp.heads = a->heads; bp.n_heads = (int)nh; bp.H = (int)a->H; bp.B = (int)a->B; bp.Lq = (int)a->Lq;
   bp.Lkv = (int)a->Lkv; bp.n_qt = (int)((a->Lq + 127) / 128);
   bp.part = (float*)a->workspace;
@@ -1052,22 +1050,22 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
   dim3 gq((unsigned)bp.n_qt, (unsigned)nh, (unsigned)a->B), gk((unsigned)((a->Lkv + 127) / 128), (unsigned)nh, (unsigned)a->B);
   const int64_t total = a->B * nh * (a->D * a->D + a->D);
   int rc;
-  if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_q_kernel<128>, gq, dim3(256), 0, s, bp);
-  else hipLaunchKernelGGL(elu1_bwd_q_kernel<64>, gq, dim3(256), 0, s, bp);
+  if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_q_kernel<128>, gq, dim3(512), 0, s, bp);
+  else hipLaunchKernelGGL(elu1_bwd_q_kernel<64>, gq, dim3(512), 0, s, bp);
   if ((rc = wa_launch_status("elu1_bwd_q"))) return rc;
   hipLaunchKernelGGL(elu1_bwd_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, bp, (int)a->D);
   if ((rc = wa_launch_status("elu1_bwd_reduce"))) return rc;
-  // bf16 K / V and bf16 dK / dV with 16-byte aligned rows: the coalesced kernel
+  // bf16 K / V and bf16 dK / dV with 16-byte aligned rows: the streaming kernel
   const bool kv16 = bp.dkv_bf16 && a->kv_dtype == WA_BF16 && wa_aligned16(a->dk) && wa_aligned16(a->dv) &&
                     a->dk_sb % 8 == 0 && a->dk_st % 8 == 0 && a->dk_sh % 8 == 0 && a->dv_sb % 8 == 0 &&
-                    a->dv_st % 8 == 0 && a->dv_sh % 8 == 0 && bp.k_slab < ((int64_t)1 << 31) &&
-                    bp.v_slab < ((int64_t)1 << 31) && 128 * std::max(a->k_st, a->v_st) < ((int64_t)1 << 30);
+                    a->dv_st % 8 == 0 && a->dv_sh % 8 == 0;
   if (kv16) {
-    // about one workgroup per CU: each stages the state gradient once for its run of tiles
-    const int64_t n_tiles = (a->Lkv + 127) / 128;
-    const int64_t per_bh = std::max<int64_t>(1, std::min<int64_t>(n_tiles, (256 + a->B * nh - 1) / (a->B * nh)));
-    bp.kv_tiles_per_wg = (int)((n_tiles + per_bh - 1) / per_bh);
-    const dim3 gk16((unsigned)((n_tiles + bp.kv_tiles_per_wg - 1) / bp.kv_tiles_per_wg), (unsigned)nh, (unsigned)a->B);
+    // about two workgroups per CU (64 KB of staged state each at D = 128), each staging the state
+    // gradient once for its run of 32-token groups
+    const int64_t n_groups = (a->Lkv + 31) / 32;
+    const int64_t per_bh = std::max<int64_t>(1, std::min<int64_t>((n_groups + 3) / 4, (512 + a->B * nh - 1) / (a->B * nh)));
+    bp.kv_groups_per_wg = (int)((n_groups + per_bh - 1) / per_bh);
+    const dim3 gk16((unsigned)((n_groups + bp.kv_groups_per_wg - 1) / bp.kv_groups_per_wg), (unsigned)nh, (unsigned)a->B);
     if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk16, dim3(256), 0, s, bp);
     else hipLaunchKernelGGL(elu1_bwd_kv16_kernel<64>, gk16, dim3(256), 0, s, bp);
   } else {
