@@ -261,11 +261,11 @@ __global__ void __launch_bounds__(256) k2q_kernel(BwdParams p) {
 // the slab's first rows), so the waits count them: at the top of step t only the loads of the (up to
 // two) later tiles may still be pending. Row lists (with each block's valid row count) are staged
 // in LDS once, so the loop issues no other memory reads while they fit.
-// Ring depth and staged list length. dK/dV (one workgroup per CU at D = 128: its accumulators and
-// K/V fragments take ~450 registers per lane) takes four stages for 128-row blocks; dQ fits two
-// waves per SIMD (256 registers), so two workgroups share a CU and it keeps a 2-stage ring (two
-// rings fit the CU's LDS).
-template <int BS> constexpr int bwd_stages() { return BS == 128 ? 4 : 2; }
+// Ring depth and staged list length of the dK/dV pass: one workgroup per CU (8 waves for 128-row
+// blocks) with a 3-stage ring, the staged list and the P exchange in its LDS; dQ fits two waves per
+// SIMD (256 registers), so two workgroups share a CU and it keeps a 2-stage ring (two rings fit the
+// CU's LDS).
+template <int BS> constexpr int bwd_stages() { return BS == 128 ? 3 : 2; }
 template <int BS> constexpr int bwd_list_max() { return BS == 128 ? 4096 : 1024; }
 constexpr int DQ_STAGES = 2, DQ_LIST_MAX = 1024;
 
@@ -493,60 +493,72 @@ __global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// dkdv: one workgroup (BS / 32 waves, wave w = keys 32w..) per (batch, head slot, key block);
-// 64-query steps over the query blocks that listed it; Q, dO and the rows' log-sum-exp and delta
-// stream through the ring (the statistics as 4-byte direct-to-LDS loads, scaled at use).
+// dkdv: one workgroup per (batch, head slot, key block); 64-query steps over the query blocks that
+// listed it; Q, dO and the rows' log-sum-exp and delta stream through the ring (the statistics as
+// 4-byte direct-to-LDS loads, scaled at use). Each 32-key group has two waves, w and w + NKG, which
+// share a SIMD:
+//   the S-wave (w < NKG) holds the group's K fragments and the dV accumulators: S = Q K^T,
+//     P = exp2(S scale - lse2) (fp32, to LDS), dV += P^T dO;
+//   the dP-wave holds the V fragments and the dK accumulators: dP = dO V^T, then (P from LDS)
+//     dS = P (dP - delta), dK += dS^T Q.
+// Each wave keeps about half the registers of one wave per group (K/V fragments and both
+// accumulators, ~450 per lane), so two waves fit a SIMD and one's softmax runs beside the other's
+// MFMAs.
 // ---------------------------------------------------------------------------------------------
 template <int D, int BS>
-__global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
-  constexpr int NW = BS / 32, DC = D / 16, DT = D / 32;
+__global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
+  constexpr int NKG = BS / 32, NW = 2 * NKG, NT = 64 * NW, DC = D / 16, DT = D / 32;
   constexpr int TILE = 64 * D, ST = bwd_stages<BS>(), LM = bwd_list_max<BS>();
   constexpr int QPB = BS / 64;                     // 64-query steps per query block
   using TS = TileStream<D, NW>;
   constexpr int PER = 2 * TS::NI + 2;              // Q and dO tiles, lse and delta rows
   // stage s: Q tile at [0, TILE), dO tile at [TILE, 2 TILE), then 64 lse and 64 delta floats
-  constexpr int SS = 2 * TILE + 256, XS = ST == 4 ? SS : 8;
+  constexpr int SS = 2 * TILE + 256, XS2 = ST >= 3 ? SS : 8, XS3 = ST >= 4 ? SS : 8;
   __shared__ __attribute__((aligned(1024))) bf16_t qd0[SS];
   __shared__ __attribute__((aligned(1024))) bf16_t qd1[SS];
-  __shared__ __attribute__((aligned(1024))) bf16_t qd2[XS];
-  __shared__ __attribute__((aligned(1024))) bf16_t qd3[XS];
+  __shared__ __attribute__((aligned(1024))) bf16_t qd2[XS2];
+  __shared__ __attribute__((aligned(1024))) bf16_t qd3[XS3];
+  // P of each key group (fp32, accumulator order), register r of 32-query tile qt of lane L at
+  // [group][qt][r / 4][L]: every access is 16 bytes per lane, lanes contiguous
+  __shared__ __attribute__((aligned(1024))) f32x4 s_p[NKG][2][4][64];
   __shared__ int32_t s_lst[LM];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
+  const int kg = w % NKG;
+  const bool swave = w < NKG;  // wave-uniform role
   // 1-D grid over (batch, head slot, key block), in kv_order when there is one
   const int id = p.kv_order ? p.kv_order[blockIdx.x] : (int)blockIdx.x;
   const int j = id % p.Nkv, hs = (id / p.Nkv) % p.n_heads, b = id / (p.Nkv * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
   const int real = kv_real(p, j, BS);
-  const int key = w * 32 + l32;  // this lane's key within the block
+  const int key = kg * 32 + l32;  // this lane's key within the block
   const bool k_ok = key < real;
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
   const int32_t* lst = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
   const int nl = p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j];
   // the whole row of the table (Nq slots, the first nl valid): no wait for nl before the reads
-  for (int i = tid; i < min(p.Nq, LM); i += 2 * BS) s_lst[i] = lst[i];
+  for (int i = tid; i < min(p.Nq, LM); i += NT) s_lst[i] = lst[i];
 
-  // K^T and V^T fragments (B operands): lane holds row `key`, channels 16c + 8g .. +8
-  bf16x8 kf[DC], vf[DC];
+  // K^T (S-wave) or V^T (dP-wave) fragments (B operands): lane holds row `key`, channels
+  // 16c + 8g .. +8
+  bf16x8 kvf[DC];
   {
     const int kr = j * BS + (k_ok ? key : 0);
-    const bf16_t* kp = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)kr * p.k_st;
-    const bf16_t* vp = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)kr * p.v_st;
+    const bf16_t* src = swave ? p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)kr * p.k_st
+                              : p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)kr * p.v_st;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
-      const bf16x8 a = *(const bf16x8*)(kp + c * 16 + g * 8);
-      const bf16x8 d = *(const bf16x8*)(vp + c * 16 + g * 8);
-      kf[c] = k_ok ? a : bf16x8{};
-      vf[c] = k_ok ? d : bf16x8{};
+      const bf16x8 a = *(const bf16x8*)(src + c * 16 + g * 8);
+      kvf[c] = k_ok ? a : bf16x8{};
     }
   }
 #pragma unroll
-  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(kf[c]), "+v"(vf[c]));  // before the ring's loads
+  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(kvf[c]));  // before the ring's loads
   __syncthreads();  // s_lst
-  f32x16 dkacc[DT], dvacc[DT];
+  f32x16 acc[DT];   // S-wave: dV; dP-wave: dK (lane = channel 32 tt + l32, registers = keys)
 #pragma unroll
-  for (int t = 0; t < DT; ++t) dkacc[t] = dvacc[t] = f32x16{};
+  for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
 
   TS qs, ds;
   qs.init(p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh, p.q_st, p.q_slab, w, lane);
@@ -581,136 +593,147 @@ __global__ void __launch_bounds__(2 * BS) bwd_dkdv_kernel(BwdParams p) {
     const int e = entry(t / QPB);
     const float mult = (float)(e >> 16);
     const int q0r = (e & 0xFFFF) * BS + 64 * (t % QPB);
-    if (q0r >= p.Lq) return;
+    if (q0r >= p.Lq) return;  // uniform over the workgroup
     const bf16_t* qc = stage_of<SV>(qd0, qd1, qd2, qd3);
     const bf16_t* dc = qc + TILE;
     const float* st_lse2 = (const float*)(qc + 2 * TILE);
     const float* st_dl = st_lse2 + 64;
-    // S[q, key] = Q K^T and dP[q, key] = dO V^T per 32-query tile (A from LDS, B from registers)
-    f32x16 sacc[2], pacc[2];
+    // S[q, key] = Q K^T (S-wave) or dP[q, key] = dO V^T (dP-wave) per 32-query tile (A from LDS,
+    // B from registers); lane = key, registers = queries q = 32 qt + 8 rq + 4 g + i
+    const bf16_t* at = swave ? qc : dc;
+    f32x16 sacc[2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) sacc[qt] = pacc[qt] = f32x16{};
+    for (int qt = 0; qt < 2; ++qt) sacc[qt] = f32x16{};
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        sacc[qt] = wa_mfma32(tile_row8<D>(qc, qt * 32 + l32, 2 * c + g), kf[c], sacc[qt]);
-        pacc[qt] = wa_mfma32(tile_row8<D>(dc, qt * 32 + l32, 2 * c + g), vf[c], pacc[qt]);
-      }
+      for (int qt = 0; qt < 2; ++qt) sacc[qt] = wa_mfma32(tile_row8<D>(at, qt * 32 + l32, 2 * c + g), kvf[c], sacc[qt]);
     }
-    // P and dS in accumulator order (lane = key, registers = queries q = 32 qt + 8 rq + 4 g + i),
-    // scaled by multiplicity. Queries past Lq stream zero Q, dO and statistics rows: their dS and
-    // dO are 0, so they add nothing; keys past the block's end are dropped by the epilogue.
-    bf16x8 pb[4], dsb[4];
+    // P (scaled by multiplicity) to LDS, or dS from the group's P; queries past Lq stream zero Q,
+    // dO and statistics rows, so their dS and dO are 0 and they add nothing; keys past the
+    // block's end are dropped by the epilogue
+    bf16x8 ab[4];
+    if (swave) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < 2; ++qt) {
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x4 l4 = *(const f32x4*)(st_lse2 + qt * 32 + 8 * rq + 4 * g);
-        const f32x4 d4 = *(const f32x4*)(st_dl + qt * 32 + 8 * rq + 4 * g);
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 l4 = *(const f32x4*)(st_lse2 + qt * 32 + 8 * rq + 4 * g);
+          f32x4 p4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = rq * 4 + i;
-          const float pr = __builtin_amdgcn_exp2f(fmaf(sacc[qt][r], p.scale_log2, -l4[i])) * mult;
-          pb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)pr;
-          dsb[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(pr * (pacc[qt][r] - d4[i]));
+          for (int i = 0; i < 4; ++i) {
+            const int r = rq * 4 + i;
+            p4[i] = __builtin_amdgcn_exp2f(fmaf(sacc[qt][r], p.scale_log2, -l4[i])) * mult;
+            ab[qt * 2 + (r >> 3)][r & 7] = (bf16_t)p4[i];
+          }
+          s_p[kg][qt][rq][lane] = p4;
         }
       }
     }
-    // dV[key, d] += P^T dO, dK[key, d] += dS^T Q: A from registers, B by transpose reads
+    __syncthreads();  // P of every group in LDS
+    if (!swave) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 d4 = *(const f32x4*)(st_dl + qt * 32 + 8 * rq + 4 * g);
+          const f32x4 p4 = s_p[kg][qt][rq][lane];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = rq * 4 + i;
+            ab[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(p4[i] * (sacc[qt][r] - d4[i]));
+          }
+        }
+      }
+    }
+    // dV[key, d] += P^T dO (S-wave), dK[key, d] += dS^T Q (dP-wave): A from registers, B by
+    // transpose reads
+    const bf16_t* bt = swave ? dc : qc;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int tt = 0; tt < DT; ++tt) {
-        dvacc[tt] = wa_mfma32(pb[c], tile_tr8<D>(dc, c, 32 * tt, lane), dvacc[tt]);
-        dkacc[tt] = wa_mfma32(dsb[c], tile_tr8<D>(qc, c, 32 * tt, lane), dkacc[tt]);
-      }
+      for (int tt = 0; tt < DT; ++tt) acc[tt] = wa_mfma32(ab[c], tile_tr8<D>(bt, c, 32 * tt, lane), acc[tt]);
     }
   };
   // prologue: tiles 0 .. ST - 2
   if (total > 0) issue(IC<0>{}, 0);
-  if constexpr (ST == 4) {
+  if constexpr (ST >= 3) {
     if (total > 1) issue(IC<1>{}, 1);
+  }
+  if constexpr (ST >= 4) {
     if (total > 2) issue(IC<2>{}, 2);
   }
   for (int t = 0; t < total; t += ST) {
     step(IC<0>{}, t);
     if (t + 1 < total) step(IC<1>{}, t + 1);
-    if constexpr (ST == 4) {
+    if constexpr (ST >= 3) {
       if (t + 2 < total) step(IC<2>{}, t + 2);
+    }
+    if constexpr (ST >= 4) {
       if (t + 3 < total) step(IC<3>{}, t + 3);
     }
   }
-  // accumulator lane (d = 32t + l32, g) holds keys 32w + 8(r/4) + 4g + r%4 (keys past the
-  // block's end are dropped)
-  const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
-  const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32;
+  // accumulator lane (d = 32t + l32, g) holds keys 32 kg + 8(r/4) + 4g + r%4 (keys past the
+  // block's end are dropped); dK is scaled here
+  const float osc = swave ? 1.f : p.scale;
   if (p.dkv_vec) {
     // bf16 tiles staged in the (drained) ring: row r, 16-byte chunk c at chunk c ^ 4 ((r >> 2) & 1),
     // so the two rows a wave writes per register use different banks; then 16-byte stores
     __syncthreads();
-    bf16_t* sk = qd0;
-    bf16_t* sv = qd1;
+    bf16_t* stg = swave ? qd1 : qd0;  // dV, dK
 #pragma unroll
     for (int tt = 0; tt < DT; ++tt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3), col = 32 * tt + l32;
+        const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3), col = 32 * tt + l32;
         const int at = kk * D + (((col >> 3) ^ (4 * ((kk >> 2) & 1))) << 3) + (col & 7);
-        const bool kval = kk < real;
-        sk[at] = (bf16_t)(kval ? dkacc[tt][r] * p.scale : 0.f);
-        sv[at] = (bf16_t)(kval ? dvacc[tt][r] : 0.f);
+        stg[at] = (bf16_t)(kk < real ? acc[tt][r] * osc : 0.f);
       }
     }
     __syncthreads();
     constexpr int CPR = D / 8;
-    for (int u = tid; u < BS * CPR; u += 2 * BS) {
+    const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh;
+    const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh;
+    for (int u = tid; u < BS * CPR; u += NT) {
       const int kk = u / CPR, c = u % CPR, row = j * BS + kk;
       if (row >= p.Lkv) continue;
       const int at = kk * D + ((c ^ (4 * ((kk >> 2) & 1))) << 3);
-      *(bf16x8*)((bf16_t*)p.dk + dk0 - l32 + (int64_t)row * p.dk_st + c * 8) = *(const bf16x8*)(sk + at);
-      *(bf16x8*)((bf16_t*)p.dv + dv0 - l32 + (int64_t)row * p.dv_st + c * 8) = *(const bf16x8*)(sv + at);
+      *(bf16x8*)((bf16_t*)p.dk + dk0 + (int64_t)row * p.dk_st + c * 8) = *(const bf16x8*)(qd0 + at);
+      *(bf16x8*)((bf16_t*)p.dv + dv0 + (int64_t)row * p.dv_st + c * 8) = *(const bf16x8*)(qd1 + at);
     }
     return;
   }
+  const int64_t o0 = swave ? (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32 : (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
+  const int64_t ost = swave ? p.dv_st : p.dk_st;
   if (p.dkv_bf16) {
+    bf16_t* dst = (bf16_t*)(swave ? p.dv : p.dk) + o0;
 #pragma unroll
     for (int tt = 0; tt < DT; ++tt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
         const int row = j * BS + kk;
-        if (row < p.Lkv) {
-          const bool kval = kk < real;
-          ((bf16_t*)p.dk)[dk0 + (int64_t)row * p.dk_st + 32 * tt] = (bf16_t)(kval ? dkacc[tt][r] * p.scale : 0.f);
-          ((bf16_t*)p.dv)[dv0 + (int64_t)row * p.dv_st + 32 * tt] = (bf16_t)(kval ? dvacc[tt][r] : 0.f);
-        }
+        if (row < p.Lkv) dst[(int64_t)row * ost + 32 * tt] = (bf16_t)(kk < real ? acc[tt][r] * osc : 0.f);
       }
     }
     return;
   }
   // fp32: previous values of a tile are all read before any store (see the dq epilogue)
-  float* dk_col = (float*)p.dk + dk0;
-  float* dv_col = (float*)p.dv + dv0;
+  float* col = (float*)(swave ? p.dv : p.dk) + o0;
+  const int add = swave ? p.dv_acc : p.dk_acc;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
-    float pk[16], pv[16];
+    float prev[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = j * BS + w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-      const bool in = row < p.Lkv;
-      pk[r] = p.dk_acc && in ? dk_col[(int64_t)row * p.dk_st + 32 * tt] : 0.f;
-      pv[r] = p.dv_acc && in ? dv_col[(int64_t)row * p.dv_st + 32 * tt] : 0.f;
+      const int row = j * BS + kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+      prev[r] = add && row < p.Lkv ? col[(int64_t)row * ost + 32 * tt] : 0.f;
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int kk = w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+      const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
       const int row = j * BS + kk;
-      if (row < p.Lkv) {
-        const bool kval = kk < real;
-        dk_col[(int64_t)row * p.dk_st + 32 * tt] = pk[r] + (kval ? dkacc[tt][r] * p.scale : 0.f);
-        dv_col[(int64_t)row * p.dv_st + 32 * tt] = pv[r] + (kval ? dvacc[tt][r] : 0.f);
-      }
+      if (row < p.Lkv) col[(int64_t)row * ost + 32 * tt] = prev[r] + (kk < real ? acc[tt][r] * osc : 0.f);
     }
   }
 }
@@ -755,7 +778,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     } else {
       kp.kv_order = nullptr;
     }
-    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(2 * BS), 0, s, kp);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(4 * BS), 0, s, kp);
     if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return rc;
   }
   return WA_OK;
