@@ -49,7 +49,7 @@ struct BwdParams {
   bf16_t* dob;       // [B, n_heads, Lq, D]
   int32_t* k2q;      // [B, n_heads, Nkv, Nq]: (query block) | (multiplicity << 16)
   int32_t* k2q_num;  // [B, n_heads, Nkv]
-  int32_t* kv_order; // [B * n_heads * Nkv] key blocks by descending list length (dkdv launch order)
+  int32_t* kv_order; // [B * n_heads * Nkv] per slab, key blocks by descending list length (dkdv launch order)
 };
 
 __device__ __forceinline__ int head_of(const BwdParams& p, int hs) { return p.heads ? p.heads[hs] : hs; }
@@ -455,19 +455,22 @@ __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))
 }
 
 // ---------------------------------------------------------------------------------------------
-// kv_order: the dkdv launch order, longest transposed list first, so that the longest workgroups
-// start first and the kernel does not end on a tail of long ones (a counting sort by list length
-// in one workgroup; blocks of equal length land in any order, which changes nothing but the
-// schedule: every block's dK / dV is computed by one workgroup alone). Needs Nq < KV_ORDER_T.
+// kv_order: the dkdv launch order. Workgroup s sorts the key blocks of (batch, head) slab s by
+// transposed list length, longest first, into kv_order[s Nkv ..] (a counting sort; blocks of
+// equal length land in any order, which changes nothing but the schedule: every block's dK / dV is
+// computed by one workgroup alone). The dkdv grid takes this order XCD by XCD (wa_xcd_remap: XCD x
+// runs a contiguous run of it), so each XCD works through whole slabs, longest blocks first, and a
+// slab's Q and dO tiles are fetched into one L2 instead of eight. Needs Nq < KV_ORDER_T.
 // ---------------------------------------------------------------------------------------------
 constexpr int KV_ORDER_T = 1024;
 
 __global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
   __shared__ int hist[KV_ORDER_T];
-  const int tid = threadIdx.x, n = p.B * p.n_heads * p.Nkv;
+  const int tid = threadIdx.x, n = p.Nkv, base = blockIdx.x * p.Nkv;
+  const int32_t* num = p.k2q_num + base;
   hist[tid] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += KV_ORDER_T) atomicAdd(&hist[min(max(p.k2q_num[i], 0), p.Nq)], 1);
+  for (int i = tid; i < n; i += KV_ORDER_T) atomicAdd(&hist[min(max(num[i], 0), p.Nq)], 1);
   __syncthreads();
   // start[c] = number of blocks longer than c: an inclusive scan over c = Nq, Nq - 1, ..., 0
   const int c = p.Nq - tid;  // this thread's length, for tid <= Nq
@@ -487,8 +490,8 @@ __global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
   if (c >= 0) hist[c] = first;
   __syncthreads();
   for (int i = tid; i < n; i += KV_ORDER_T) {
-    const int len = min(max(p.k2q_num[i], 0), p.Nq);
-    p.kv_order[atomicAdd(&hist[len], 1)] = i;
+    const int len = min(max(num[i], 0), p.Nq);
+    p.kv_order[base + atomicAdd(&hist[len], 1)] = base + i;
   }
 }
 
@@ -526,8 +529,10 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
   const int g = lane >> 5, l32 = lane & 31;
   const int kg = w % NKG;
   const bool swave = w < NKG;  // wave-uniform role
-  // 1-D grid over (batch, head slot, key block), in kv_order when there is one
-  const int id = p.kv_order ? p.kv_order[blockIdx.x] : (int)blockIdx.x;
+  // 1-D grid over (batch, head slot, key block): XCD by XCD through kv_order when there is one
+  // (else through the slabs in order), so an XCD's workgroups share their slabs' Q and dO tiles
+  const int pos = wa_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int id = p.kv_order ? p.kv_order[pos] : pos;
   const int j = id % p.Nkv, hs = (id / p.Nkv) % p.n_heads, b = id / (p.Nkv * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
@@ -773,7 +778,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
   if (bp.dk && bp.dv) {
     BwdParams kp = bp;
     if (bp.Nq < KV_ORDER_T) {
-      hipLaunchKernelGGL(kv_order_kernel, dim3(1), dim3(KV_ORDER_T), 0, s, bp);
+      hipLaunchKernelGGL(kv_order_kernel, dim3((unsigned)(bp.B * nh)), dim3(KV_ORDER_T), 0, s, bp);
       if ((rc = wa_launch_status("bsa_bwd_kv_order"))) return rc;
     } else {
       kp.kv_order = nullptr;
