@@ -49,7 +49,8 @@ struct BwdParams {
   bf16_t* dob;       // [B, n_heads, Lq, D]
   int32_t* k2q;      // [B, n_heads, Nkv, Nq]: (query block) | (multiplicity << 16)
   int32_t* k2q_num;  // [B, n_heads, Nkv]
-  int32_t* kv_order; // [B * n_heads * Nkv] per slab, key blocks by descending list length (dkdv launch order)
+  int4* kv_info;     // [B * n_heads * Nkv] dkdv launch order: per slab, key blocks by descending list
+                     // length as {block id, list length, first list entry, 0}
 };
 
 __device__ __forceinline__ int head_of(const BwdParams& p, int hs) { return p.heads ? p.heads[hs] : hs; }
@@ -456,7 +457,9 @@ __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))
 
 // ---------------------------------------------------------------------------------------------
 // kv_order: the dkdv launch order. Workgroup s sorts the key blocks of (batch, head) slab s by
-// transposed list length, longest first, into kv_order[s Nkv ..] (a counting sort; blocks of
+// transposed list length, longest first, into kv_info[s Nkv ..] with each block's list length and
+// first list entry, so a dkdv workgroup learns all it needs for its first tiles from one load
+// (a counting sort; blocks of
 // equal length land in any order, which changes nothing but the schedule: every block's dK / dV is
 // computed by one workgroup alone). The dkdv grid takes this order XCD by XCD (wa_xcd_remap: XCD x
 // runs a contiguous run of it), so each XCD works through whole slabs, longest blocks first, and a
@@ -491,7 +494,8 @@ __global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
   __syncthreads();
   for (int i = tid; i < n; i += KV_ORDER_T) {
     const int len = min(max(num[i], 0), p.Nq);
-    p.kv_order[base + atomicAdd(&hist[len], 1)] = base + i;
+    const int e0 = len > 0 ? p.k2q[(int64_t)(base + i) * p.Nq] : 0;
+    p.kv_info[base + atomicAdd(&hist[len], 1)] = int4{base + i, len, e0, 0};
   }
 }
 
@@ -529,39 +533,61 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
   const int g = lane >> 5, l32 = lane & 31;
   const int kg = w % NKG;
   const bool swave = w < NKG;  // wave-uniform role
-  // 1-D grid over (batch, head slot, key block): XCD by XCD through kv_order when there is one
-  // (else through the slabs in order), so an XCD's workgroups share their slabs' Q and dO tiles
+  // 1-D grid over (batch, head slot, key block): XCD by XCD through kv_info when there is one
+  // (else through the slabs in order), so an XCD's workgroups share their slabs' Q and dO tiles;
+  // one load gives the block, its list length and its first list entry
   const int pos = wa_xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int id = p.kv_order ? p.kv_order[pos] : pos;
+  int id, nl, e0;
+  if (p.kv_info) {
+    const int4 inf = p.kv_info[pos];
+    id = inf.x;
+    nl = inf.y;
+    e0 = inf.z;
+  } else {
+    id = pos;
+    nl = min(max(p.k2q_num[id], 0), p.Nq);
+    e0 = nl > 0 ? p.k2q[(int64_t)id * p.Nq] : 0;
+  }
+  id = __builtin_amdgcn_readfirstlane(id);
+  nl = __builtin_amdgcn_readfirstlane(nl);
+  e0 = __builtin_amdgcn_readfirstlane(e0);
   const int j = id % p.Nkv, hs = (id / p.Nkv) % p.n_heads, b = id / (p.Nkv * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
+  if (nl == 0) {
+    // no query block listed this key block: its written gradients are zero (accumulated ones
+    // keep their values), with no tile streamed
+    const int rows = max(0, min(BS, p.Lkv - j * BS));
+    constexpr int CPR = D / 8;
+    const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + (int64_t)j * BS * p.dk_st;
+    const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + (int64_t)j * BS * p.dv_st;
+    if (p.dkv_vec) {
+      for (int u = tid; u < rows * CPR; u += NT) {
+        const int kk = u / CPR, c = u % CPR;
+        *(bf16x8*)((bf16_t*)p.dk + dk0 + (int64_t)kk * p.dk_st + c * 8) = bf16x8{};
+        *(bf16x8*)((bf16_t*)p.dv + dv0 + (int64_t)kk * p.dv_st + c * 8) = bf16x8{};
+      }
+    } else {
+      for (int u = tid; u < rows * D; u += NT) {
+        const int kk = u / D, c = u % D;
+        if (p.dkv_bf16) {
+          ((bf16_t*)p.dk)[dk0 + (int64_t)kk * p.dk_st + c] = (bf16_t)0.f;
+          ((bf16_t*)p.dv)[dv0 + (int64_t)kk * p.dv_st + c] = (bf16_t)0.f;
+        } else {
+          if (!p.dk_acc) ((float*)p.dk)[dk0 + (int64_t)kk * p.dk_st + c] = 0.f;
+          if (!p.dv_acc) ((float*)p.dv)[dv0 + (int64_t)kk * p.dv_st + c] = 0.f;
+        }
+      }
+    }
+    return;
+  }
   const int real = kv_real(p, j, BS);
   const int key = kg * 32 + l32;  // this lane's key within the block
   const bool k_ok = key < real;
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
   const int32_t* lst = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
-  const int nl = p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j];
-  // the whole row of the table (Nq slots, the first nl valid): no wait for nl before the reads
-  for (int i = tid; i < min(p.Nq, LM); i += NT) s_lst[i] = lst[i];
-
-  // K^T (S-wave) or V^T (dP-wave) fragments (B operands): lane holds row `key`, channels
-  // 16c + 8g .. +8
   bf16x8 kvf[DC];
-  {
-    const int kr = j * BS + (k_ok ? key : 0);
-    const bf16_t* src = swave ? p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)kr * p.k_st
-                              : p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)kr * p.v_st;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      const bf16x8 a = *(const bf16x8*)(src + c * 16 + g * 8);
-      kvf[c] = k_ok ? a : bf16x8{};
-    }
-  }
-#pragma unroll
-  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(kvf[c]));  // before the ring's loads
-  __syncthreads();  // s_lst
-  f32x16 acc[DT];   // S-wave: dV; dP-wave: dK (lane = channel 32 tt + l32, registers = keys)
+  f32x16 acc[DT];   // S-wave: dV^T; dP-wave: dK^T (lane = key, registers = channels)
 #pragma unroll
   for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
 
@@ -569,10 +595,12 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
   qs.init(p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh, p.q_st, p.q_slab, w, lane);
   ds.init(p.dob + srow * D, D, (int64_t)p.Lq * D * 2, w, lane);
   const int total = nl * QPB;
-  // list entry: (query block) | (multiplicity << 16); lists longer than the LDS copy read the rest
-  // (the empty asm keeps the two reads apart: merged, they become one flat load that must wait
-  // for every direct-to-LDS load in flight)
+  // list entry: (query block) | (multiplicity << 16); the first comes with the block, the rest
+  // from the LDS copy, and lists longer than the copy read global memory (the empty asm keeps the
+  // two reads apart: merged, they become one flat load that must wait for every direct-to-LDS
+  // load in flight)
   auto entry = [&](int s2) {
+    if (s2 == 0) return e0;
     if (s2 < LM) return __builtin_amdgcn_readfirstlane(s_lst[s2]);
     int e = lst[s2];
     asm volatile("" : "+v"(e));
@@ -651,23 +679,39 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
         }
       }
     }
-    // dV[key, d] += P^T dO (S-wave), dK[key, d] += dS^T Q (dP-wave): A from registers, B by
-    // transpose reads
+    // dV^T[d, key] += dO^T P (S-wave), dK^T[d, key] += Q^T dS (dP-wave): A by transpose reads,
+    // B from registers (lane = key, registers = channels d = 32 tt + 8 rq + 4 g + i)
     const bf16_t* bt = swave ? dc : qc;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int tt = 0; tt < DT; ++tt) acc[tt] = wa_mfma32(ab[c], tile_tr8<D>(bt, c, 32 * tt, lane), acc[tt]);
+      for (int tt = 0; tt < DT; ++tt) acc[tt] = wa_mfma32(tile_tr8<D>(bt, c, 32 * tt, lane), ab[c], acc[tt]);
     }
   };
-  // prologue: tiles 0 .. ST - 2
-  if (total > 0) issue(IC<0>{}, 0);
+  // Set-up, all behind the one load of the block's info: the prologue tiles 0 .. ST - 2 (within
+  // the first list entry's query block: no list needed), the list copy, and the K^T (S-wave) or
+  // V^T (dP-wave) fragments (B operands: lane holds row `key`, channels 16c + 8g .. +8). The
+  // fragments are waited for before the first step: later, the compiler (which cannot count the
+  // ring's inline-assembly loads) would wait for every load in flight.
+  static_assert(ST - 1 <= QPB, "the prologue tiles must come from the first list entry");
+  issue(IC<0>{}, 0);
   if constexpr (ST >= 3) {
     if (total > 1) issue(IC<1>{}, 1);
   }
-  if constexpr (ST >= 4) {
-    if (total > 2) issue(IC<2>{}, 2);
+  for (int i = tid; i < min(nl, LM); i += NT) s_lst[i] = lst[i];
+  {
+    const int kr = j * BS + (k_ok ? key : 0);
+    const bf16_t* src = swave ? p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh + (int64_t)kr * p.k_st
+                              : p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + (int64_t)kr * p.v_st;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const bf16x8 a = *(const bf16x8*)(src + c * 16 + g * 8);
+      kvf[c] = k_ok ? a : bf16x8{};
+    }
   }
+#pragma unroll
+  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(kvf[c]));
+  __syncthreads();  // s_lst
   for (int t = 0; t < total; t += ST) {
     step(IC<0>{}, t);
     if (t + 1 < total) step(IC<1>{}, t + 1);
@@ -678,21 +722,23 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
       if (t + 3 < total) step(IC<3>{}, t + 3);
     }
   }
-  // accumulator lane (d = 32t + l32, g) holds keys 32 kg + 8(r/4) + 4g + r%4 (keys past the
-  // block's end are dropped); dK is scaled here
+  // each lane holds its key's row: channels 32 tt + 8 rq + 4 g .. + 3 of tile tt (keys past the
+  // block's end get zeros); dK is scaled here
   const float osc = swave ? 1.f : p.scale;
   if (p.dkv_vec) {
-    // bf16 tiles staged in the (drained) ring: row r, 16-byte chunk c at chunk c ^ 4 ((r >> 2) & 1),
-    // so the two rows a wave writes per register use different banks; then 16-byte stores
+    // bf16 rows staged in the (drained) ring, row r's 16-byte chunk c at chunk c ^ swz(r): one
+    // 8-byte write per (tile, rq), then 16-byte stores of whole rows
+    auto swz = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
     __syncthreads();
     bf16_t* stg = swave ? qd1 : qd0;  // dV, dK
 #pragma unroll
     for (int tt = 0; tt < DT; ++tt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3), col = 32 * tt + l32;
-        const int at = kk * D + (((col >> 3) ^ (4 * ((kk >> 2) & 1))) << 3) + (col & 7);
-        stg[at] = (bf16_t)(kk < real ? acc[tt][r] * osc : 0.f);
+      for (int rq = 0; rq < 4; ++rq) {
+        bf16x4 v4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = (bf16_t)(k_ok ? acc[tt][rq * 4 + i] * osc : 0.f);
+        *(bf16x4*)(stg + key * D + (((4 * tt + rq) ^ swz(key)) << 3) + 4 * g) = v4;
       }
     }
     __syncthreads();
@@ -702,44 +748,40 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
     for (int u = tid; u < BS * CPR; u += NT) {
       const int kk = u / CPR, c = u % CPR, row = j * BS + kk;
       if (row >= p.Lkv) continue;
-      const int at = kk * D + ((c ^ (4 * ((kk >> 2) & 1))) << 3);
+      const int at = kk * D + ((c ^ swz(kk)) << 3);
       *(bf16x8*)((bf16_t*)p.dk + dk0 + (int64_t)row * p.dk_st + c * 8) = *(const bf16x8*)(qd0 + at);
       *(bf16x8*)((bf16_t*)p.dv + dv0 + (int64_t)row * p.dv_st + c * 8) = *(const bf16x8*)(qd1 + at);
     }
     return;
   }
-  const int64_t o0 = swave ? (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + l32 : (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + l32;
-  const int64_t ost = swave ? p.dv_st : p.dk_st;
+  const int row = j * BS + key;
+  if (row >= p.Lkv) return;
+  const int64_t o0 = (swave ? (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + (int64_t)row * p.dv_st
+                            : (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + (int64_t)row * p.dk_st) + 4 * g;
   if (p.dkv_bf16) {
     bf16_t* dst = (bf16_t*)(swave ? p.dv : p.dk) + o0;
 #pragma unroll
     for (int tt = 0; tt < DT; ++tt) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const int row = j * BS + kk;
-        if (row < p.Lkv) dst[(int64_t)row * ost + 32 * tt] = (bf16_t)(kk < real ? acc[tt][r] * osc : 0.f);
-      }
+      for (int r = 0; r < 16; ++r)
+        dst[32 * tt + 8 * (r >> 2) + (r & 3)] = (bf16_t)(k_ok ? acc[tt][r] * osc : 0.f);
     }
     return;
   }
-  // fp32: previous values of a tile are all read before any store (see the dq epilogue)
-  float* col = (float*)(swave ? p.dv : p.dk) + o0;
+  // fp32: every previous value is read before any store (a load issued after a store waits for it)
+  float* dst = (float*)(swave ? p.dv : p.dk) + o0;
   const int add = swave ? p.dv_acc : p.dk_acc;
+  float prev[DT][16];
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
-    float prev[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = j * BS + kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-      prev[r] = add && row < p.Lkv ? col[(int64_t)row * ost + 32 * tt] : 0.f;
-    }
+    for (int r = 0; r < 16; ++r) prev[tt][r] = add ? dst[32 * tt + 8 * (r >> 2) + (r & 3)] : 0.f;
+  }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kk = kg * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-      const int row = j * BS + kk;
-      if (row < p.Lkv) col[(int64_t)row * ost + 32 * tt] = prev[r] + (kk < real ? acc[tt][r] * osc : 0.f);
-    }
+  for (int tt = 0; tt < DT; ++tt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      dst[32 * tt + 8 * (r >> 2) + (r & 3)] = prev[tt][r] + (k_ok ? acc[tt][r] * osc : 0.f);
   }
 }
 
@@ -781,7 +823,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
       hipLaunchKernelGGL(kv_order_kernel, dim3((unsigned)(bp.B * nh)), dim3(KV_ORDER_T), 0, s, bp);
       if ((rc = wa_launch_status("bsa_bwd_kv_order"))) return rc;
     } else {
-      kp.kv_order = nullptr;
+      kp.kv_info = nullptr;
     }
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(4 * BS), 0, s, kp);
     if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return rc;
@@ -797,7 +839,7 @@ extern "C" int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_
                                               int64_t block_size) {
   const int64_t nq = (Lq + block_size - 1) / block_size, nkv = (Lkv + block_size - 1) / block_size;
   return 2 * align256(B * n_heads * Lq * 4) + align256(B * n_heads * Lq * D * 2) +
-         align256(B * n_heads * nkv * nq * 4) + 2 * align256(B * n_heads * nkv * 4);
+         align256(B * n_heads * nkv * nq * 4) + align256(B * n_heads * nkv * 4) + align256(B * n_heads * nkv * 16);
 }
 
 extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
@@ -863,7 +905,7 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   ws += align256(a->B * nh * nkv * nq * 4);
   bp.k2q_num = (int32_t*)ws;
   ws += align256(a->B * nh * nkv * 4);
-  bp.kv_order = (int32_t*)ws;
+  bp.kv_info = (int4*)ws;
 
   hipStream_t s = (hipStream_t)stream;
   if (a->D == 64 && a->block_size == 64) return launch_bwd<64, 64>(bp, s);
