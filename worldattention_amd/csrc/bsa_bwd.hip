@@ -311,7 +311,10 @@ __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))
   __shared__ int32_t s_lst[LM];  // visited block | (its valid key count << 16)
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
-  const int qb = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
+  // 1-D grid over (batch, head slot, query block), taken XCD by XCD (wa_xcd_remap): an XCD runs
+  // a contiguous run of whole slabs, so the query blocks of a head share its K / V tiles in one L2
+  const int pos = wa_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int qb = pos % p.Nq, hs = (pos / p.Nq) % p.n_heads, b = pos / (p.Nq * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
   const int64_t irow = ((int64_t)b * p.H + h) * p.Nq + qb;
@@ -814,7 +817,7 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     hipLaunchKernelGGL(k2q_kernel, dim3((bp.Nkv + 255) / 256, nh, bp.B), dim3(256), 0, s, bp);
   if ((rc = wa_launch_status("bsa_bwd_k2q"))) return rc;
   if (bp.dq) {
-    hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3(bp.Nq, nh, bp.B), dim3(2 * BS), 0, s, bp);
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3((unsigned)(bp.Nq * nh * bp.B)), dim3(2 * BS), 0, s, bp);
     if ((rc = wa_launch_status("bsa_bwd_dq"))) return rc;
   }
   if (bp.dk && bp.dv) {
@@ -865,7 +868,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(nq <= 65535 && nkv <= 65535 && a->Lq < (1 << 30) && a->Lkv < (1 << 30), "wa_bsa_bwd: problem too large");
   const int64_t nh = a->heads ? a->n_heads : a->H;
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_bwd: bad head count");
-  WA_CHECK_ARG(a->B * nh * nkv < ((int64_t)1 << 31), "wa_bsa_bwd: too many key blocks");
+  WA_CHECK_ARG(a->B * nh * nkv < ((int64_t)1 << 31) && a->B * nh * nq < ((int64_t)1 << 31),
+               "wa_bsa_bwd: too many key or query blocks");
   // the tile streams address one (batch, head) slab with 32-bit byte offsets
   const int64_t q_slab = ((a->Lq - 1) * a->q_st + a->D) * 2;
   const int64_t k_slab = ((a->Lkv - 1) * a->k_st + a->D) * 2, v_slab = ((a->Lkv - 1) * a->v_st + a->D) * 2;
