@@ -352,6 +352,9 @@ bsa_unit_kernel(FwdParams p) {
   const int g = lane >> 5, l32 = lane & 31;
 
   const int u = wa_xcd_remap(blockIdx.x, p.n_units);
+  // The prologue's memory reads in two round trips: the unit entry with the head map beside it,
+  // then (once the row is known) its visit count, its list window and Q together.
+  const int hmap = p.heads && lane < min(p.n_heads, 64) ? p.heads[lane] : 0;
   int64_t row;
   int split;
   if (p.units) {
@@ -365,23 +368,23 @@ bsa_unit_kernel(FwdParams p) {
   const int qb = (int)(row % p.Nq);
   const int64_t bh = row / p.Nq;
   const int hs = (int)(bh % p.n_heads), b = (int)(bh / p.n_heads);
-  const int h = p.heads ? p.heads[hs] : hs;
+  int h = hs;
+  if (p.heads) h = p.n_heads <= 64 ? __builtin_amdgcn_readlane(hmap, hs) : p.heads[hs];
   if (h < 0 || h >= p.H) return;  // uniform per workgroup
   const int64_t irow = ((int64_t)b * p.H + h) * p.Nq + qb;
 
-  const int n = row_visits(p, irow);
-  const int s_begin = split * p.split;
-  const int s_end = min(n, s_begin + p.split);
-  // A unit beyond this row's list returns; split 0 of a row with no visits runs on with an empty
-  // list and writes the empty row (zero attention).
-  if (s_begin >= s_end && (n > 0 || split > 0)) return;
-  const int ns = min((n + p.split - 1) / p.split, p.max_splits);
-
+  // The row's list entries at positions lane (j0) and split * p.split + lane (j1), read before its
+  // visit count is known (in bounds of the row's index_width entries); the count then picks one.
+  const int nraw = p.index ? p.num[irow] : p.Nkv;
+  int j0 = 0, j1 = 0;
+  if (p.index) {
+    const int32_t* lrow = p.index + irow * p.index_width;
+    if (lane < min((int)p.index_width, 64)) j0 = lrow[lane];
+    const int lo1 = split * p.split;
+    if (split > 0 && lane < min((int)p.index_width - lo1, 64)) j1 = lrow[lo1 + lane];
+  }
   const int qi = qb * BS + w * 32 + l32;
   const bool q_ok = qi < p.Lq;
-  const bf16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
-  const bf16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
-
   // Q^T fragments (B operand): lane holds Q[qi, 16c + 8g .. +8).
   const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
   bf16x8 qf[DC];
@@ -390,6 +393,16 @@ bsa_unit_kernel(FwdParams p) {
     bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
     qf[c] = q_ok ? t : bf16x8{};
   }
+
+  const int n = p.index ? max(0, min(nraw, (int)p.index_width)) : nraw;
+  const int s_begin = split * p.split;
+  const int s_end = min(n, s_begin + p.split);
+  // A unit beyond this row's list returns; split 0 of a row with no visits runs on with an empty
+  // list and writes the empty row (zero attention).
+  if (s_begin >= s_end && (n > 0 || split > 0)) return;
+  const int ns = min((n + p.split - 1) / p.split, p.max_splits);
+  const bf16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
+  const bf16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
 
   // List entries one per lane, read once: the loop fetches them with readlane and issues no memory
   // reads besides the tile streams. A row of at most 64 visits is loaded whole and sorted by block
@@ -402,8 +415,7 @@ bsa_unit_kernel(FwdParams p) {
   const int lo = whole ? 0 : s_begin;
   const int take = whole ? n : s_end - s_begin;
   int my_j = 0;
-  if (lane < take)
-    my_j = p.index ? min(max(p.index[irow * p.index_width + lo + lane], 0), p.Nkv - 1) : lo + lane;
+  if (lane < take) my_j = p.index ? min(max(lo == 0 ? j0 : j1, 0), p.Nkv - 1) : lo + lane;
   if (whole) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
   const bool mine = whole ? lane < n && lane % ns == split : lane < take;
   const int my_real = mine ? block_real(p, my_j, BS) : 0;
