@@ -163,7 +163,13 @@ class _HSA(torch.autograd.Function):
 
         qb, kb, vb = _lib.kernel_ready(q), _lib.kernel_ready(k), _lib.kernel_ready(v)
         f32 = dict(dtype=torch.float32, device=dev)
-        sparse = torch.empty((bsz, q_len, heads, d), **f32) if plan.sparse else None
+        out = torch.empty((bsz, q_len, heads, d), dtype=comp, device=dev)
+        # Split heads (each head in one branch): a sparse head's output is its attention rounded to
+        # bf16, which the sparse kernel writes straight into `out`; that output is also the O whose
+        # row sums with dO the backward takes (as the reference's backward takes its bf16 output).
+        # Heads with both branches keep the fp32 sparse output for the fusion.
+        split = not plan.both
+        sparse = torch.empty((bsz, q_len, heads, d), **f32) if plan.sparse and not split else None
         lin = torch.empty((bsz, q_len, heads, d), **f32) if plan.linear else None
         gate = torch.empty((bsz, q_len, heads, d), **f32) if plan.linear else None
         saved = dict(plan=plan, spec=spec, modes_t=modes_t, lin_round=lin_round, comp=comp)
@@ -199,17 +205,23 @@ class _HSA(torch.autograd.Function):
                 route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st, **key_args)
                 visits = [min(ks[h], nkv) for h in plan.sparse]
             _, lse_s = bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size,
-                                   layout="blhd", heads=st, out=sparse, lq=q_len, lkv=kv_len, want_lse=True,
-                                   visits=visits)
-        out = torch.empty((bsz, q_len, heads, d), dtype=comp, device=dev)
-        fuse_forward(qb, sparse, lin, modes_t, gate, spec, out, attn_round=True, lin_round=lin_round)
+                                   layout="blhd", heads=st, out=out if split else sparse, lq=q_len, lkv=kv_len,
+                                   want_lse=True, visits=visits, attn_round_bf16=split)
+        if split:
+            if plan.linear:  # gate and gated output of the linear heads; the sparse heads are written
+                lin_modes = _lib.head_list([MODE_LINEAR if h in plan.linear else 0 for h in range(heads)], dev)
+                fuse_forward(qb, None, lin, lin_modes, gate, spec, out, attn_round=True, lin_round=lin_round)
+        else:
+            fuse_forward(qb, sparse, lin, modes_t, gate, spec, out, attn_round=True, lin_round=lin_round)
+        sparse_o = out if split else sparse  # the sparse heads' O for the backward
 
         ctx.cfg = cfg
         ctx.extra = saved
         ctx.has_coarse = k_coarse is not None
         ctx.dtypes = tuple(t.dtype if t is not None else None
                            for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b))
-        ctx.save_for_backward(q, k, v, qb, kb, vb, sparse, lin, gate, lse_s, lse_l, kc, vc, kcb, vcb, state, zsum,
+        ctx.save_for_backward(q, k, v, qb, kb, vb, sparse_o if plan.sparse else None, lin, gate, lse_s, lse_l, kc,
+                              vc, kcb, vcb, state, zsum,
                               route.index if route is not None else None,
                               route.num if route is not None else None, k_proj_mat, v_proj_mat)
         return out if out.dtype == q.dtype else out.to(q.dtype)
