@@ -124,6 +124,31 @@ def stream_time_ms(fn, iters: int, stream=None) -> float:
     return start.elapsed_time(end) / iters
 
 
+def graph_batch_ms(fn, calls: int, replays: int = 5) -> float:
+    """GPU time per call of ``fn``: ``calls`` calls captured in one HIP graph, replayed ``replays``
+    times (no per-call Python or launch latency, which exceeds the GPU time of a short launch)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / (replays * calls)
+    del graph
+    return ms
+
+
 def median_ms(fn, iters: int) -> float:
     times = []
     for _ in range(iters):
@@ -249,7 +274,8 @@ def bench_cfg2_cached_sums(args, cfg, kw, step):
 
 
 def memory_legs(cfg, plan, route, gate, dev, iters):
-    """HBM rates of the memory-bound launches of one cfg 2 call, each timed alone with HIP events:
+    """HBM rates of the memory-bound launches of one cfg 2 call, each timed alone (calls captured in
+    a HIP graph, so that the rate is the GPU's and not the Python launch rate):
     the block pooling of the routed heads' Q and K (one launch), the elu1 state pass over the
     linear heads' K and V (state + chunk reduce), and the gated elu1 readout. Bytes are the
     algorithmic ones: every input element read once, every output element written once."""
@@ -286,7 +312,7 @@ def memory_legs(cfg, plan, route, gate, dev, iters):
             ("elu1_readout", readout, 2 * lq * n_lin * d * 2 + n_lin * (d * d + d) * 4)):
         for _ in range(3):
             fn()
-        ms = stream_time_ms(fn, iters)
+        ms = graph_batch_ms(fn, iters)
         gbs = nbytes / (ms * 1e-3) / 1e9
         legs[name] = {"ms": round(ms, 4), "bytes": int(nbytes), "gb_s": round(gbs, 1),
                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
@@ -553,8 +579,12 @@ def bench_cfg5(args, dev):
 
     for _ in range(3):
         fwd_bwd()
-    step_ms = median_ms(fwd_bwd, 20)
-    fwd_ms = median_ms(fwd, 20)
+    # As for cfg 2: the step captured once in a HIP graph and replayed (the same kernels on the same
+    # inputs, without per-call Python and launch latency), the eager per-call median beside it.
+    step_eager_ms = median_ms(fwd_bwd, 20)
+    fwd_eager_ms = median_ms(fwd, 20)
+    step_ms = graph_time_ms(fwd_bwd, 3, 20)
+    fwd_ms = graph_time_ms(fwd, 3, 20)
     save = {}
     with torch.no_grad():
         g2, p2 = gate_and_proj(d, dev)
@@ -567,9 +597,13 @@ def bench_cfg5(args, dev):
     res = {"workload": "cfg5: cfg2 shapes, top-16 on 8 sparse heads + 4 elu1 heads, bf16, dO ~ N(0,1); "
                        "routing recomputed without grad; trained gate",
            "fwd_bwd_ms": round(step_ms, 4), "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(step_ms - fwd_ms, 4),
+           "fwd_bwd_ms_eager": round(step_eager_ms, 4), "fwd_ms_eager": round(fwd_eager_ms, 4),
+           "timing": "graph replay of forward + backward (and of the forward alone); *_eager: median of eager "
+                     "calls, each synchronized",
            "sparse_useful_gflop_fwd": round(useful / 1e9, 3),
            "effective_sparse_tflops_fwd_bwd": round(3.5 * useful / (step_ms * 1e-3) / 1e12, 2)}
-    log(f"cfg5: fwd+bwd {step_ms:.3f} ms (fwd {fwd_ms:.3f})")
+    log(f"cfg5: fwd+bwd {step_ms:.3f} ms (fwd {fwd_ms:.3f}; graph replay), eager {step_eager_ms:.3f} ms "
+        f"(fwd {fwd_eager_ms:.3f})")
     return res
 
 

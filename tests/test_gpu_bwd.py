@@ -253,3 +253,47 @@ def test_hsa_bf16_inputs_get_bf16_gradients_within_tolerance():
     assert kg.grad.dtype == vg.grad.dtype == torch.bfloat16
     for name, g, r in (("dq", qg.grad, qr.grad), ("dk", kg.grad, kr.grad), ("dv", vg.grad, vr.grad)):
         assert_close(g, r, what=f"bf16 {name}")
+
+
+def test_training_step_graph_replays_equal_eager_steps():
+    """Forward + backward at the cfg 5 shape captured in a HIP graph (as bench.py times the training
+    step): every replay, with eager steps and synchronizations between replays, gives the eager
+    step's gradients bit for bit."""
+    cfg = workloads.cfg5(device=DEV, seed=4)
+    d = cfg["q"].shape[-1]
+    gate = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        gate.weight.normal_(0, 0.02)
+        gate.bias.normal_(0, 0.02)
+    q, k, v = (cfg[n].detach().requires_grad_() for n in ("q", "k", "v"))
+    kw = dict(k_proj_mat=None, v_proj_mat=None, gate_lin=gate, block_size=128, routing="topk", topk=cfg["topk"],
+              head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
+    params = (q, k, v, gate.weight, gate.bias)
+
+    def step():
+        for t in params:
+            t.grad = None
+        W.hsa_attention(q, k, v, **kw).backward(cfg["do"])
+
+    step()
+    want = [t.grad.clone() for t in params]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    got = [t.grad for t in params]
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, g, w in zip(("dq", "dk", "dv", "dW", "db"), got, want):
+            assert torch.equal(g, w), f"replay {i}: {name} differs from the eager step"
+        step()                            # eager step between replays
+        torch.cuda.synchronize()
+        for name, t, w in zip(("dq", "dk", "dv", "dW", "db"), params, want):
+            assert torch.equal(t.grad, w), f"eager step after replay {i}: {name} differs"

@@ -194,19 +194,22 @@ __global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
 }
 
 // bf16 K / V: raw [64 token][D] tiles stream global -> LDS by direct-to-LDS loads into a 4-stage
-// ring, so three tiles are in flight while one is processed (the register-staged kernel above
-// keeps one). The loads are inline assembly that the compiler does not track: through the builtin
-// it made the first LDS read of every tile wait for all loads in flight (s_waitcnt vmcnt(0)),
-// which drained the ring each step; the waits below count the loads instead. Per tile: wait for it, issue the tile three ahead into the stage freed by the
-// previous one, apply phi in place (each thread owns a fixed 8-channel column, so it also sums z),
-// then the same MFMAs. Rows past the chunk re-read an in-bounds row and get phi = 0, so they add
-// nothing to S or z.
-// Output tile (dt, et) of S^T (NT x NT tiles of 32 x 32) for the i-th of a wave's TPW tiles: waves
-// take consecutive runs of TPW tiles in row-major tile order.
+// ring. The loads are inline assembly that the compiler does not track: through the builtin it
+// made the first LDS read of every tile wait for all loads in flight (s_waitcnt vmcnt(0)), which
+// drained the ring each step; the waits below count the loads instead. The loop is software
+// pipelined over tiles: while the MFMAs of tile `it` read its stage, the same waves apply phi in
+// place to the K rows of tile it + 1 (each thread owns a fixed 8-channel column, so it also sums
+// z), and tiles it + 2 and it + 3 stream in. One barrier per tile: it publishes the phi writes of
+// tile it + 1 and frees the stage that tile it + 4 streams into. (With phi and the products in
+// separate phases, every wave ran its VALU work and then its MFMAs between two barriers, and the
+// kernel ran at half the rate of the same ring without compute.) Rows past the chunk read zeros
+// and get phi = 0, so they add nothing to S or z.
+// Output tiles (dt, et) of S^T (NT x NT tiles of 32 x 32): wave w owns the TPW tiles of column et
+// = w % NT in rows (w / NT) TPW + i, so its products share one phi(K) fragment per 16 tokens.
 template <int NT, int TPW>
-__device__ __forceinline__ int tile_d(int w, int i) { return (w * TPW + i) / NT; }
+__device__ __forceinline__ int tile_d(int w, int i) { return (w / NT) * TPW + i; }
 template <int NT, int TPW>
-__device__ __forceinline__ int tile_e(int w, int i) { return (w * TPW + i) % NT; }
+__device__ __forceinline__ int tile_e(int w, int) { return w % NT; }
 
 template <int D, int NW>
 __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) {
@@ -216,7 +219,7 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
   constexpr int NI = TC / (RPI * NW);     // DMA instructions per wave per tensor per tile
   constexpr int UPT = TC * CPR / NTH;     // chunks per thread in the phi pass
   constexpr int NT = D / 32, TPW = NT * NT / NW;
-  static_assert(NI >= 1 && UPT >= 1 && TPW >= 1 && NT * NT == TPW * NW, "bad wave count");
+  static_assert(NI >= 1 && UPT >= 1 && TPW >= 1 && NT * NT == TPW * NW && NW % NT == 0, "bad wave count");
   __shared__ __attribute__((aligned(1024))) bf16_t kb[STAGES][TC * D];
   __shared__ __attribute__((aligned(1024))) bf16_t vb[STAGES][TC * D];
 
@@ -230,16 +233,27 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
   const bf16_t* kbase = (const bf16_t*)p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16_t* vbase = (const bf16_t*)p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
 
+  // Tile loads through one buffer descriptor per tile and tensor (scalar work only), starting at
+  // the tile's first row and ending at the chunk's last row, so rows past the chunk read zeros;
+  // this lane's byte offsets within a tile are loop-invariant.
+  int k_off[NI], v_off[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = (i * NW + w) * RPI + lane / CPR, cc = (lane % CPR) ^ tr_swizzle(row);
+    k_off[i] = (int)(row * p.k_st + cc * 8) * 2;
+    v_off[i] = (int)(row * p.v_st + cc * 8) * 2;
+  }
   auto issue = [&](int it) {
-    const int t0 = tbeg + it * TC, st = it % STAGES;
+    const int t0 = tbeg + it * TC, st = it % STAGES, rows = min(TC, tend - t0);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kbase + (int64_t)t0 * p.k_st), (short)0, (int)((rows - 1) * p.k_st + D) * 2, WA_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vbase + (int64_t)t0 * p.v_st), (short)0, (int)((rows - 1) * p.v_st + D) * 2, WA_BUF_DWORD3);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int r0 = (i * NW + w) * RPI;
-      const int row = r0 + lane / CPR;
-      const int src = t0 + row < tend ? t0 + row : t0;
-      const int cc = (lane % CPR) ^ tr_swizzle(row);
-      lds_dma16_global(kbase + (int64_t)src * p.k_st + cc * 8, &kb[st][r0 * D]);
-      lds_dma16_global(vbase + (int64_t)src * p.v_st + cc * 8, &vb[st][r0 * D]);
+      lds_dma16(krs, &kb[st][r0 * D], k_off[i]);
+      lds_dma16(vrs, &vb[st][r0 * D], v_off[i]);
     }
   };
 
@@ -251,40 +265,63 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
   for (int e = 0; e < 8; ++e) zacc[e] = 0.f;
   const int c8 = tid % CPR;  // this thread's channel chunk in the phi pass
 
-  for (int it = 0; it < min(ntiles, STAGES - 1); ++it) issue(it);
-  for (int it = 0; it < ntiles; ++it) {
-    const int ahead = min(STAGES - 2, ntiles - 1 - it);  // tiles after `it` already issued
-    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * NI) : "memory");
-    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);  // into the stage of tile it - 1
-    const int st = it % STAGES, t0 = tbeg + it * TC;
-    bf16_t* kt = kb[st];
+  // phi in place on the K rows of tile `it` (zero past the chunk), summed into z
+  auto phi = [&](int it) {
+    const int t0 = tbeg + it * TC;
+    bf16_t* kt = kb[it % STAGES];
+    bf16x8 x[UPT];
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int r = tid / CPR + u * (NTH / CPR);
-      const bool ok = t0 + r < tend;
-      bf16x8* cp = (bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8));
-      bf16x8 x = *cp;
+      x[u] = *(const bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8));
+    }
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int r = tid / CPR + u * (NTH / CPR);
+      // a row past the chunk becomes -inf, whose phi is exp(-inf) = 0 (a select, where a
+      // conditional phi compiled to one branch per element)
+      if (t0 + r >= tend) x[u] = __builtin_bit_cast(bf16x8, u32x4{0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u});
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float ph = ok ? wa_bf16_round(elu1f((float)x[e])) : 0.f;
+        const float ph = wa_bf16_round(elu1f((float)x[u][e]));
         zacc[e] += ph;
-        x[e] = (bf16_t)ph;
+        x[u][e] = (bf16_t)ph;
       }
-      *cp = x;
+      *(bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8)) = x[u];
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  // S^T tiles += V^T phi(K) over the 64 tokens of tile `it`
+  auto products = [&](int it) {
+    const int st = it % STAGES, et = tile_e<NT, TPW>(w, 0);
 #pragma unroll
     for (int c = 0; c < TC / 16; ++c) {
+      const bf16x8 bb = tr_frag<D>(kb[st], c, 32 * et, lane);
 #pragma unroll
       for (int i = 0; i < TPW; ++i) {
-        const int dt = tile_d<NT, TPW>(w, i), et = tile_e<NT, TPW>(w, i);
-        const bf16x8 a = tr_frag<D>(vb[st], c, 32 * dt, lane);
-        const bf16x8 bb = tr_frag<D>(kb[st], c, 32 * et, lane);
+        const bf16x8 a = tr_frag<D>(vb[st], c, 32 * tile_d<NT, TPW>(w, i), lane);
         acc[i] = wa_mfma32(a, bb, acc[i]);
       }
     }
+  };
+
+  for (int it = 0; it < min(ntiles, STAGES - 1); ++it) issue(it);
+  if (ntiles > 0) {
+    // tile 0 landed (tiles 1 and 2 may still stream)
+    if (ntiles >= 3) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * NI) : "memory");
+    else if (ntiles == 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    phi(0);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    // Issued so far: tiles up to it + 2. Tile it + 1 must have landed (tile it + 2 may stream),
+    // and every wave's phi writes of tile it and products of tile it - 1 be done.
+    if (it + 2 < ntiles) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);  // into the stage of tile it - 1
+    products(it);
+    // after the last tile every row is past the chunk: phi writes zeros into a stage nothing
+    // reads again and adds zero to z (unconditional, so one basic block holds both)
+    phi(it + 1);
   }
 
   float* part = p.part + (((int64_t)chunk * p.B + b) * p.n_heads + hs) * (int64_t)(D * D + D);
@@ -312,29 +349,38 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
   }
 }
 
+// Sum of the chunk partials, four bytes-in-flight-heavy waves per 64 float4 positions: wave q sums
+// the chunks of quarter q (up to 8 float4 loads in flight per lane), then wave 0 adds the four
+// quarter sums, always in the same order (bitwise reproducible).
 __global__ void __launch_bounds__(256) elu1_reduce_kernel(StateParams p, int D) {
-  const int64_t per = (int64_t)D * D + D;
+  __shared__ f32x4 qsum[4][64];
+  const int64_t per = (int64_t)D * D + D;  // a multiple of 4: no float4 straddles S^T and z
   const int64_t total = (int64_t)p.B * p.n_heads * per;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  // 16 loads in flight per thread, summed into 8 chains (fixed order: reproducible)
-  float a[8];
+  const int64_t i4 = (int64_t)blockIdx.x * 64 + (threadIdx.x & 63);
+  const int q = threadIdx.x >> 6;
+  const int c0 = (int)((int64_t)p.n_chunks * q / 4), c1 = (int)((int64_t)p.n_chunks * (q + 1) / 4);
+  f32x4 a = {0.f, 0.f, 0.f, 0.f};
+  if (i4 * 4 < total) {
+    const f32x4* src = (const f32x4*)p.part + i4;
+    const int64_t stride = total / 4;
+    int c = c0;
+    for (; c + 8 <= c1; c += 8) {
+      f32x4 v[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) a[j] = 0.f;
-  const float* src = p.part + i;
-  int c = 0;
-  for (; c + 16 <= p.n_chunks; c += 16) {
-    float v[16];
+      for (int j = 0; j < 8; ++j) v[j] = src[(int64_t)(c + j) * stride];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = src[(int64_t)(c + j) * total];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) a[j & 7] += v[j];
+      for (int j = 0; j < 8; ++j) a += v[j];
+    }
+    for (; c < c1; ++c) a += src[(int64_t)c * stride];
   }
-  for (; c < p.n_chunks; ++c) a[0] += src[(int64_t)c * total];
-  const float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-  const int64_t bh = i / per, r = i % per;
-  if (r < (int64_t)D * D) p.state[bh * D * D + r] = s;
-  else p.zsum[bh * D + (r - (int64_t)D * D)] = s;
+  qsum[q][threadIdx.x & 63] = a;
+  __syncthreads();
+  if (q != 0 || i4 * 4 >= total) return;
+  const f32x4 s = (qsum[0][threadIdx.x] + qsum[1][threadIdx.x]) + (qsum[2][threadIdx.x] + qsum[3][threadIdx.x]);
+  const int64_t bh = i4 * 4 / per, r = i4 * 4 % per;
+  float* dst = r < (int64_t)D * D ? p.state + bh * D * D + r : p.zsum + bh * D + (r - (int64_t)D * D);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = s[e];
 }
 
 // =============================================================================================
@@ -945,6 +991,8 @@ extern "C" int wa_elu1_state(const wa_elu1_state_args* a, void* stream) {
   WA_CHECK_ARG(wa_aligned16(a->k) && wa_aligned16(a->v) && a->k_sb % vec == 0 && a->k_st % vec == 0 &&
                    a->k_sh % vec == 0 && a->v_sb % vec == 0 && a->v_st % vec == 0 && a->v_sh % vec == 0,
                "wa_elu1_state: k/v must be 16-byte aligned with 16-byte aligned rows");
+  WA_CHECK_ARG(a->L == 1 || (a->k_st >= a->D && a->v_st >= a->D && a->k_st < (1 << 24) && a->v_st < (1 << 24)),
+               "wa_elu1_state: token strides must be at least D and below 2^24 elements");
   const int64_t nh = a->heads ? a->n_heads : a->H;
   if (a->B == 0 || nh == 0) return WA_OK;
   StateParams sp{};
@@ -966,8 +1014,8 @@ extern "C" int wa_elu1_state(const wa_elu1_state_args* a, void* stream) {
   }
   int rc = wa_launch_status("elu1_state");
   if (rc != WA_OK) return rc;
-  const int64_t total = a->B * nh * (a->D * a->D + a->D);
-  hipLaunchKernelGGL(elu1_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, sp, (int)a->D);
+  const int64_t total4 = a->B * nh * (a->D * a->D + a->D) / 4;
+  hipLaunchKernelGGL(elu1_reduce_kernel, dim3((unsigned)((total4 + 63) / 64)), dim3(256), 0, s, sp, (int)a->D);
   return wa_launch_status("elu1_reduce");
 }
 
