@@ -198,12 +198,11 @@ __global__ void __launch_bounds__(256) elu1_state_kernel(StateParams p) {
 // made the first LDS read of every tile wait for all loads in flight (s_waitcnt vmcnt(0)), which
 // drained the ring each step; the waits below count the loads instead. The loop is software
 // pipelined over tiles: while the MFMAs of tile `it` read its stage, the same waves apply phi in
-// place to the K rows of tile it + 1 (each thread owns a fixed 8-channel column, so it also sums
-// z), and tiles it + 2 and it + 3 stream in. One barrier per tile: it publishes the phi writes of
-// tile it + 1 and frees the stage that tile it + 4 streams into. (With phi and the products in
-// separate phases, every wave ran its VALU work and then its MFMAs between two barriers, and the
-// kernel ran at half the rate of the same ring without compute.) Rows past the chunk read zeros
-// and get phi = 0, so they add nothing to S or z.
+// place to the K rows of tile it + 1, and tiles it + 2 and it + 3 stream in. One barrier per tile:
+// it publishes the phi writes of tile it + 1 and frees the stage that tile it + 4 streams into.
+// Most of the loop's VALU instructions are phi's (~8 per element), so z is summed on the MFMA pipe
+// as a product with a ones row rather than by the phi pass. Rows past the chunk read
+// zeros and get phi = 0 (as -inf), so they add nothing to S or z.
 // Output tiles (dt, et) of S^T (NT x NT tiles of 32 x 32): wave w owns the TPW tiles of column et
 // = w % NT in rows (w / NT) TPW + i, so its products share one phi(K) fragment per 16 tokens.
 template <int NT, int TPW>
@@ -260,12 +259,14 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
   f32x16 acc[TPW];
 #pragma unroll
   for (int i = 0; i < TPW; ++i) acc[i] = f32x16{};
-  float zacc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) zacc[e] = 0.f;
+  // z = ones^T phi(K) on the MFMA pipe: every row of zt holds z over the wave's column tile (the
+  // NW / NT waves of a column tile each sum all of it: no branch between the products; the first
+  // one's is kept).
+  f32x16 zt = f32x16{};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
   const int c8 = tid % CPR;  // this thread's channel chunk in the phi pass
 
-  // phi in place on the K rows of tile `it` (zero past the chunk), summed into z
+  // phi in place on the K rows of tile `it` (zero past the chunk)
   auto phi = [&](int it) {
     const int t0 = tbeg + it * TC;
     bf16_t* kt = kb[it % STAGES];
@@ -278,15 +279,15 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
       const int r = tid / CPR + u * (NTH / CPR);
-      // a row past the chunk becomes -inf, whose phi is exp(-inf) = 0 (a select, where a
-      // conditional phi compiled to one branch per element)
-      if (t0 + r >= tend) x[u] = __builtin_bit_cast(bf16x8, u32x4{0xff80ff80u, 0xff80ff80u, 0xff80ff80u, 0xff80ff80u});
+      // a row past the chunk becomes -inf, whose phi is exp(-inf) = 0 (a bitwise blend: a
+      // conditional phi, or a conditional assignment, compiled to branches)
+      const unsigned past = 0u - (unsigned)(t0 + r >= tend);
+      u32x4 xw = __builtin_bit_cast(u32x4, x[u]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float ph = wa_bf16_round(elu1f((float)x[u][e]));
-        zacc[e] += ph;
-        x[u][e] = (bf16_t)ph;
-      }
+      for (int j = 0; j < 4; ++j) xw[j] = (xw[j] & ~past) | (0xff80ff80u & past);
+      x[u] = __builtin_bit_cast(bf16x8, xw);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[u][e] = (bf16_t)elu1f((float)x[u][e]);
       *(bf16x8*)(kt + r * D + ((c8 ^ tr_swizzle(r)) * 8)) = x[u];
     }
   };
@@ -301,15 +302,17 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
         const bf16x8 a = tr_frag<D>(vb[st], c, 32 * tile_d<NT, TPW>(w, i), lane);
         acc[i] = wa_mfma32(a, bb, acc[i]);
       }
+      zt = wa_mfma32(ones, bb, zt);
     }
   };
 
-  for (int it = 0; it < min(ntiles, STAGES - 1); ++it) issue(it);
+  // Tiles 0 and 1 first, tile 2 once tile 0 has landed: with every workgroup of the launch
+  // starting at once, a smaller first burst brings tile 0 in sooner.
+  for (int it = 0; it < min(ntiles, 2); ++it) issue(it);
   if (ntiles > 0) {
-    // tile 0 landed (tiles 1 and 2 may still stream)
-    if (ntiles >= 3) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(4 * NI) : "memory");
-    else if (ntiles == 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
+    if (ntiles >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (ntiles > 2) issue(2);
     phi(0);
   }
   for (int it = 0; it < ntiles; ++it) {
@@ -320,7 +323,7 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
     if (it + STAGES - 1 < ntiles) issue(it + STAGES - 1);  // into the stage of tile it - 1
     products(it);
     // after the last tile every row is past the chunk: phi writes zeros into a stage nothing
-    // reads again and adds zero to z (unconditional, so one basic block holds both)
+    // reads again (unconditional, so one basic block holds both)
     phi(it + 1);
   }
 
@@ -335,18 +338,8 @@ __global__ void __launch_bounds__(64 * NW) elu1_state_dma_kernel(StateParams p) 
       part[d * D + 32 * et + l32] = acc[i][r];
     }
   }
-  __syncthreads();
-  static_assert(NTH * 8 * 4 <= STAGES * TC * D * 2, "z staging exceeds the K ring");
-  float* zbuf = (float*)kb[0];  // [NTH threads][8], over the drained K ring
-#pragma unroll
-  for (int e = 0; e < 8; ++e) zbuf[tid * 8 + e] = zacc[e];
-  __syncthreads();
-  if (tid < D) {
-    const int cc = tid / 8, e = tid % 8;
-    float sum = 0.f;
-    for (int r = 0; r < NTH / CPR; ++r) sum += zbuf[(r * CPR + cc) * 8 + e];
-    part[D * D + tid] = sum;
-  }
+  // z over column tile w: row 0 of zt (lanes 0..31)
+  if (w < NT && g == 0) part[D * D + 32 * w + l32] = zt[0];
 }
 
 // Sum of the chunk partials, four bytes-in-flight-heavy waves per 64 float4 positions: wave q sums
