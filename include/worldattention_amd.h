@@ -202,6 +202,8 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * Query block i (block_size rows) attends to key blocks index[b,h,i,0:num[b,h,i]] (ids clamped
  * to [0, Nkv-1]); key tokens past min(block_sizes[j], Lkv - j*block_size) are masked; a row with
  * num = 0 yields 0 (and lse = -inf). index == NULL selects every key block (dense attention).
+ * heads (optional): device int32[n_heads], the heads to attend (head slots 0 .. n_heads - 1);
+ * NULL with n_heads = 0 = all H heads (NULL with n_heads > 0 is an error).
  * lse (optional): [B, H, Lq] natural-log log-sum-exp of the scaled logits.
  * Epilogue (per element, gate g = sigmoid(q . gate_w[d] + gate_b[d]) or sigmoid(q) when gate_w
  * is NULL, optionally rounded to bf16 before/after the sigmoid):

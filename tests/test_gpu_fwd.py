@@ -242,6 +242,30 @@ def test_elu1_linear_branch_matches_oracle(d, dtype):
     assert torch.count_nonzero(out[:, :, 1]) == 0
 
 
+def test_empty_head_lists_launch_nothing():
+    """An empty head list writes nothing (the library reads a missing list as every head, so the
+    wrappers never pass an empty one down)."""
+    from worldattention_amd.hsa._bwd import bsa_backward
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(5)
+    b, h, lq, lkv, d = 1, 3, 300, 700, 128
+    q, k, v = (torch.randn(b, n, h, d, device=DEV).bfloat16() for n in (lq, lkv, lkv))
+    empty = torch.zeros(0, dtype=torch.int32, device=DEV)
+    out, _ = bsa_forward(q, k, v, index=None, num=None, block_size=128, layout="blhd", heads=empty,
+                         out=torch.zeros(b, lq, h, d, dtype=torch.bfloat16, device=DEV))
+    assert torch.count_nonzero(out) == 0
+    s, z = WA.elu1_state(k, v, empty)
+    assert s.shape == (b, 0, d, d) and z.shape == (b, 0, d)
+    o2 = torch.zeros(b, lq, h, d, device=DEV)
+    WA.elu1_readout(q, s, z, empty, o2)
+    assert torch.count_nonzero(o2) == 0
+    lse = torch.zeros(b, h, lq, device=DEV)
+    dq, dk, dv = bsa_backward(q, k, v, o2, lse, o2, index=None, num=None, block_size=128, layout="blhd",
+                              heads=empty, dq=torch.zeros(b, lq, h, d, device=DEV),
+                              dk=torch.zeros(b, lkv, h, d, device=DEV), dv=torch.zeros(b, lkv, h, d, device=DEV))
+    assert not dq.any() and not dk.any() and not dv.any()
+
+
 # ----------------------------------------------------------------------------------------------
 # hsa_attention end to end
 # ----------------------------------------------------------------------------------------------

@@ -119,3 +119,14 @@ def test_gate_kernel_copies_follow_the_parameter_object():
     with torch.no_grad():
         a.weight.add_(1.0)
     assert torch.equal(GateSpec(a, torch.float32).w.float(), a.weight.detach().bfloat16().float())
+
+
+def test_empty_head_lists_are_refused_at_the_c_boundary():
+    """A missing head list means every head to the library, so an empty one (whose data pointer
+    can be NULL) is refused before any call; a list of heads passes through."""
+    from worldattention_amd import _lib
+    with pytest.raises(ValueError, match="empty head list"):
+        _lib.heads_arg(torch.zeros(0, dtype=torch.int32))
+    assert _lib.heads_arg(None) == (None, 0)
+    t = torch.tensor([1, 3], dtype=torch.int32)
+    assert _lib.heads_arg(t) == (t.data_ptr(), 2)

@@ -340,6 +340,17 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def heads_arg(t):
+    """``(pointer, count)`` of an optional device head list for the C ABI, where NULL means every
+    head. An empty list is refused: its data pointer can be NULL, which the library would read as
+    every head while the caller's outputs hold none."""
+    if t is None:
+        return None, 0
+    if t.numel() == 0:
+        raise ValueError("empty head list (the library reads a missing list as every head): skip the call")
+    return t.data_ptr(), t.numel()
+
+
 def blhd(t: torch.Tensor):
     """(ptr, sb, st, sh) of a [B, L, H, C] tensor whose channel dim is contiguous."""
     if t.stride(-1) != 1:

@@ -139,17 +139,21 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
                                              const bf16x8 (&qf)[D / 16], const bf16_t* qrow, int b, int h,
                                              int qi, bool q_ok, int g, int l32) {
   constexpr int DC = D / 16, DT = D / 32;
-  const bool need_gate = p.epilogue != WA_EPI_PLAIN;
+  const int epilogue = p.epilogue;
+  const bool need_gate = epilogue != WA_EPI_PLAIN;
   f32x16 gacc[DT];
   if (need_gate && p.gate_w) {
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
+      // the tile's gate rows in one round trip (left to itself the scheduler waited for each)
+      bf16x8 a[DC];
+#pragma unroll
+      for (int c = 0; c < DC; ++c) a[c] = *(const bf16x8*)(p.gate_w + (t * 32 + l32) * D + c * 16 + g * 8);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(a[c]));
       gacc[t] = f32x16{};
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        const bf16x8 a = *(const bf16x8*)(p.gate_w + (t * 32 + l32) * D + c * 16 + g * 8);
-        gacc[t] = wa_mfma32(a, qf[c], gacc[t]);
-      }
+      for (int c = 0; c < DC; ++c) gacc[t] = wa_mfma32(a[c], qf[c], gacc[t]);
     }
   }
   if (!q_ok) return;
@@ -162,14 +166,42 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
   for (int t = 0; t < DT; ++t) {
     float pre[4][4], xv[4][4];
     if (need_gate) {
+      // The options branch around whole tiles and the tile's loads are all issued before the first
+      // use (with the options tested per element, every element waited for its own load).
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
         const int d0 = t * 32 + 8 * rq + 4 * g;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pre[rq][i] = p.gate_w ? gacc[t][rq * 4 + i] + (p.gate_b ? p.gate_b[d0 + i] : 0.f) : (float)qrow[d0 + i];
-          xv[rq][i] = p.epilogue == WA_EPI_FUSE ? wa_load_f(p.x, xo + d0 + i, p.x_dtype) : 0.f;
+          if (p.gate_w) pre[rq][i] = p.gate_b ? p.gate_b[d0 + i] : 0.f;
+          else pre[rq][i] = (float)qrow[d0 + i];
         }
+      }
+      if (epilogue == WA_EPI_FUSE && p.x_dtype == WA_BF16) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xv[rq][i] = (float)((const bf16_t*)p.x)[xo + t * 32 + 8 * rq + 4 * g + i];
+      } else if (epilogue == WA_EPI_FUSE) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xv[rq][i] = ((const float*)p.x)[xo + t * 32 + 8 * rq + 4 * g + i];
+      } else {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) xv[rq][i] = 0.f;
+      }
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(pre[rq][i]), "+v"(xv[rq][i]));
+      if (p.gate_w) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) pre[rq][i] = gacc[t][rq * 4 + i] + pre[rq][i];
       }
     }
 #pragma unroll
@@ -185,7 +217,7 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
           if (p.gate_pre_bf16) pr = wa_bf16_round(pr);
           float gs = wa_sigmoid(pr);
           if (p.gate_out_bf16) gs = wa_bf16_round(gs);
-          a = p.epilogue == WA_EPI_FUSE ? wa_add_rn(a, wa_mul_rn(xv[rq][i], gs)) : wa_mul_rn(a, gs);
+          a = epilogue == WA_EPI_FUSE ? wa_add_rn(a, wa_mul_rn(xv[rq][i], gs)) : wa_mul_rn(a, gs);
         }
         val[i] = a;
       }
@@ -823,6 +855,8 @@ int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream) {
   if (a->index) WA_CHECK_ARG(a->num && a->index_width > 0, "wa_bsa_fwd: index needs num and width");
   const int64_t nq = (a->Lq + a->block_size - 1) / a->block_size;
   const int64_t nkv = (a->Lkv + a->block_size - 1) / a->block_size;
+  WA_CHECK_ARG(a->heads != nullptr || a->n_heads == 0, "wa_bsa_fwd: n_heads = %lld without a heads list",
+               (long long)a->n_heads);
   const int64_t nh = a->heads ? a->n_heads : a->H;
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_fwd: bad head count");
   const int64_t rows = a->B * nh * nq;

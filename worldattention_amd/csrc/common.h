@@ -49,6 +49,10 @@ static inline bool wa_aligned16(const void* p) { return (((uintptr_t)p) & 15u) =
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ float wa_bf16_round(float x) { return (float)(bf16_t)x; }
 
+// The linear heads' feature map phi(x) = elu(x) + 1 (one definition for every kernel that forms it,
+// so that they agree bit for bit).
+__device__ __forceinline__ float elu1f(float x) { return x > 0.f ? x + 1.f : __expf(x); }
+
 // Single-rounding fp32 operations that the compiler may not fuse with a neighbouring multiply or
 // add: HIP's __fadd_rn / __fmul_rn are plain operators, which the default -ffp-contract=fast turns
 // into fused multiply-adds (one rounding instead of two). Used where results must round as the

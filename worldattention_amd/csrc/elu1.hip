@@ -18,8 +18,6 @@ namespace {
 typedef wa_s16x4 s16x4;
 #define WA_LDS4(p) WA_LDS_S16X4(p)
 
-__device__ __forceinline__ float elu1f(float x) { return x > 0.f ? x + 1.f : __expf(x); }
-
 // Row swizzles of 16-byte chunks (see bsa_fwd.hip): transpose reads cover 4 rows x 32 bytes per
 // 16 lanes; 128-bit reads cover 16 rows x 16 bytes.
 __device__ __forceinline__ int tr_swizzle(int r) { return 2 * (r & 3); }

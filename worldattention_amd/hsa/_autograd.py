@@ -69,6 +69,8 @@ def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumul
     """Adds the elu(x)+1 branch's gradients into fp32 ``dq``, ``dk``, ``dv`` (``wa_elu1_bwd``); with
     an ``*_accumulate`` flag off the gradient is written instead (then ``dk`` / ``dv`` may be bf16)."""
     dev = _lib.require_gpu(q, k, v, dout)
+    if heads_t.numel() == 0:
+        return
     if k.dtype != v.dtype:
         v = v.to(k.dtype)
     q = q if q.stride(-1) == 1 else q.contiguous()
@@ -82,7 +84,7 @@ def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumul
         *_lib.blhd(q), _lib.dtype_code(q), *_lib.blhd(k), *_lib.blhd(v), _lib.dtype_code(k),
         *_lib.blhd(dout), _lib.dtype_code(dout), state.data_ptr(), zsum.data_ptr(),
         *_lib.blhd(dq), int(dq_accumulate), *_lib.blhd(dk), int(kv_accumulate), *_lib.blhd(dv), int(kv_accumulate),
-        heads_t.data_ptr(), n, bsz, heads, lq, lkv, d, ws.data_ptr(), _lib.dtype_code(dk))
+        *_lib.heads_arg(heads_t), bsz, heads, lq, lkv, d, ws.data_ptr(), _lib.dtype_code(dk))
     _lib.call("wa_elu1_bwd", args, _lib.stream_ptr(dev))
 
 

@@ -42,6 +42,8 @@ def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_s
         raise ValueError("bf16 dk / dv are written, not accumulated")
     grad_out = grad_out if grad_out.stride(-1) == 1 else grad_out.contiguous()
     n_slots = heads.numel() if heads is not None else nheads
+    if n_slots == 0:
+        return dq, dk, dv
     ws = torch.empty((_lib.lib().wa_bsa_bwd_workspace_bytes(bsz, n_slots, lq, lkv, d, block_size),),
                      dtype=torch.uint8, device=dev)
     width = index.shape[-1] if index is not None else 0
@@ -50,7 +52,7 @@ def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_s
         *strides(out), _lib.dtype_code(out),
         *strides(grad_out), _lib.dtype_code(grad_out),
         lse.data_ptr(), _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
-        _lib.ptr(heads), n_slots if heads is not None else 0,
+        *_lib.heads_arg(heads),
         bsz, nheads, lq, lkv, d, block_size, 0.0,
         *strides(dq), int(accumulate), *strides(dk), int(accumulate), *strides(dv), int(accumulate),
         ws.data_ptr(), _lib.dtype_code(dk))

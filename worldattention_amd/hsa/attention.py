@@ -197,11 +197,13 @@ def elu1_state(k: torch.Tensor, v: torch.Tensor, heads_t: torch.Tensor):
     n = heads_t.numel()
     state = torch.empty((bsz, n, d, d), dtype=torch.float32, device=dev)
     zsum = torch.empty((bsz, n, d), dtype=torch.float32, device=dev)
+    if n == 0:
+        return state, zsum
     ws = torch.empty((_lib.lib().wa_elu1_state_workspace_bytes(bsz, n, length, d),), dtype=torch.uint8, device=dev)
     kp, k_sb, k_st, k_sh = _lib.blhd(k)
     vp, v_sb, v_st, v_sh = _lib.blhd(v)
     args = _lib.Elu1StateArgs(kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh, _lib.dtype_code(k), bsz, heads, length, d,
-                              heads_t.data_ptr(), n, state.data_ptr(), zsum.data_ptr(), ws.data_ptr())
+                              *_lib.heads_arg(heads_t), state.data_ptr(), zsum.data_ptr(), ws.data_ptr())
     _lib.call("wa_elu1_state", args, _lib.stream_ptr(dev))
     return state, zsum
 
@@ -209,6 +211,8 @@ def elu1_state(k: torch.Tensor, v: torch.Tensor, heads_t: torch.Tensor):
 def elu1_readout(q, state, zsum, heads_t, out, *, epilogue=_lib.WA_EPI_PLAIN, gate_w=None, gate_b=None,
                  gate_pre_bf16=False, gate_out_bf16=False, lin_round_bf16=False):
     dev = _lib.require_gpu(q, state, out)
+    if heads_t.numel() == 0:
+        return out
     q = q if q.dtype in (torch.float32, torch.bfloat16) else q.float()
     q = q if q.stride(-1) == 1 else q.contiguous()
     bsz, length, heads, d = q.shape
@@ -216,7 +220,7 @@ def elu1_readout(q, state, zsum, heads_t, out, *, epilogue=_lib.WA_EPI_PLAIN, ga
     op, o_sb, o_st, o_sh = _lib.blhd(out)
     args = _lib.Elu1ReadoutArgs(qp, q_sb, q_st, q_sh, _lib.dtype_code(q), state.data_ptr(), zsum.data_ptr(),
                                 op, o_sb, o_st, o_sh, _lib.dtype_code(out), bsz, heads, length, d,
-                                heads_t.data_ptr(), heads_t.numel(), epilogue, _lib.ptr(gate_w), _lib.ptr(gate_b),
+                                *_lib.heads_arg(heads_t), epilogue, _lib.ptr(gate_w), _lib.ptr(gate_b),
                                 int(gate_pre_bf16), int(gate_out_bf16), int(lin_round_bf16))
     _lib.call("wa_elu1_readout", args, _lib.stream_ptr(dev))
     return out

@@ -71,8 +71,8 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
     then covers exactly the needed (row, split) units. ``arrivals`` (optional): an int32 tensor of
     at least ``B * n_heads * ceil(lq / block_size)`` zeros (left zero), which spares the launch
     clearing its own. ``noalloc``: launch ``wa_bsa_fwd_noalloc`` instead, whose workspace is the
-    library's static device array (no workspace tensor; ``arrivals`` must be None). Returns
-    ``(out, lse)``.
+    library's static device array (no workspace tensor; ``arrivals`` must be None). An empty
+    ``heads`` list launches nothing. Returns ``(out, lse)``.
     """
     dev = _lib.require_gpu(q, k, v)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -101,6 +101,8 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
     nq = -(-lq // block_size)
     width = index.shape[-1] if index is not None else nkv
     n_slots = heads.numel() if heads is not None else nheads
+    if n_slots == 0:
+        return out, lse
     split = int(split or _lib.BSA_DEFAULT_SPLIT)
     units, n_units, max_visits = None, 0, width
     if visits is not None:
@@ -124,7 +126,7 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         qp, q_sb, q_st, q_sh, kp, k_sb, k_st, k_sh, vp, v_sb, v_st, v_sh,
         op, o_sb, o_st, o_sh, _lib.dtype_code(out), _lib.ptr(lse),
         _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
-        _lib.ptr(heads), n_slots if heads is not None else 0,
+        *_lib.heads_arg(heads),
         bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
         xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
         int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16),

@@ -113,8 +113,7 @@ def kv_append(kv_cache: dict, k_new: torch.Tensor, v_new: torch.Tensor, *, write
     ck, cv, nk, nv = _lib.blhd(kc), _lib.blhd(vc), _lib.blhd(k_src), _lib.blhd(v_src)
     args = _lib.KvAppendArgs(ck[0], ck[1], ck[2], ck[3], cv[0], cv[1], cv[2], cv[3],
                              nk[0], nk[1], nk[2], nk[3], nv[0], nv[1], nv[2], nv[3], _lib.dtype_code(kc),
-                             bsz, cap, heads_n, d, start, n, _lib.ptr(sums), bs, _lib.ptr(heads_t),
-                             0 if heads_t is None else heads_t.numel())
+                             bsz, cap, heads_n, d, start, n, _lib.ptr(sums), bs, *_lib.heads_arg(heads_t))
     _lib.call("wa_kv_append", args, _lib.stream_ptr(dev))
 
     new_kc = new_vc = None
@@ -236,8 +235,7 @@ def kv_roll(kv_cache: dict, *, sink_tokens: int, num_evicted: int, num_rolled: i
     kcp = _lib.blhd(kcc) if coarse else (None, 0, 0, 0)
     vcp = _lib.blhd(vcc) if coarse else (None, 0, 0, 0)
     args = _lib.KvRollArgs(*kp, *vp, _lib.dtype_code(kc), bsz, cap, heads_n, d, int(sink_tokens), int(num_evicted),
-                           int(num_rolled), _lib.ptr(sums), int(block_size or 0), _lib.ptr(heads_t),
-                           0 if heads_t is None else heads_t.numel(), *kcp, *vcp,
+                           int(num_rolled), _lib.ptr(sums), int(block_size or 0), *_lib.heads_arg(heads_t), *kcp, *vcp,
                            kcc.shape[1] if coarse else 0, c_dst, c_src, c_rows)
     _lib.call("wa_kv_roll", args, _lib.stream_ptr(dev))
 

@@ -86,7 +86,7 @@ def pool_blhd(x: torch.Tensor, logical_len: int, num_blocks: int, block_size: in
         out = torch.empty((b, h, num_blocks, d), dtype=torch.float32, device=dev)
     p, sb, st, sh = _lib.blhd(x)
     args = _lib.PoolArgs(p, sb, st, sh, _lib.dtype_code(x), b, logical_len, h, d, block_size, num_blocks,
-                         _lib.ptr(heads), 0 if heads is None else heads.numel(), out.data_ptr(), int(emulate))
+                         *_lib.heads_arg(heads), out.data_ptr(), int(emulate))
     _lib.call("wa_block_mean_pool", args, _lib.stream_ptr(dev))
     return out
 
@@ -107,7 +107,7 @@ def pool_blhd_many(jobs, block_size: int, heads: Optional[torch.Tensor] = None, 
         out = torch.empty((b, h, num_blocks, d), dtype=torch.float32, device=dev)
         p, sb, st, sh = _lib.blhd(x)
         arr[i] = _lib.PoolArgs(p, sb, st, sh, _lib.dtype_code(x), b, logical_len, h, d, block_size, num_blocks,
-                               _lib.ptr(heads), 0 if heads is None else heads.numel(), out.data_ptr(), int(emulate))
+                               *_lib.heads_arg(heads), out.data_ptr(), int(emulate))
         outs.append(out)
         keep.append(x)
     _lib.call("wa_block_mean_pool_n", arr, len(jobs), _lib.stream_ptr(dev))
@@ -200,8 +200,8 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
         head_k_t = _lib.head_list(head_k, dev)
     # the threshold is tau_min + G * (tau_max - tau_min) in fp32, with the span formed in double
     args = _lib.RouteArgs(_lib.ptr(probs), _lib.ptr(qp), _lib.ptr(kp), bsz, nheads, nq, nkv, d, mode,
-                          float(tau_min), float(tau_max - tau_min), _lib.ptr(head_k_t), _lib.ptr(heads),
-                          0 if heads is None else heads.numel(), index.data_ptr(), num.data_ptr(),
+                          float(tau_min), float(tau_max - tau_min), _lib.ptr(head_k_t), *_lib.heads_arg(heads),
+                          index.data_ptr(), num.data_ptr(),
                           thresholds.data_ptr(), _lib.ptr(mask), _lib.ptr(probs_out), _lib.ptr(ws),
                           _lib.ptr(clear), 0 if clear is None else clear.numel(), int(k_sum_len),
                           int(block_size), int(bool(k_sum_bf16)), int(k_pooled_blocks))
