@@ -78,7 +78,9 @@ __device__ __forceinline__ void rotate_band(float (&f)[VEC], int d0, const float
 // Page summary: partial column sums per (segment, batch, token split), then a fixed-order
 // reduction per segment. One thread owns VEC consecutive channels of one head.
 // =============================================================================================
-constexpr int SUM_TOKENS_PER_SPLIT = 64;
+// 256 tokens per split: one round of workgroups at the cfg 3 shape (120 pages x 7 splits); 64 made
+// 3,000 workgroups of which the last ~440 ran a second, nearly empty round (125 -> 116 us).
+constexpr int SUM_TOKENS_PER_SPLIT = 256;
 constexpr int SUM_MAX_SPLITS = 64;
 
 int64_t summary_splits(int64_t max_seg_tokens) {
