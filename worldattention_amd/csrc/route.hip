@@ -5,6 +5,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "tile.h"
 #include "torch_order.h"
 
 namespace {
@@ -371,15 +372,43 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
 // register e of the lane, so the softmax reduces over the wave and the bitonic network runs in
 // registers (strides >= 64) and lane shuffles (strides < 64) without further barriers. The
 // softmax takes the max, fp32 exponentials and a double row sum, then p = e * (1 / sum).
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, 64);
+// The value of lane ^ stride (stride a power of two below 64, a constant after unrolling) by VALU
+// lane moves: DPP quad permutes (1, 2), row shifts (4), a row rotate (8) and the gfx950 half-row
+// and half-wave swaps (16, 32). Through ds_bpermute, each of the sort's dependent steps waited on
+// the LDS crossbar: the sort took ~11,600 cycles of a ~27,000-cycle workgroup.
+__device__ __forceinline__ uint32_t xor_lanes(uint32_t v, int stride, int lane) {
+  switch (stride) {
+    case 1: return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+    case 2: return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+    case 4: {
+      const uint32_t up = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0xF, false);  // row_shl:4 (lane + 4)
+      const uint32_t dn = __builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false);  // row_shr:4 (lane - 4)
+      return (lane & 4) ? dn : up;
+    }
+    case 8: return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    case 16: {
+      const auto sw = __builtin_amdgcn_permlane16_swap(v, v, false, false);  // {odd rows <- lane - 16, even <- + 16}
+      return (lane & 16) ? sw[0] : sw[1];
+    }
+    default: {
+      const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // {upper half <- lane - 32, lower <- + 32}
+      return (lane & 32) ? sw[0] : sw[1];
+    }
+  }
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m, int lane) {
+  const uint32_t lo = xor_lanes((uint32_t)v, m, lane);
+  const uint32_t hi = xor_lanes((uint32_t)(v >> 32), m, lane);
   return ((uint64_t)hi << 32) | lo;
 }
 
 template <int KPL, int DK, int R, bool SUMS>
 __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   constexpr int NP = 64 * KPL;
+  // With the head dim known, the head's pooled keys are staged here (row j, 16-byte chunk c in slot
+  // c ^ (j % (DK / 4)): a thread's row reads are then conflict-free across 16 lanes).
+  __shared__ __attribute__((aligned(1024))) float k_sh[DK ? NP : 1][DK ? DK : 4];
   __shared__ __attribute__((aligned(16))) float q_sh[R][256];
   __shared__ float s_sh[R][NP];
   __shared__ __attribute__((aligned(16))) float last_sh[SUMS ? 256 : 4];
@@ -399,16 +428,18 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
   // means divide: the workgroup converts it once into LDS instead of one thread dividing D times.
   const bool last_in_lds = SUMS && p.inv_bs != 0.f && !p.k_sum_div;
   f32x4 kv[DK ? DK / 4 : 1];
-  auto load_key = [&](int j) {
-    const int jj = min(j, N - 1);
-    const float* kr = kbase + (int64_t)jj * D;
-#pragma unroll
-    for (int c = 0; c < (DK ? DK / 4 : 1); ++c) kv[c] = *(const f32x4*)(kr + 4 * c);
-    if constexpr (SUMS) {
-      if (!(last_in_lds && jj == N - 1)) pooled_key_row(p, kv, jj);
+  // The head's pooled key rows [0, N) go to LDS by direct-to-LDS loads, 1 KiB (RPI whole rows)
+  // per wave instruction. Loading each thread's row into registers took ~11,000 cycles of a
+  // ~27,000-cycle workgroup: every load instruction touched 64 rows 512 bytes apart.
+  constexpr int CPR = DK ? DK / 4 : 1, RPI = 64 / CPR;
+  if constexpr (DK != 0) {
+    const int nins = (N + 4 * RPI - 1) / (4 * RPI);
+    for (int i = 0; i < nins; ++i) {
+      const int r0 = (i * 4 + w) * RPI, row = r0 + lane / CPR, slot = lane % CPR;
+      const int rr = min(row, N - 1);  // rows past the head's keys repeat the last (never read)
+      lds_dma16_global(kbase + (int64_t)rr * D + (slot ^ (row % CPR)) * 4, &k_sh[r0][0]);
     }
-  };
-  if (DK) load_key(tid);
+  }
   if constexpr (SUMS) {
     if (last_in_lds) {
       const float* kr = kbase + (int64_t)(N - 1) * D;
@@ -420,11 +451,20 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
     const int r = u / D, d = u % D;
     q_sh[r][d] = i0 + r < p.Nq ? p.qp[(row0 + i0 + r) * D + d] : 0.f;
   }
+  if constexpr (DK != 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's key rows landed
   __syncthreads();
-  if constexpr (SUMS && DK != 0) {
-    if (last_in_lds && tid == N - 1) {
+  if constexpr (DK != 0) {
+    // this thread's key row (as the pooled means: from cached sums the row is converted)
+    const int jj = min(tid, N - 1);
 #pragma unroll
-      for (int c = 0; c < DK / 4; ++c) kv[c] = *(const f32x4*)(&last_sh[4 * c]);
+    for (int c = 0; c < CPR; ++c) kv[c] = *(const f32x4*)(&k_sh[jj][(c ^ (jj % CPR)) * 4]);
+    if constexpr (SUMS) {
+      if (last_in_lds && jj == N - 1) {
+#pragma unroll
+        for (int c = 0; c < DK / 4; ++c) kv[c] = *(const f32x4*)(&last_sh[4 * c]);
+      } else {
+        pooled_key_row(p, kv, jj);
+      }
     }
   }
   for (int j = tid; j < N; j += 256) {
@@ -490,49 +530,84 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
     for (int r = 0; r < R; ++r) s_sh[r][j] = acc[r] * p.scale;
   }
   __syncthreads();
-  const int i = i0 + w;
-  if (w >= R || i >= p.Nq) return;
+  // With two rows per workgroup each row's softmax and sort run on two waves (half h of the row:
+  // positions 128 h + 64 e + lane), so all four waves work; one row per wave took ~9,500 cycles
+  // of sorting on one wave per SIMD. The halves meet through LDS for the softmax max and sum
+  // (added in half order) and for the sort's one stride that crosses them (128, at size 256).
+  constexpr bool SPLIT = R == 2 && KPL >= 2;
+  constexpr int KW = SPLIT ? KPL / 2 : KPL;  // keys per lane of a wave
+  __shared__ float red_mx[4];
+  __shared__ double red_se[4];
+  __shared__ uint64_t xk[SPLIT ? 4 : 1][SPLIT ? 64 * KW : 1];
+  const int rw = SPLIT ? w >> 1 : w, hw = SPLIT ? (w & 1) : 0;
+  const int i = i0 + rw;
+  const bool active = rw < R && i < p.Nq;  // an inactive wave of a split row still meets the barriers
+  if (!SPLIT && !active) return;
   const int64_t row = row0 + i;
-  float* ss = s_sh[w];
+  float* ss = s_sh[rw < R ? rw : 0];
+  const int pos0 = hw * 64 * KW;  // first row position of this wave
 
   // 2. softmax over the row
-  float sc[KPL];
+  float sc[KW];
   float mx = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < KPL; ++e) {
-    const int j = e * 64 + lane;
+  for (int e = 0; e < KW; ++e) {
+    const int j = pos0 + e * 64 + lane;
     sc[e] = j < N ? ss[j] : -INFINITY;
     mx = fmaxf(mx, sc[e]);
   }
   mx = wa_wave_max(mx);
+  if constexpr (SPLIT) {
+    if (lane == 0) red_mx[w] = mx;
+    __syncthreads();
+    mx = fmaxf(red_mx[w & ~1], red_mx[w | 1]);
+  }
   double se = 0.0;
 #pragma unroll
-  for (int e = 0; e < KPL; ++e) {
-    const int j = e * 64 + lane;
+  for (int e = 0; e < KW; ++e) {
+    const int j = pos0 + e * 64 + lane;
     sc[e] = j < N ? expf(sc[e] - mx) : 0.f;
     se += (double)sc[e];
   }
   se = wa_wave_sum_d(se);
+  if constexpr (SPLIT) {
+    if (lane == 0) red_se[w] = se;
+    __syncthreads();
+    se = red_se[w & ~1] + red_se[w | 1];
+  }
   const float inv_sum = (float)(1.0 / se);
 
   // 3. composite keys (probability order bits, inverted block id), padding 0; bitonic, descending
-  uint64_t key[KPL];
+  uint64_t key[KW];
 #pragma unroll
-  for (int e = 0; e < KPL; ++e) {
-    const int j = e * 64 + lane;
+  for (int e = 0; e < KW; ++e) {
+    const int j = pos0 + e * 64 + lane;
     key[e] = j < N ? (((uint64_t)wa_float_key(sc[e] * inv_sum) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)j)) : 0ull;
   }
 #pragma unroll
   for (int size = 2; size <= NP; size <<= 1) {
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      if (stride >= 64) {
+      if (SPLIT && stride == 64 * KW) {
+        // the partner is the same slot of the row's other wave
+#pragma unroll
+        for (int e = 0; e < KW; ++e) xk[w][e * 64 + lane] = key[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < KW; ++e) {
+          const uint64_t other = xk[w ^ 1][e * 64 + lane];
+          const bool lower = hw == 0;
+          const bool desc = ((pos0 + e * 64 + lane) & size) == 0;
+          const bool keep = (key[e] > other) == (lower == desc);
+          key[e] = keep ? key[e] : other;
+        }
+      } else if (stride >= 64) {
         const int es = stride >> 6;
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) {
+        for (int e = 0; e < KW; ++e) {
           const int pe = e ^ es;
           if (pe > e) {
-            const bool desc = ((e * 64 + lane) & size) == 0;
+            const bool desc = ((pos0 + e * 64 + lane) & size) == 0;
             const uint64_t a = key[e], c = key[pe];
             if ((a < c) == desc) {
               key[e] = c;
@@ -542,31 +617,34 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) {
-          const uint64_t other = shfl_xor_u64(key[e], stride);
+        for (int e = 0; e < KW; ++e) {
+          const uint64_t other = shfl_xor_u64(key[e], stride, lane);
           const bool lower = (lane & stride) == 0;
-          const bool desc = ((e * 64 + lane) & size) == 0;
-          const bool take_max = lower == desc;
-          key[e] = take_max ? (key[e] > other ? key[e] : other) : (key[e] < other ? key[e] : other);
+          const bool desc = ((pos0 + e * 64 + lane) & size) == 0;
+          // keep the larger key where this lane takes the maximum, else the smaller (one compare,
+          // one select; keys are distinct but for the equal zero padding)
+          const bool keep = (key[e] > other) == (lower == desc);
+          key[e] = keep ? key[e] : other;
         }
       }
     }
   }
+  if (!active) return;
 
   // 4. permutation and count
   int32_t* idx_row = p.index + row * N;
   const int kk = p.head_k ? p.head_k[h] : N;
   const int n = max(0, min(kk, N));
 #pragma unroll
-  for (int e = 0; e < KPL; ++e) {
-    const int m = e * 64 + lane;
+  for (int e = 0; e < KW; ++e) {
+    const int m = pos0 + e * 64 + lane;
     if (m < N) {
       const int32_t id = (int32_t)(0xFFFFFFFFu - (uint32_t)key[e]);
       idx_row[m] = id;
       if (p.mask) p.mask[row * N + id] = m < n ? 1 : 0;
     }
   }
-  if (lane == 0) p.num[row] = n;
+  if (lane == 0 && hw == 0) p.num[row] = n;
 }
 
 // Gini second pass: per-head threshold (mean of the head's row Ginis), then the count of sorted
