@@ -4,7 +4,7 @@
  * Every entry point takes plain device pointers, element strides and sizes, launches on the
  * caller's HIP stream (`stream` is a hipStream_t passed as void*), allocates nothing and keeps no
  * global device state, except wa_bsa_fwd_noalloc, whose workspace is a static device array of the
- * library. Inputs, outputs and workspaces are owned by the caller; workspace sizes come from the
+ * library, and wa_hsa_fwd, which creates a side stream and two events per device on its first call. Inputs, outputs and workspaces are owned by the caller; workspace sizes come from the
  * matching *_workspace_bytes query.
  *
  * Return value: WA_OK (0) on success; a negative WA_ERR_* for argument errors; a positive
@@ -260,6 +260,38 @@ int wa_bsa_fwd(const wa_bsa_fwd_args* args, void* stream);
  * calls in one stream are ordered and safe. Results equal wa_bsa_fwd's bit for bit. */
 #define WA_BSA_FWD_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* args, void* stream);
+
+/* The HSA forward of heads that take one branch each, in one call: block pooling of the sparse
+ * heads' queries and keys (wa_block_mean_pool_n), their top-k routing (wa_route, TOPK; index / num
+ * written for the caller), the block-sparse attention of those heads rounded to bf16 (wa_bsa_fwd,
+ * PLAIN), the elu(x)+1 state of the linear heads (wa_elu1_state) and their gated readout
+ * (wa_elu1_readout, GATED), from one workspace of wa_hsa_fwd_workspace_bytes. The two elu1 calls
+ * run on a side stream of the library's, forked from and joined back to `stream` inside the call
+ * (created, with two events, on a device's first call that is not under stream capture, and kept
+ * until the process ends; before that, and with one kind of head, everything runs on `stream`).
+ * It replaces the orchestration of hsa_attention, wan/modules/hsa/attention.py:153-259, for the
+ * north-star head modes (sparse / linear heads, no head in both branches) with bf16 q / k / v;
+ * the result equals those calls made one by one.
+ * head_k: [H] top-k budget per global head. units / n_units / max_visits: the unit table of the
+ * sparse launch (see wa_bsa_fwd). */
+typedef struct wa_hsa_fwd_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  void* o; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  int64_t B, H, Lq, Lkv, D, block_size;
+  const int32_t* sparse_heads; int64_t n_sparse;
+  const int32_t* head_k;
+  const int32_t* units; int64_t n_units; int64_t max_visits;
+  int32_t* index; int32_t* num;
+  const int32_t* linear_heads; int64_t n_linear;
+  const void* gate_w; const float* gate_b;
+  int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
+  void* workspace;
+} wa_hsa_fwd_args;
+int64_t wa_hsa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t Lq, int64_t Lkv, int64_t D, int64_t block_size,
+                                   int64_t n_sparse, int64_t n_linear, int64_t max_visits);
+int wa_hsa_fwd(const wa_hsa_fwd_args* args, void* stream);
 
 /* Backward of wa_bsa_fwd: dQ, dK, dV (fp32, BLHD) of the block-sparse attention output o.
  * Replaces _bwd_preprocess/_bwd_kernel/_backward, wan/modules/hsa/block_sparse_triton.py:142-368

@@ -511,3 +511,47 @@ def test_hsa_forward_graph_replays_equal_eager_calls():
         other = call()                    # eager work between replays
         assert torch.equal(other, want)
         torch.cuda.synchronize()
+
+
+def test_native_split_forward_equals_the_python_orchestration():
+    """hsa_forward of split heads (top-k sparse, elu1 linear, bf16) runs as one library call
+    (wa_hsa_fwd). With a trained gate it gives, bit for bit, the output and routing of the same
+    entry points called one by one from Python (pooling, routing, the sparse launch, the elu1
+    state and the gated readout)."""
+    from worldattention_amd import _lib
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    cfg = workloads.cfg2(device=DEV, seed=6)
+    q, k, v = cfg["q"], cfg["k"], cfg["v"]
+    b, lq, h, d = q.shape
+    lkv, bs = k.shape[1], cfg["block_size"]
+    gate = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        gate.weight.normal_(0, 0.05)
+        gate.bias.normal_(0, 0.05)
+    kw = dict(k_coarse=None, v_coarse=None, k_proj_mat=None, v_proj_mat=None, gate_lin=gate,
+              block_size=bs, tau_min=0.35, tau_max=1.0, proj_segment_len=cfg["proj_segment_len"],
+              routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode=cfg["linear_mode"])
+    save = {}
+    with torch.no_grad():
+        got = WA.hsa_forward(q, k, v, save=save, **kw)
+
+    plan = WA.HeadPlan(h, cfg["head_modes"], DEV)
+    spec = WA.GateSpec(gate, v.dtype)
+    ks = WA._per_head_k(cfg["topk"], h)
+    _, _, nq, nkv = WR.block_counts(lq, lkv, bs)
+    want = torch.empty_like(got)
+    with torch.no_grad():
+        qp, kp, key_args = WR.pool_for_routing(q, k, lq, lkv, bs, plan.t["sparse"])
+        arrivals = torch.empty(b * len(plan.sparse_only) * nq, dtype=torch.int32, device=DEV)
+        route, _ = WR._route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=plan.t["sparse"],
+                             clear=arrivals, **key_args)
+        bsa_forward(q, k, v, index=route.index, num=route.num, block_size=bs, layout="blhd",
+                    heads=plan.t["sparse_only"], out=want, lq=lq, lkv=lkv, attn_round_bf16=True,
+                    visits=[min(ks[i], nkv) for i in plan.sparse_only], arrivals=arrivals)
+        s, z = WA.elu1_state(k, v, plan.t["linear_only"])
+        WA.elu1_readout(q, s, z, plan.t["linear_only"], want, epilogue=_lib.WA_EPI_GATED, lin_round_bf16=True,
+                        **spec.kwargs())
+    assert torch.equal(got, want)
+    sparse = plan.sparse_only
+    assert torch.equal(save["route"].index[:, sparse], route.index[:, sparse])
+    assert torch.equal(save["route"].num[:, sparse], route.num[:, sparse])

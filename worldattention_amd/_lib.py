@@ -149,6 +149,22 @@ Elu1ReadoutArgs = _struct("wa_elu1_readout_args", [
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
 ])
 
+HsaFwdArgs = _struct("wa_hsa_fwd_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("o", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64), ("block_size", c_int64),
+    ("sparse_heads", c_void_p), ("n_sparse", c_int64),
+    ("head_k", c_void_p),
+    ("units", c_void_p), ("n_units", c_int64), ("max_visits", c_int64),
+    ("index", c_void_p), ("num", c_void_p),
+    ("linear_heads", c_void_p), ("n_linear", c_int64),
+    ("gate_w", c_void_p), ("gate_b", c_void_p),
+    ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
+    ("workspace", c_void_p),
+])
+
 BsaBwdArgs = _struct("wa_bsa_bwd_args", [
     ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
     ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
@@ -262,6 +278,8 @@ SIGNATURES = {
     "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_elu1_state": (c_int, [POINTER(Elu1StateArgs), c_void_p]),
     "wa_elu1_readout": (c_int, [POINTER(Elu1ReadoutArgs), c_void_p]),
+    "wa_hsa_fwd_workspace_bytes": (c_int64, [c_int64] * 9),
+    "wa_hsa_fwd": (c_int, [POINTER(HsaFwdArgs), c_void_p]),
     "wa_bsa_bwd_workspace_bytes": (c_int64, [c_int64] * 6),
     "wa_bsa_bwd": (c_int, [POINTER(BsaBwdArgs), c_void_p]),
     "wa_elu1_bwd_workspace_bytes": (c_int64, [c_int64] * 4),

@@ -29,8 +29,8 @@ import torch.nn as nn
 
 from .. import _lib
 from . import distill
-from .block_sparse import bsa_forward
-from .routing import _route, block_counts, pool_for_routing
+from .block_sparse import bsa_forward, unit_table
+from .routing import BlockRouting, _route, block_counts, pool_for_routing
 
 __all__ = [
     "HSAAttention",
@@ -297,6 +297,12 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     kb = _lib.kernel_ready(k)
     vb = _lib.kernel_ready(v)
     out = torch.empty((bsz, q_len, heads, head_dim), dtype=comp_dtype, device=dev)
+    if (routing == "topk" and linear_mode == "elu1" and plan.sparse_only and plan.linear_only and not plan.both
+            and k_block_sums is None and k_pooled is None and qb is q and kb is k and vb is v
+            and q.dtype == torch.bfloat16):
+        _native_split_forward(q, k, v, plan, _per_head_k(topk, heads), gate, lin_round, block_size, q_len, kv_len,
+                              out, save)
+        return out if out.dtype == out_dtype else out.to(out_dtype)
     lin_tmp = torch.empty_like(out) if plan.both else None
 
     # With both branches present the linear branch runs on a side stream, concurrently with
@@ -363,6 +369,36 @@ def _branch_stream(dev: torch.device) -> torch.cuda.Stream:
         s = torch.cuda.Stream(device=dev)
         _BRANCH_STREAMS[dev] = s
     return s
+
+
+def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len, kv_len, out, save):
+    """:func:`hsa_forward` of top-k sparse heads and elu1 linear heads as one library call
+    (``wa_hsa_fwd``): the same entry points with the same arguments as the Python orchestration,
+    the linear heads' on a side stream of the library's that the caller's stream forks and joins
+    inside the call (so graph capture records the same two branches). An eager call then pays one
+    crossing into the library instead of ~20 (allocations, argument structs, launches, events):
+    171 -> 48 us of host time, and at cfg 2 the eager call went from 195 to 141 us (GPU-bound)."""
+    dev = q.device
+    bsz, _, heads, d = q.shape
+    _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
+    vis = [min(ks[h], nkv) for h in plan.sparse_only]
+    units, n_units = unit_table(bsz, vis, nq, _lib.BSA_DEFAULT_SPLIT, dev)
+    max_visits = max(max(vis), 1)
+    n_sp, n_lin = len(plan.sparse_only), len(plan.linear_only)
+    index = torch.empty((bsz, heads, nq, nkv), dtype=torch.int32, device=dev)
+    num = torch.empty((bsz, heads, nq), dtype=torch.int32, device=dev)
+    ws = torch.empty((_lib.lib().wa_hsa_fwd_workspace_bytes(bsz, heads, q_len, kv_len, d, block_size, n_sp, n_lin,
+                                                             max_visits),), dtype=torch.uint8, device=dev)
+    args = _lib.HsaFwdArgs(*_lib.blhd(q), *_lib.blhd(k), *_lib.blhd(v), *_lib.blhd(out), _lib.dtype_code(out),
+                           bsz, heads, q_len, kv_len, d, block_size,
+                           *_lib.heads_arg(plan.t["sparse_only"]), _lib.head_list(ks, dev).data_ptr(),
+                           units.data_ptr(), n_units, max_visits, index.data_ptr(), num.data_ptr(),
+                           *_lib.heads_arg(plan.t["linear_only"]), _lib.ptr(gate.w), _lib.ptr(gate.b),
+                           int(gate.pre_bf16), int(gate.out_bf16), int(lin_round), ws.data_ptr())
+    _lib.call("wa_hsa_fwd", args, _lib.stream_ptr(dev))
+    if save is not None:  # top-k routing has no thresholds (the kernel writes zeros)
+        save.update(route=BlockRouting(index=index, num=num, mask=None,
+                                       thresholds=torch.zeros((heads,), dtype=torch.float32, device=dev)))
 
 
 def _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat, proj_segment_len,
