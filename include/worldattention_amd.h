@@ -344,6 +344,30 @@ typedef struct wa_compress_args {
 } wa_compress_args;
 int wa_compress_kv(const wa_compress_args* args, void* stream);
 
+/* Backward of wa_compress_kv. dout: gradient of the compressed rows (fp32, BLHD strides, the Lc
+ * rows wa_compress_kv wrote); x, proj and the sizes as in the forward, with E = proj's stored
+ * values (fp32, or bf16 widened). Per segment (rows row0 .. row0 + r of dout, tokens start ..):
+ *   dx[b, start + t, h, :] = sum_j E[j, t] dout[b, row0 + j, h, :]      (fp32; optional)
+ *   dproj[j, t] = sum over segments, batches, heads and channels of dout[row0 + j] x[start + t]
+ * dproj (optional) is [proj_rank, proj_len] fp32 row-major; entries no segment covers get zero.
+ * With *_accumulate set the gradient is added to the existing contents. fp32 arithmetic; the
+ * dproj sum runs in a fixed order (per-segment partials in `workspace`, of
+ * wa_compress_kv_bwd_workspace_bytes, added in segment order), so results repeat bit for bit.
+ * dout and dx are read / written by float4 and x by 16 bytes: each must be 16-byte aligned with
+ * strides that keep every row so.
+ * Replaces the autograd of compress_kv's per-segment matmul, wan/modules/hsa/attention.py:64-110. */
+typedef struct wa_compress_bwd_args {
+  const float* dout; int64_t d_sb, d_st, d_sh;
+  const void* x; int64_t x_sb, x_st, x_sh; int32_t x_dtype;
+  const void* proj; int32_t proj_dtype; int64_t proj_rank, proj_len;
+  int64_t B, L, H, D, segment_len, block_size;
+  float* dx; int64_t dx_sb, dx_st, dx_sh; int32_t dx_accumulate;
+  float* dproj; int32_t dproj_accumulate;
+  void* workspace;
+} wa_compress_bwd_args;
+int64_t wa_compress_kv_bwd_workspace_bytes(int64_t L, int64_t proj_rank, int64_t segment_len, int64_t block_size);
+int wa_compress_kv_bwd(const wa_compress_bwd_args* args, void* stream);
+
 /* Kernelized linear attention state (north star, no reference counterpart):
  * state[b,s,d,e] = sum_t v[t,d] * phi(k[t,e]) and zsum[b,s,e] = sum_t phi(k[t,e]) with
  * phi(x) = elu(x) + 1, for each listed head heads[s] (fp32 outputs, [B, n_heads, D, D] / [B, n_heads, D]);

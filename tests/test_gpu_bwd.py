@@ -160,6 +160,38 @@ def test_hsa_split_heads_topk_elu1_gradients_match_oracle():
         assert_close(g, r, *tol, what=name)
 
 
+@pytest.mark.parametrize("b,length,h,d,seg,bs,rank,plen,xdt", [
+    (2, 700, 3, 64, 256, 64, 4, 256, torch.bfloat16),     # three segments, the last of rank 3
+    (1, 1000, 5, 128, 1000, 32, 20, 1000, torch.float32),  # one segment, rank 20, fp32 x
+    (1, 300, 2, 32, 128, 64, 8, 200, torch.bfloat16),     # rows and columns of E no segment uses
+])
+def test_compress_backward_matches_oracle_autograd(b, length, h, d, seg, bs, rank, plen, xdt):
+    """wa_compress_kv_bwd: dx and dE against autograd through the oracle's compress_kv in fp32 (the
+    same fp32 arithmetic, so only the summation order differs: 1e-3 max-abs, 1e-4 mean-abs), dx
+    added to an existing gradient, and two calls bit for bit equal (fixed-order dE sum)."""
+    from worldattention_amd.hsa._autograd import _compress_backward
+    torch.manual_seed(length + d)
+    x = torch.randn(b, length, h, d).to(xdt)
+    proj = (torch.randn(rank, plen) / 16).bfloat16()
+    lc = O.compress_kv(x.permute(0, 2, 1, 3), x.permute(0, 2, 1, 3), segment_len=seg, k_proj_mat=proj,
+                       v_proj_mat=proj, block_size=bs)[0].shape[2]
+    g = torch.randn(b, lc, h, d)
+    xr = x.float().permute(0, 2, 1, 3).clone().requires_grad_(True)
+    pr = proj.float().clone().requires_grad_(True)
+    out, _ = O.compress_kv(xr, xr.detach(), segment_len=seg, k_proj_mat=pr, v_proj_mat=pr.detach(), block_size=bs)
+    (out * g.permute(0, 2, 1, 3)).sum().backward()
+    want_dx, want_dp = xr.grad.permute(0, 2, 1, 3), pr.grad
+
+    xg, pg, gg = x.to(DEV), proj.to(DEV), g.to(DEV)
+    dx, dp = _compress_backward(gg, xg, pg, seg, bs)
+    assert_close(dx, want_dx, 1e-3, 1e-4, what="dx")
+    assert_close(dp, want_dp, 1e-3, 1e-4, what="dE")
+    base = torch.randn(b, length, h, d, device=DEV)
+    dx2, dp2 = _compress_backward(gg, xg, pg, seg, bs, dx=base.clone())
+    assert torch.equal(dp2, dp), "dE differs between two calls"
+    assert_close(dx2, base + dx, 1e-6, 1e-7, what="accumulated dx")
+
+
 def test_hsa_reference_mode_gradients_match_oracle():
     """Reference semantics: every head runs both branches, Gini routing, low-rank softmax branch."""
     torch.manual_seed(3)

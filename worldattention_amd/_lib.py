@@ -129,6 +129,17 @@ CompressArgs = _struct("wa_compress_args", [
     ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
 ])
 
+CompressBwdArgs = _struct("wa_compress_bwd_args", [
+    ("dout", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64),
+    ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64), ("x_dtype", c_int32),
+    ("proj", c_void_p), ("proj_dtype", c_int32), ("proj_rank", c_int64), ("proj_len", c_int64),
+    ("B", c_int64), ("L", c_int64), ("H", c_int64), ("D", c_int64), ("segment_len", c_int64),
+    ("block_size", c_int64),
+    ("dx", c_void_p), ("dx_sb", c_int64), ("dx_st", c_int64), ("dx_sh", c_int64), ("dx_accumulate", c_int32),
+    ("dproj", c_void_p), ("dproj_accumulate", c_int32),
+    ("workspace", c_void_p),
+])
+
 Elu1StateArgs = _struct("wa_elu1_state_args", [
     ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
     ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
@@ -275,6 +286,8 @@ SIGNATURES = {
     "wa_bsa_fwd": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_bsa_fwd_noalloc": (c_int, [POINTER(BsaFwdArgs), c_void_p]),
     "wa_compress_kv": (c_int, [POINTER(CompressArgs), c_void_p]),
+    "wa_compress_kv_bwd_workspace_bytes": (c_int64, [c_int64] * 4),
+    "wa_compress_kv_bwd": (c_int, [POINTER(CompressBwdArgs), c_void_p]),
     "wa_elu1_state_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
     "wa_elu1_state": (c_int, [POINTER(Elu1StateArgs), c_void_p]),
     "wa_elu1_readout": (c_int, [POINTER(Elu1ReadoutArgs), c_void_p]),

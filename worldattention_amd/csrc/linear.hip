@@ -1,9 +1,12 @@
 // Low-rank linear branch of the reference (wan/modules/hsa/attention.py:64-118) for gfx950:
 //  * compress_kv — low-rank sequence projection per segment (attention.py:64-110); the softmax
-//    over the compressed keys then runs in the block-sparse kernel as dense attention.
+//    over the compressed keys then runs in the block-sparse kernel as dense attention;
+//  * its backward (dx and the projection's gradient) for training in the reference's head mode.
 // The contraction runs on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the token-axis
 // operand is staged through LDS transposed ([channel][token]).
 // The north-star elu(x)+1 linear branch lives in elu1.hip.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -110,7 +113,230 @@ __global__ void __launch_bounds__(256) compress_kernel(CompressParams p) {
   }
 }
 
+// =============================================================================================
+// compress_kv backward. For segment s (tokens start .. start + n, rows row0 .. row0 + r of the
+// compressed output, row0 = s * r_full): dx[start + t] = sum_j E[j, t] dout[row0 + j] and the
+// segment's share of dE[j, t] = sum_{b, h, d} dout[b, row0 + j, h, d] x[b, start + t, h, d].
+// fp32 arithmetic throughout; E is the projection's stored value (bf16 widened exactly).
+// =============================================================================================
+struct CompressBwdParams {
+  const float* dout; int64_t d_sb, d_st, d_sh;
+  const void* x; int64_t x_sb, x_st, x_sh; int x_dtype;
+  const void* proj; int proj_dtype; int R, P;
+  int B, L, H, D, seg, block, n_first, r_full, n_seg;
+  float* dx; int64_t dx_sb, dx_st, dx_sh; int dx_acc;
+  float* dproj; int dproj_acc;
+  float* part;  // [n_seg][r_full][n_first]
+};
+
+__device__ __forceinline__ float proj_at(const CompressBwdParams& p, int j, int t) {
+  const int64_t off = (int64_t)j * p.P + t;
+  return p.proj_dtype == WA_BF16 ? (float)((const bf16_t*)p.proj)[off] : ((const float*)p.proj)[off];
+}
+
+// dx: one workgroup per (16-token tile of a segment, 128 float4 columns of (head, channel), batch);
+// a thread keeps its column of the segment's dout rows 16 at a time in registers and the matching
+// 16 x 16 block of E in LDS, and sums over j in increasing order.
+constexpr int kDxTokens = 16, kDxRows = 16, kDxThreads = 128;
+__global__ void __launch_bounds__(kDxThreads) compress_bwd_dx_kernel(CompressBwdParams p) {
+  __shared__ float es[kDxRows][kDxTokens];
+  const int tps = (p.n_first + kDxTokens - 1) / kDxTokens;
+  const int s = blockIdx.x / tps, t0 = (blockIdx.x % tps) * kDxTokens, b = blockIdx.z;
+  const int start = s * p.seg, n = min(p.seg, p.L - start);
+  if (t0 >= n) return;  // uniform
+  const int r = min(p.R, (n + p.block - 1) / p.block), row0 = s * p.r_full;
+  const int tid = threadIdx.x;
+  const int c = blockIdx.y * kDxThreads + tid;  // float4 column
+  const bool active = c < p.H * p.D / 4;
+  const int h = active ? c * 4 / p.D : 0, d = active ? c * 4 % p.D : 0;
+  const float* gcol = p.dout + (int64_t)b * p.d_sb + (int64_t)h * p.d_sh + d;
+  f32x4 acc[kDxTokens];
+#pragma unroll
+  for (int i = 0; i < kDxTokens; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < r; j0 += kDxRows) {
+    __syncthreads();  // the previous block of E has been read
+    for (int i = tid; i < kDxRows * kDxTokens; i += kDxThreads) {
+      const int jj = i / kDxTokens, tl = i % kDxTokens, j = j0 + jj, t = t0 + tl;
+      es[jj][tl] = j < r && t < n ? proj_at(p, j, t) : 0.f;
+    }
+    f32x4 g[kDxRows];
+#pragma unroll
+    for (int jj = 0; jj < kDxRows; ++jj)
+      g[jj] = active && j0 + jj < r ? *(const f32x4*)(gcol + (int64_t)(row0 + j0 + jj) * p.d_st)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+#pragma unroll
+    for (int tl = 0; tl < kDxTokens; ++tl) {
+#pragma unroll
+      for (int jj = 0; jj < kDxRows; ++jj) {
+        const float e = es[jj][tl];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[tl][q] = fmaf(e, g[jj][q], acc[tl][q]);
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int tl = 0; tl < kDxTokens; ++tl) {
+    const int t = t0 + tl;
+    if (t >= n) break;
+    f32x4* dst = (f32x4*)(p.dx + (int64_t)b * p.dx_sb + (int64_t)(start + t) * p.dx_st + (int64_t)h * p.dx_sh + d);
+    *dst = p.dx_acc ? *dst + acc[tl] : acc[tl];
+  }
+}
+
+// dE share of one segment: one workgroup of 4 waves per (64-token tile, segment); lane = token,
+// wave w sums heads w, w + 4, ... of every batch for all r rows, then the four waves' sums are added
+// in wave order through LDS into the segment's partial.
+template <int RMAX>
+__global__ void __launch_bounds__(256) compress_bwd_dproj_kernel(CompressBwdParams p) {
+  __shared__ float red[4][16][64];
+  const int s = blockIdx.y, t0 = blockIdx.x * 64;
+  const int start = s * p.seg, n = min(p.seg, p.L - start);
+  if (t0 >= n) return;  // uniform
+  const int r = min(p.R, (n + p.block - 1) / p.block), row0 = s * p.r_full;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = t0 + lane;
+  const bool ok = t < n;
+  float acc[RMAX];
+#pragma unroll
+  for (int j = 0; j < RMAX; ++j) acc[j] = 0.f;
+  for (int b = 0; b < p.B; ++b) {
+    for (int h = w; h < p.H; h += 4) {
+      const int64_t xo = (int64_t)b * p.x_sb + (int64_t)(start + (ok ? t : 0)) * p.x_st + (int64_t)h * p.x_sh;
+      const float* grow = p.dout + (int64_t)b * p.d_sb + (int64_t)row0 * p.d_st + (int64_t)h * p.d_sh;
+      for (int d0 = 0; d0 < p.D; d0 += 8) {
+        float xf[8];
+        if (p.x_dtype == WA_BF16) {
+          const bf16x8 v = *(const bf16x8*)((const bf16_t*)p.x + xo + d0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xf[e] = ok ? (float)v[e] : 0.f;
+        } else {
+          const f32x4 v0 = *(const f32x4*)((const float*)p.x + xo + d0);
+          const f32x4 v1 = *(const f32x4*)((const float*)p.x + xo + d0 + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            xf[e] = ok ? v0[e] : 0.f;
+            xf[4 + e] = ok ? v1[e] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < RMAX; ++j) {
+          if (j >= r) break;
+          const f32x4 g0 = *(const f32x4*)(grow + (int64_t)j * p.d_st + d0);
+          const f32x4 g1 = *(const f32x4*)(grow + (int64_t)j * p.d_st + d0 + 4);
+          float a = acc[j];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a = fmaf(xf[e], g0[e], a);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a = fmaf(xf[4 + e], g1[e], a);
+          acc[j] = a;
+        }
+      }
+    }
+  }
+  float* part = p.part + (int64_t)s * p.r_full * p.n_first;
+#pragma unroll
+  for (int j0 = 0; j0 < RMAX; j0 += 16) {
+    if (j0 >= r) break;
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) red[w][jj][lane] = acc[j0 + jj < RMAX ? j0 + jj : 0];
+    __syncthreads();
+    // wave q writes rows j0 + q, j0 + q + 4, ...: the sum over waves 0..3 in order
+    for (int jj = w; jj < 16; jj += 4) {
+      const int j = j0 + jj;
+      if (j < r && ok)
+        part[(int64_t)j * p.n_first + t] = ((red[0][jj][lane] + red[1][jj][lane]) + red[2][jj][lane]) + red[3][jj][lane];
+    }
+  }
+}
+
+// dproj[j, t] (+)= sum over segments, in segment order, of the partials that cover (j, t); every
+// entry of the [R, P] matrix is visited, so in write mode untouched entries become zero.
+__global__ void __launch_bounds__(256) compress_bwd_reduce_kernel(CompressBwdParams p) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.R * p.P) return;
+  const int j = (int)(i / p.P), t = (int)(i % p.P);
+  float sum = 0.f;
+  if (j < p.r_full && t < p.n_first) {
+    for (int s = 0; s < p.n_seg; ++s) {
+      const int n = min(p.seg, p.L - s * p.seg);
+      const int r = min(p.R, (n + p.block - 1) / p.block);
+      if (j < r && t < n) sum += p.part[((int64_t)s * p.r_full + j) * p.n_first + t];
+    }
+  }
+  p.dproj[i] = p.dproj_acc ? p.dproj[i] + sum : sum;
+}
+
 }  // namespace
+
+extern "C" int64_t wa_compress_kv_bwd_workspace_bytes(int64_t L, int64_t proj_rank, int64_t segment_len,
+                                                      int64_t block_size) {
+  if (L <= 0 || proj_rank <= 0 || segment_len <= 0 || block_size <= 0) return 0;
+  const int64_t n_first = segment_len < L ? segment_len : L;
+  const int64_t r_full = std::min(proj_rank, (n_first + block_size - 1) / block_size);
+  const int64_t n_seg = (L + segment_len - 1) / segment_len;
+  return n_seg * r_full * n_first * 4;
+}
+
+extern "C" int wa_compress_kv_bwd(const wa_compress_bwd_args* a, void* stream) {
+  WA_CHECK_ARG(a && a->dout && a->x && a->proj, "wa_compress_kv_bwd: null argument");
+  WA_CHECK_ARG(a->dproj == nullptr || a->workspace != nullptr, "wa_compress_kv_bwd: dproj needs the workspace");
+  WA_CHECK_ARG(a->D == 32 || a->D == 64 || a->D == 128, "wa_compress_kv_bwd: head dim %lld not in {32, 64, 128}",
+               (long long)a->D);
+  WA_CHECK_ARG(a->x_dtype == WA_F32 || a->x_dtype == WA_BF16, "wa_compress_kv_bwd: bad dtype");
+  WA_CHECK_ARG(a->proj_dtype == WA_F32 || a->proj_dtype == WA_BF16, "wa_compress_kv_bwd: bad proj dtype");
+  WA_CHECK_ARG(a->segment_len > 0 && a->block_size > 0 && a->L > 0 && a->B >= 0 && a->H > 0,
+               "wa_compress_kv_bwd: bad sizes");
+  WA_CHECK_ARG(a->proj_rank > 0 && a->proj_rank <= 128, "wa_compress_kv_bwd: projection rank must be in [1, 128]");
+  const int64_t n_first = a->segment_len < a->L ? a->segment_len : a->L;
+  WA_CHECK_ARG(n_first <= a->proj_len, "wa_compress_kv_bwd: segment length %lld exceeds projection length %lld",
+               (long long)n_first, (long long)a->proj_len);
+  // vector accesses: dout / dx by float4, x by 16 bytes (8 bf16 or 2 x 4 fp32)
+  const int64_t xv = a->x_dtype == WA_BF16 ? 8 : 4;
+  WA_CHECK_ARG(wa_aligned16(a->dout) && a->d_sb % 4 == 0 && a->d_st % 4 == 0 && a->d_sh % 4 == 0,
+               "wa_compress_kv_bwd: dout must be 16-byte aligned with strides that are multiples of 4");
+  WA_CHECK_ARG(wa_aligned16(a->x) && a->x_sb % xv == 0 && a->x_st % xv == 0 && a->x_sh % xv == 0,
+               "wa_compress_kv_bwd: x must be 16-byte aligned with strides that are multiples of 16 bytes");
+  WA_CHECK_ARG(a->dx == nullptr || (wa_aligned16(a->dx) && a->dx_sb % 4 == 0 && a->dx_st % 4 == 0 && a->dx_sh % 4 == 0),
+               "wa_compress_kv_bwd: dx must be 16-byte aligned with strides that are multiples of 4");
+  WA_CHECK_ARG(a->L <= INT32_MAX && a->proj_rank * a->proj_len <= INT32_MAX, "wa_compress_kv_bwd: sizes too large");
+  const int64_t r_full = std::min(a->proj_rank, (n_first + a->block_size - 1) / a->block_size);
+  const int64_t n_seg = (a->L + a->segment_len - 1) / a->segment_len;
+  CompressBwdParams cp{a->dout, a->d_sb, a->d_st, a->d_sh, a->x, a->x_sb, a->x_st, a->x_sh, a->x_dtype,
+                       a->proj, a->proj_dtype, (int)a->proj_rank, (int)a->proj_len,
+                       (int)a->B, (int)a->L, (int)a->H, (int)a->D, (int)a->segment_len, (int)a->block_size,
+                       (int)n_first, (int)r_full, (int)n_seg,
+                       a->dx, a->dx_sb, a->dx_st, a->dx_sh, a->dx_accumulate,
+                       a->dproj, a->dproj_accumulate, (float*)a->workspace};
+  hipStream_t s = (hipStream_t)stream;
+  if (a->B > 0 && a->dx) {
+    const int64_t tps = (n_first + kDxTokens - 1) / kDxTokens;
+    const int64_t cols = a->H * a->D / 4;
+    dim3 grid((unsigned)(n_seg * tps), (unsigned)((cols + kDxThreads - 1) / kDxThreads), (unsigned)a->B);
+    hipLaunchKernelGGL(compress_bwd_dx_kernel, grid, dim3(kDxThreads), 0, s, cp);
+    const int rc = wa_launch_status("compress_kv_bwd (dx)");
+    if (rc != WA_OK) return rc;
+  }
+  if (a->dproj) {
+    if (a->B > 0) {
+      dim3 grid((unsigned)((n_first + 63) / 64), (unsigned)n_seg);
+      if (r_full <= 16) hipLaunchKernelGGL(compress_bwd_dproj_kernel<16>, grid, dim3(256), 0, s, cp);
+      else if (r_full <= 32) hipLaunchKernelGGL(compress_bwd_dproj_kernel<32>, grid, dim3(256), 0, s, cp);
+      else if (r_full <= 64) hipLaunchKernelGGL(compress_bwd_dproj_kernel<64>, grid, dim3(256), 0, s, cp);
+      else hipLaunchKernelGGL(compress_bwd_dproj_kernel<128>, grid, dim3(256), 0, s, cp);
+      const int rc = wa_launch_status("compress_kv_bwd (dproj)");
+      if (rc != WA_OK) return rc;
+    } else {
+      cp.n_seg = 0;  // no batches: every partial is zero
+    }
+    const int64_t total = a->proj_rank * a->proj_len;
+    hipLaunchKernelGGL(compress_bwd_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, cp);
+    return wa_launch_status("compress_kv_bwd (reduce)");
+  }
+  return WA_OK;
+}
 
 extern "C" int wa_compress_kv(const wa_compress_args* a, void* stream) {
   WA_CHECK_ARG(a && a->x && a->proj && a->out, "wa_compress_kv: null argument");

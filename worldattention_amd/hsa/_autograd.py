@@ -9,7 +9,6 @@ not differentiated, as in the reference (its ``argsort`` / thresholds carry no g
 """
 from __future__ import annotations
 
-import math
 
 import torch
 
@@ -91,23 +90,32 @@ def elu1_backward(q, k, v, dout, state, zsum, heads_t, dq, dk, dv, *, dq_accumul
 # ----------------------------------------------------------------------------------------------
 # low-rank compression (attention.py:64-110) under autograd
 # ----------------------------------------------------------------------------------------------
-def _compress_backward(grad, x, proj, segment_len, block_size):
-    """Gradients of ``out_seg = E[:r, :len] @ x_seg`` per segment: ``dx_seg = E^T dout_seg`` and
-    ``dE[:r, :len] = sum_{b, h} dout_seg x_seg^T`` (fp32 library GEMMs over [B, H] batches)."""
+def _compress_backward(grad, x, proj, segment_len, block_size, dx=None):
+    """Gradients of ``out_seg = E[:r, :len] @ x_seg`` per segment (``wa_compress_kv_bwd``):
+    ``dx_seg = E^T dout_seg`` and ``dE[:r, :len] = sum_{b, h} dout_seg x_seg^T``, fp32, for a
+    ``[B, L, H, D]`` x and a ``[B, Lc, H, D]`` gradient. ``dx`` (optional): an fp32 ``[B, L, H, D]``
+    tensor with unit last stride that the x gradient is added to; otherwise a new one is returned.
+    Returns ``(dx, dproj)``, dproj fp32 of the projection's shape."""
+    dev = _lib.require_gpu(x, proj)
     bsz, length, heads, d = x.shape
     seg = segment_len if segment_len > 0 else length
-    dx = torch.zeros((bsz, length, heads, d), dtype=torch.float32, device=x.device)
-    dproj = torch.zeros(proj.shape, dtype=torch.float32, device=x.device)
-    row = 0
-    for start in range(0, length, seg):
-        n = min(seg, length - start)
-        r = min(proj.shape[0], math.ceil(n / block_size))
-        e = proj[:r, :n].float().contiguous()                                     # [r, n]
-        go = grad[:, row:row + r].float().permute(0, 2, 1, 3).contiguous()        # [B, H, r, D]
-        xs = x[:, start:start + n].float().permute(0, 2, 1, 3).contiguous()       # [B, H, n, D]
-        dx[:, start:start + n] = torch.matmul(e.t().contiguous(), go).permute(0, 2, 1, 3)
-        dproj[:r, :n] += torch.matmul(go.reshape(-1, r, d), xs.reshape(-1, n, d).transpose(1, 2).contiguous()).sum(0)
-        row += r
+    g = grad if grad.dtype == torch.float32 and grad.is_contiguous() else grad.float().contiguous()
+    xs = x if x.dtype in (torch.float32, torch.bfloat16) and x.is_contiguous() else (
+        x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous())
+    pj = proj if proj.dtype in (torch.float32, torch.bfloat16) else proj.float()
+    pj = pj.contiguous()
+    accumulate = dx is not None
+    if dx is None:
+        dx = torch.empty((bsz, length, heads, d), dtype=torch.float32, device=dev)
+    elif dx.dtype != torch.float32 or tuple(dx.shape) != (bsz, length, heads, d) or dx.stride(-1) != 1:
+        raise ValueError(f"dx must be float32 {(bsz, length, heads, d)} with unit last stride")
+    dproj = torch.empty(pj.shape, dtype=torch.float32, device=dev)
+    ws = torch.empty((max(_lib.lib().wa_compress_kv_bwd_workspace_bytes(length, pj.shape[0], seg, block_size), 4),),
+                     dtype=torch.uint8, device=dev)
+    args = _lib.CompressBwdArgs(*_lib.blhd(g), *_lib.blhd(xs), _lib.dtype_code(xs), pj.data_ptr(),
+                                _lib.dtype_code(pj), pj.shape[0], pj.shape[1], bsz, length, heads, d, seg,
+                                block_size, *_lib.blhd(dx), int(accumulate), dproj.data_ptr(), 0, ws.data_ptr())
+    _lib.call("wa_compress_kv_bwd", args, _lib.stream_ptr(dev))
     return dx, dproj
 
 
@@ -274,10 +282,8 @@ class _HSA(torch.autograd.Function):
                 bsa_backward(qb, kcb, vcb, lin, lse_l, dlin, index=None, num=None, block_size=block_size,
                              layout="blhd", heads=lt, lq=q_len, lkv=lc, dq=dq, dk=dkc, dv=dvc, accumulate=True)
                 if not ctx.has_coarse:
-                    dk_c, dEk = _compress_backward(dkc, k, k_proj_mat, cfg["proj_segment_len"], block_size)
-                    dv_c, dEv = _compress_backward(dvc, v, v_proj_mat, cfg["proj_segment_len"], block_size)
-                    dk += dk_c
-                    dv += dv_c
+                    _, dEk = _compress_backward(dkc, k, k_proj_mat, cfg["proj_segment_len"], block_size, dx=dk)
+                    _, dEv = _compress_backward(dvc, v, v_proj_mat, cfg["proj_segment_len"], block_size, dx=dv)
         qd, kd, vd, kcd, vcd, ekd, evd, gwd, gbd = ctx.dtypes
 
         def cast(t, dt):
