@@ -5,8 +5,9 @@
 Headline (``value``, ``ms_per_step``, ``roofline``, ``cpu_baseline``): cfg 2, the Wan-1.3B chunk.
 A step is one ``hsa_forward`` call (routing + sparse branch + elu(x)+1 linear branch + fusion) on
 seeded synthetic inputs already resident in HBM: B=1, H=12 (8 sparse heads with per-head top-k from
-{8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16. The timed steps replay
-the call captured once in a HIP graph (the eager per-call time is reported beside it). ``value`` is
+{8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16. The timed steps are
+plain eager calls, K of them between two device synchronizations (the same call captured once in a
+HIP graph and replayed is reported beside it). ``value`` is
 the effective sparse TFLOP/s of the whole call (useful sparse FLOP / call time); ``roofline`` is the
 sparse kernel's own rate, timed with HIP events on the stream it runs on. ``hbm_bound_launches``
 gives the HBM rate of the memory-bound launches of the same call (Q/K block pooling, elu1 state,
@@ -203,10 +204,11 @@ def bench_cfg2(args, dev):
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     # The same call captured once in a HIP graph and replayed (a serving loop): the kernels and their
-    # inputs are identical; the replay drops the per-call Python and launch overhead.
-    ms_per_step = graph_time_ms(step, args.warmup, args.steps)
+    # inputs are identical; the replay drops the per-call host work but runs the two streams' kernels
+    # one after the other.
+    graph_ms = graph_time_ms(step, args.warmup, args.steps)
 
     cached = bench_cfg2_cached_sums(args, cfg, kw, step)
 
@@ -227,10 +229,10 @@ def bench_cfg2(args, dev):
         sparse_only()
     sparse_ms = stream_time_ms(sparse_only, max(args.steps, 20))
     achieved = useful_flop / (sparse_ms * 1e-3) / 1e12
-    log(f"cfg2: {ms_per_step:.4f} ms/call (graph replay; eager {eager_ms:.4f}), sparse kernel {sparse_ms:.4f} ms = "
+    log(f"cfg2: {ms_per_step:.4f} ms/call (eager; graph replay {graph_ms:.4f}), sparse kernel {sparse_ms:.4f} ms = "
         f"{achieved:.1f} TFLOP/s")
     hbm = memory_legs(cfg, plan, route, gate, dev, max(args.steps, 20))
-    return cfg, proj, dict(ms_per_step=ms_per_step, eager_ms=eager_ms, useful_flop=useful_flop, tile_flop=tile_flop,
+    return cfg, proj, dict(ms_per_step=ms_per_step, graph_ms=graph_ms, useful_flop=useful_flop, tile_flop=tile_flop,
                            sparse_ms=sparse_ms, achieved=achieved, hbm=hbm, cached=cached)
 
 
@@ -751,9 +753,9 @@ def main():
                                "8 sparse heads top-k from {8,16,32} + 4 elu1 linear heads",
                    "topk": cfg["topk"], "head_modes": cfg["head_modes"], "seed": args.seed},
         "hsa_fwd_ms_per_chunk": round(c2["ms_per_step"], 4),
-        "hsa_fwd_ms_per_chunk_eager": round(c2["eager_ms"], 4),
-        "timing": "ms_per_step: the hsa_forward call captured once in a HIP graph and replayed; "
-                  "hsa_fwd_ms_per_chunk_eager: the same call launched eagerly from Python",
+        "hsa_fwd_ms_per_chunk_graph": round(c2["graph_ms"], 4),
+        "timing": "ms_per_step: eager hsa_forward calls timed between two device synchronizations; "
+                  "hsa_fwd_ms_per_chunk_graph: the same call captured once in a HIP graph and replayed",
         "hsa_fwd_ms_per_chunk_cached_key_sums": c2["cached"],
         "sparse_kernel_ms": round(c2["sparse_ms"], 4),
         "sparse_useful_gflop": round(c2["useful_flop"] / 1e9, 3),
