@@ -46,7 +46,9 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the eager call reaches its steady time after ~100 calls (0.144 ms over calls 20-70, 0.131 over
+    # calls 170-220 in one run): the untimed warmup covers that
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-calls", type=int, default=12)
