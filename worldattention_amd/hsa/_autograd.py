@@ -207,16 +207,19 @@ class _HSA(torch.autograd.Function):
             qp, kp, key_args = pool_for_routing(q, k, q_len, kv_len, block_size, st,
                                                 k_block_sums=cfg["k_block_sums"], k_pooled=cfg["k_pooled"])
             visits = None
+            # the routing launch also zeroes the arrival counters of the sparse launch
+            arrivals = torch.empty((bsz * len(plan.sparse) * nq,), dtype=torch.int32, device=dev)
             if routing == "gini":
                 route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=cfg["tau_min"],
-                                  tau_max=cfg["tau_max"], heads=st, **key_args)
+                                  tau_max=cfg["tau_max"], heads=st, clear=arrivals, **key_args)
             else:
                 ks = _per_head_k(topk, heads)
-                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st, **key_args)
+                route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st, clear=arrivals,
+                                  **key_args)
                 visits = [min(ks[h], nkv) for h in plan.sparse]
             _, lse_s = bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size,
                                    layout="blhd", heads=st, out=out if split else sparse, lq=q_len, lkv=kv_len,
-                                   want_lse=True, visits=visits, attn_round_bf16=split)
+                                   want_lse=True, visits=visits, attn_round_bf16=split, arrivals=arrivals)
         if split:
             if plan.linear:  # gate and gated output of the linear heads; the sparse heads are written
                 lin_modes = _lib.head_list([MODE_LINEAR if h in plan.linear else 0 for h in range(heads)], dev)
