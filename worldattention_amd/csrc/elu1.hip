@@ -840,10 +840,17 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv_kernel(Elu1BwdParams p) {
 // own, without barriers: K and V rows load straight into MFMA fragments, the next group's loads
 // go out once the last column tile's products have read the fragments (before that tile's stores:
 // on gfx9 loads and stores share one counter, so a load issued after a store waits for it), and
-// each lane writes 4 channels of its token per store. The dK factor elu1'(k) comes from the K
+// each lane writes 8 channels (16 bytes) of its token per store, the two lanes of a token having
+// swapped halves (with 8-byte stores the stores cost ~20 us of a ~46 us launch at cfg 5). The dK factor elu1'(k) comes from the K
 // fragments: the two lanes of a token exchange the halves of their 16-byte chunks. (Holding the
 // next group's fragments in registers for the whole group needs ~320 registers: one wave per
 // SIMD, slower.)
+// value of lane ^ 32 (g = lane >> 5): the gfx950 half-wave swap
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t v, int g) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(v, v, false, false);  // {upper <- lane - 32, lower <- lane + 32}
+  return g ? sw[0] : sw[1];
+}
+
 template <int D>
 __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
   constexpr int DC = D / 16, DT = D / 32;
@@ -874,8 +881,8 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
   stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
   for (int e = tid; e < D; e += 256) s_z[e] = p.dz[bh * D + e];
   __syncthreads();
-  bf16_t* dkb = (bf16_t*)p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + 4 * g;
-  bf16_t* dvb = (bf16_t*)p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + 4 * g;
+  bf16_t* dkb = (bf16_t*)p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh;
+  bf16_t* dvb = (bf16_t*)p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh;
 #pragma unroll 1
   for (; gi < g_end; gi += 4) {
     const int t = gi * 32 + l32;
@@ -911,21 +918,45 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
       // after the last column tile's products the fragments are dead: the next group's loads go out
       // before this tile's stores
       if (jt == DT - 1 && gi + 4 < g_end) load_group(gi + 4, kf, vf);
-      if (ok) {
+      // this lane's bf16 results: channels 32 jt + 8 rq + 4 g .. + 3 of its token, as two u32 each
+      uint32_t ku[4][2], vu[4][2];
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int e0 = 32 * jt + 8 * rq + 4 * g;
-          const f32x4 z4 = *(const f32x4*)(s_z + e0);
-          const bf16x8 kc = k01[rq >> 1];  // fragments 2 jt, 2 jt + 1
-          bf16x4 ok4, ov4;
+      for (int rq = 0; rq < 4; ++rq) {
+        const int e0 = 32 * jt + 8 * rq + 4 * g;
+        const f32x4 z4 = *(const f32x4*)(s_z + e0);
+        const bf16x8 kc = k01[rq >> 1];  // fragments 2 jt, 2 jt + 1
+        bf16x4 ok4, ov4;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float kv = (float)kc[4 * (rq & 1) + i];
-            ok4[i] = (bf16_t)((dk[rq * 4 + i] + z4[i]) * elu1_grad(kv));
-            ov4[i] = (bf16_t)dv[rq * 4 + i];
-          }
-          *(bf16x4*)(dkb + (int64_t)t * p.dk_st + 32 * jt + 8 * rq) = ok4;
-          *(bf16x4*)(dvb + (int64_t)t * p.dv_st + 32 * jt + 8 * rq) = ov4;
+        for (int i = 0; i < 4; ++i) {
+          const float kv = (float)kc[4 * (rq & 1) + i];
+          ok4[i] = (bf16_t)((dk[rq * 4 + i] + z4[i]) * elu1_grad(kv));
+          ov4[i] = (bf16_t)dv[rq * 4 + i];
+        }
+        const u32x2 k2 = __builtin_bit_cast(u32x2, ok4), v2 = __builtin_bit_cast(u32x2, ov4);
+        ku[rq][0] = k2[0]; ku[rq][1] = k2[1];
+        vu[rq][0] = v2[0]; vu[rq][1] = v2[1];
+      }
+      // The two lanes of a token swap halves so that each stores 16 bytes (8 consecutive channels):
+      // of chunks 2 kk and 2 kk + 1, lane g keeps chunk 2 kk + g and sends its partner its own four
+      // channels of chunk 2 kk + 1 - g. (Every lane swaps; only the store depends on the token.)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        uint32_t out_k[4], out_v[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t sk = g ? ku[2 * kk][j] : ku[2 * kk + 1][j], sv = g ? vu[2 * kk][j] : vu[2 * kk + 1][j];
+          const uint32_t mk = g ? ku[2 * kk + 1][j] : ku[2 * kk][j], mv = g ? vu[2 * kk + 1][j] : vu[2 * kk][j];
+          const uint32_t rk = lane_xor32(sk, g), rv = lane_xor32(sv, g);
+          // channels 0..3 of the chunk come from the g = 0 lane, 4..7 from the g = 1 lane
+          out_k[j] = g ? rk : mk;
+          out_k[2 + j] = g ? mk : rk;
+          out_v[j] = g ? rv : mv;
+          out_v[2 + j] = g ? mv : rv;
+        }
+        if (ok) {
+          const int e = 32 * jt + 8 * (2 * kk + g);
+          *(u32x4*)(dkb + (int64_t)t * p.dk_st + e) = u32x4{out_k[0], out_k[1], out_k[2], out_k[3]};
+          *(u32x4*)(dvb + (int64_t)t * p.dv_st + e) = u32x4{out_v[0], out_v[1], out_v[2], out_v[3]};
         }
       }
       // rotate so the next column tile's fragments sit at 0 and 1 (static register indices: a
