@@ -1,10 +1,12 @@
 // One call for the HSA forward of split heads (host code). It runs the same entry points, with the
 // same arguments, as the Python orchestration of hsa_forward does for heads that take one branch
-// each (top-k sparse heads, elu(x)+1 linear heads): the elu1 state pass and the gated readout of
-// the linear heads; block pooling of the sparse heads' queries and keys, top-k routing (which also
-// clears the sparse launch's arrival counters) and the block-sparse launch, from
-// one workspace, the linear heads on a side stream of the library's. An eager call then crosses
-// from Python once instead of ~20 times (allocations, argument structs and launches).
+// each (top-k sparse heads, elu(x)+1 linear heads), from one workspace:
+//  * the elu1 state pass and the gated readout of the linear heads, on a side stream of the
+//    library's;
+//  * block pooling of the sparse heads' queries and keys, top-k routing (which also clears the
+//    sparse launch's arrival counters) and the block-sparse launch, on the caller's stream.
+// An eager call then crosses from Python once instead of ~20 times (allocations, argument structs
+// and launches).
 //
 // Reference semantics: wan/modules/hsa/attention.py:153-259 (hsa_attention) with the north-star
 // head modes; each step follows the entry point it calls.
@@ -43,10 +45,19 @@ int side_stream(hipStream_t stream, SideStream** out) {
     if ((e = hipStreamIsCapturing(stream, &st)) != hipSuccess)
       return wa_fail((int)e, "wa_hsa_fwd: hipStreamIsCapturing: %s", hipGetErrorString(e));
     if (st != hipStreamCaptureStatusNone) return WA_OK;
-    if ((e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&s.join, hipEventDisableTiming)) != hipSuccess)
+    // published only once all three exist (a failed call leaves the slot empty for the next)
+    hipStream_t st_new = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if ((e = hipStreamCreateWithFlags(&st_new, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreateWithFlags(&fork, hipEventDisableTiming)) != hipSuccess ||
+        (e = hipEventCreateWithFlags(&join, hipEventDisableTiming)) != hipSuccess) {
+      if (fork) (void)hipEventDestroy(fork);
+      if (st_new) (void)hipStreamDestroy(st_new);
       return wa_fail((int)e, "wa_hsa_fwd: side stream: %s", hipGetErrorString(e));
+    }
+    s.fork = fork;
+    s.join = join;
+    s.stream = st_new;
   }
   *out = &s;
   return WA_OK;
