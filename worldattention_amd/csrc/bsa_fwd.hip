@@ -9,22 +9,27 @@
 // independent of scheduling (one launch, no merge kernel).
 //
 // Unit kernel (one workgroup = BS/32 waves; wave w owns query rows [32w, 32w+32) of the block).
-// Per visited key block the K and V tiles are streamed global -> LDS with direct-to-LDS loads
-// (no register staging), into two separate buffers so that the next K tile streams in while the
-// softmax and the PV product of the current one run. Products use the transposed formulation
+// The visited key blocks are 64-key steps whose K and V tiles stream global -> LDS with
+// direct-to-LDS loads (no register staging) into two stages per tensor. Products use the
+// transposed formulation
 //     S^T[key, q] = K[key, :] . Q[q, :]         (A = K from LDS, B = Q^T in registers)
 //     O^T[d, q]  += V^T[d, key] . P^T[key, q]   (A = V^T by transpose-reads of row-major V)
 // so each lane owns one query column: the row max / row sum need one exchange with lane^32 and
-// the probabilities feed the PV product straight from the QK accumulator registers.
+// the probabilities feed the PV product straight from the QK accumulator registers. The step loop
+// is software-pipelined in 32-key halves: each slot interleaves the softmax of one half with the
+// QK product of the next and the PV product of the previous one inside the wave.
 //
-// LDS layouts (no padding; XOR swizzles on 16-byte chunks keep every read conflict-free):
+// LDS layouts (no padding; XOR swizzles on 16-byte chunks):
 //   K[key][chunk ^ (key & 15)]      read with ds_read_b128 (16 lanes = 16 keys, one chunk; D = 128)
 //   V[key][chunk ^ 2*(key & 3)]      read with ds_read_b64_tr_b16 (16 lanes = 4 keys x 32 bytes)
+// Each 16-lane read phase touches distinct chunk slots, but the counters still see bank conflicts:
+// 1.3 conflict cycles per LDS instruction in the kernel before the pipelined loop.
 //
 // Reference semantics: wan/modules/hsa/block_sparse_triton.py:67-139 (online softmax, partial
 // trailing block mask, empty list -> 0, LSE output) and block_sparse_torch.py:16-64 (id clamping,
 // listed order, duplicates attended twice, fp32 math).
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "tile.h"
@@ -59,12 +64,6 @@ struct FwdParams {
   float* part_lse;       // [rows * max_splits][BS] log2-sum-exp of the partials
   int* arrivals;         // [rows] units of the row done so far (zeroed by the launch)
 };
-
-// Workgroup barrier without the global-memory fence of __syncthreads (which would wait for the
-// in-flight K/V tile loads). LDS reads before it have completed: their results were consumed.
-__device__ __forceinline__ void wa_lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 // `irow` numbers rows by global head, (b * H + h) * Nq + i: the layout of index / num. Units and
 // workspace slots number rows by head slot instead, (b * n_heads + slot) * Nq + i.
@@ -118,15 +117,6 @@ struct NextTile {
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;               // rows per wave instruction (4 or 8)
   static constexpr int NI = 64 / (RPI * NW);         // instructions per wave per tensor
-  __amdgpu_buffer_rsrc_t k_rs, v_rs;                 // start at the tile's first row; empty past the list
-  bf16_t* k_lds; bf16_t* v_lds;
-  int k_off[NI], v_off[NI];                          // this lane's byte offset per instruction
-  __device__ __forceinline__ void k(int i, int w, int) const {
-    if (i < NI) lds_dma16(k_rs, k_lds + (i * NW + w) * RPI * D, k_off[i]);
-  }
-  __device__ __forceinline__ void v(int i, int w, int) const {
-    if (i < NI) lds_dma16(v_rs, v_lds + (i * NW + w) * RPI * D, v_off[i]);
-  }
 };
 
 // Writes one query column's result (lane = query qi, accumulator layout d = 32t + 8(r/4) + 4g +
@@ -232,153 +222,203 @@ __device__ __forceinline__ void write_output(const FwdParams& p, const f32x16 (&
   }
 }
 
-// Step cursor over the unit's visits: a visit of a BS = 128 block is two 64-key steps (the second
-// only when the block has more than 64 real keys), of a BS = 64 block one step. All fields are
-// wave-uniform.
-struct Cursor {
-  uint64_t todo;  // visits not yet started (bit = lane holding the visit)
-  int j, real;    // current block and its real key count
-  int half;       // current 64-key step within the block
-  bool valid;
+// ---------------------------------------------------------------------------------------------
+// Software-pipelined step loop. A 64-key step is two 32-key halves, and the loop runs in "slots",
+// one half each. Slot (block b, half h) does three independent pieces of work:
+//   * the softmax of the half-step whose scores the previous slot produced: S[1 - h] -> the
+//     probability chunks P[2(1-h)], P[2(1-h)+1] and the slot's row sum;
+//   * the QK product of half h of step b (K stage of step b) -> S[h];
+//   * the PV product of half h of step b - 1 (V stage of step b - 1) with P[2h], P[2h+1];
+// plus, in the block's first slot, the tile loads of the next block (K of step b + 1, V of step b:
+// both stages were last read in block b - 1, so the loads go out a whole block ahead). The softmax (~56 VALU instructions at D = 128)
+// interleaves with the 16 products inside the wave, so the SIMD issues VALU work while the MFMA
+// pipe is busy instead of after it.
+// ---------------------------------------------------------------------------------------------
+
+// Direct-to-LDS 16-byte load through the compiler's builtin: the scheduler sees a memory load (LDS
+// reads move freely around it) and the wait-count pass tracks it per LDS array. Every ring stage is
+// an array of its own and every access names its stage statically, so a read of one stage never
+// waits for loads into another; the kernel still orders loads across waves itself (s_waitcnt
+// vmcnt(0) + s_barrier at the top of each block).
+__device__ __forceinline__ void pipe_dma16(__amdgpu_buffer_rsrc_t rs, bf16_t* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Instruction-group order of one slot: after a few leading LDS reads, each product is followed by
+// up to DSN LDS reads and VAN VALU instructions, and every VMEVERY-th product by one tile load.
+template <int I, int N, int DSN, int VAN, int VMEVERY>
+__device__ __forceinline__ void pipe_sched() {
+  if constexpr (I < N) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, DSN, 0);  // LDS read
+    __builtin_amdgcn_sched_group_barrier(0x002, VAN, 0);  // VALU
+    if constexpr (VMEVERY > 0 && I % VMEVERY == 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
+    pipe_sched<I + 1, N, DSN, VAN, VMEVERY>();
+  }
+}
+
+// Tile loads of one slot: NI direct-to-LDS loads of a tensor's next tile into stage `lds`.
+struct PipeLoad {
+  __amdgpu_buffer_rsrc_t rs;
+  bf16_t* lds;
 };
 
-template <int BS>
-__device__ __forceinline__ void cursor_next(Cursor& c, int my_j, int my_real) {
-  if (BS == 128 && c.valid && c.half == 0 && c.real > 64) {
-    c.half = 1;
-    return;
+// One slot (see above) of a wave that owns QT 32-query tiles. SMH: half whose softmax runs (1 - the
+// product half). SM / QK / PV / LD switch the pieces on for the pipeline's first and last blocks.
+// With QT = 2 every K and V fragment read from LDS feeds two products. rs[qt]: the slot's row sum
+// of exponentials of tile qt (this lane's 16 keys).
+template <int D, int NW, int QT, int SMH, bool SM, bool QK, bool PV, bool LD>
+__device__ __forceinline__ void pipe_slot(f32x16 (&S)[2][QT], bf16x8 (&P)[4][QT], f32x16 (&oacc)[QT][D / 32],
+                                          const bf16x8 (&qf)[QT][D / 16], const bf16_t* kst, const bf16_t* vst,
+                                          const int (&k_rd)[D / 16], const int (&v_rd)[2], const float (&neg_m)[QT],
+                                          float scale_log2, const PipeLoad& ldk, const int (&koff)[NextTile<D, NW>::NI],
+                                          const PipeLoad& ldv, const int (&voff)[NextTile<D, NW>::NI], int w,
+                                          float (&rs)[QT]) {
+  constexpr int H = SMH ^ 1, DC = D / 16, DT = D / 32;
+  constexpr int NI = NextTile<D, NW>::NI, RPI = NextTile<D, NW>::RPI;
+  // operands from LDS: K rows 32 H + l32 (A of S^T = K Q^T), V^T of keys 32 H .. +32 (A of O^T += V^T P^T)
+  bf16x8 kf[DC];
+  if constexpr (QK) {
+#pragma unroll
+    for (int c = 0; c < DC; ++c) kf[c] = *(const bf16x8*)(kst + k_rd[c] + H * 32 * D);
   }
-  if (c.todo) {
-    const int v = __builtin_ctzll(c.todo);
-    c.todo &= c.todo - 1;
-    c.j = __builtin_amdgcn_readlane(my_j, v);
-    c.real = __builtin_amdgcn_readlane(my_real, v);
-    c.half = 0;
-    c.valid = true;
-  } else {
-    c.valid = false;
+  bf16x8 vf[2][DT];
+  if constexpr (PV) {
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const s16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              WA_LDS4(vst + v_rd[t & 1] + (16 * (2 * H + cc) + 8 * hf) * D + (t >> 1) * 64));
+          const bf16x4 vb4 = __builtin_bit_cast(bf16x4, vv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vf[cc][t][4 * hf + e] = vb4[e];
+        }
+      }
+    }
+  }
+  if constexpr (QK) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) S[H][qt] = wa_mfma32(kf[0], qf[qt][0], f32x16{});
+#pragma unroll
+    for (int c = 1; c < DC; ++c) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) S[H][qt] = wa_mfma32(kf[c], qf[qt][c], S[H][qt]);
+    }
+  }
+  if constexpr (PV) {
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) oacc[qt][t] = wa_mfma32(vf[cc][t], P[2 * H + cc][qt], oacc[qt][t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) rs[qt] = 0.f;
+  if constexpr (SM) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float r0 = 0.f, r1 = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(S[SMH][qt][r], scale_log2, neg_m[qt]));
+        if (r & 1) r1 += pv;
+        else r0 += pv;
+        P[2 * SMH + (r >> 3)][qt][r & 7] = (bf16_t)pv;
+      }
+      rs[qt] = r0 + r1;
+    }
+  }
+  if constexpr (LD) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      pipe_dma16(ldk.rs, ldk.lds + (i * NW + w) * RPI * D, koff[i]);
+      pipe_dma16(ldv.rs, ldv.lds + (i * NW + w) * RPI * D, voff[i]);
+    }
+  }
+  constexpr int NM = QT * ((QK ? DC : 0) + (PV ? 2 * DT : 0));
+  constexpr int NDS = (QK ? DC : 0) + (PV ? 4 * DT : 0);
+  if constexpr (NM > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+    pipe_sched<0, NM, (NDS + NM - 1) / NM, 4, LD ? (NM / (2 * NI) > 0 ? NM / (2 * NI) : 1) : 0>();
   }
 }
 
-// One 64-key step of the online softmax on LDS buffer (kb, vb): S^T = K Q^T, lazily rescaled
-// exponentials, O^T += V^T P^T. `real` = real keys of this step (1..64). The next step's tile
-// stream (`nt`) is issued in slices between the products.
-template <int D, int NW>
-__device__ __forceinline__ void attend_step(const bf16_t* kb, const bf16_t* vb, const int (&k_rd)[D / 16],
-                                            const int (&v_rd)[2], const bf16x8 (&qf)[D / 16],
-                                            f32x16 (&oacc)[D / 32], float& m_i, float& l_i, int real, int g,
-                                            float scale_log2, const NextTile<D, NW>& nt, int w, int lane) {
-  constexpr int KT = 2, DC = D / 16, DT = D / 32, PC = 4;
-  constexpr int NI = NextTile<D, NW>::NI;
-  f32x16 sacc[KT];
+// Keys of half KH of a step at or past `real` get score -inf (probability 0): lane (l32, g) holds
+// keys 32 KH + 8 (r / 4) + 4 g + r % 4 in S[r].
+template <int KH, int QT>
+__device__ __forceinline__ void pipe_mask(f32x16 (&s)[QT], int real, int g) {
+  const int rr = real - 32 * KH - 4 * g;
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) sacc[kt] = f32x16{};
-  bf16x8 ka[KT], kn[KT];
+  for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-  for (int kt = 0; kt < KT; ++kt) ka[kt] = *(const bf16x8*)(kb + k_rd[0] + kt * 32 * D);
-#pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    if (c + 1 < DC) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) kn[kt] = *(const bf16x8*)(kb + k_rd[c + 1] + kt * 32 * D);
-    }
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) sacc[kt] = wa_mfma32(ka[kt], qf[c], sacc[kt]);
-    if (c % (DC / NI > 0 ? DC / NI : 1) == 0) nt.k(c / (DC / NI > 0 ? DC / NI : 1), w, lane);
-    if (c + 1 < DC) {
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) ka[kt] = kn[kt];
-    }
+    for (int r = 0; r < 16; ++r) s[qt][r] = 8 * (r >> 2) + (r & 3) >= rr ? -INFINITY : s[qt][r];
   }
-  if (DC < NI) {
+}
+
+// A slot whose exponentials failed the sum check: each tile's m_i moves to the running max over its
+// half-step s (every half-step the pipeline starts with holds a real key, so the max is finite;
+// where it does not exceed m_i the factor is 1 and nothing changes), the output accumulators
+// (which already include this slot's PV product) and l_i are rescaled, and the half's
+// probabilities P[2 PH], P[2 PH + 1] and row sums are recomputed.
+template <int D, int QT, int PH>
+__device__ __forceinline__ void pipe_rescale(const f32x16 (&s)[QT], bf16x8 (&P)[4][QT], f32x16 (&oacc)[QT][D / 32],
+                                             float (&m_i)[QT], float (&l_i)[QT], float (&rs)[QT], float scale_log2) {
 #pragma unroll
-    for (int i = DC; i < NI; ++i) nt.k(i, w, lane);
-  }
-  if (real < 64) {
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key >= real) sacc[kt][r] = -INFINITY;
-      }
-    }
-  }
-  // Exponentials against the running max m_i, which may lag the scores: the step is accepted when
-  // every lane's sum of exponentials is at most 2^16 (so is each exponential: far from fp32 / bf16
-  // overflow). Otherwise (the first step, or scores more than ~11 above m_i) m_i moves to the step
-  // max, the accumulators are rescaled and the exponentials recomputed. The final normalization
-  // uses the same m_i, so the result does not depend on how far m_i lags.
-  float rs;
-  bf16x8 pb[PC];
-  auto exps = [&]() {
-    rs = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[kt][r], scale_log2, -m_i));
-        rs += pv;
-        pb[kt * 2 + (r >> 3)][r & 7] = (bf16_t)pv;
-      }
-    }
-  };
-  exps();
-  if (__any(!(rs <= 65536.f))) {
+  for (int qt = 0; qt < QT; ++qt) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kt][r]);
-    }
-    // every step has a real key, so mx is finite; on the first step m_i = -inf and alpha = 0
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qt][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
-    const float m_new = fmaxf(mx, m_i);
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-    l_i *= alpha;
-    m_i = m_new;
+    const float m_new = fmaxf(mx, m_i[qt]);
+    const float alpha = __builtin_amdgcn_exp2f(m_i[qt] - m_new);
+    l_i[qt] *= alpha;
+    m_i[qt] = m_new;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-    exps();
-  }
-  l_i += rs;
-  // V of this step: everything but the next step's K slices (the last NI loads) has landed, and
-  // after the barrier every wave's has.
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NI) : "memory");
+    for (int t = 0; t < D / 32; ++t) oacc[qt][t] *= alpha;
+    float r0 = 0.f, r1 = 0.f;
 #pragma unroll
-  for (int c = 0; c < PC; ++c) {
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      bf16x8 a;
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const s16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            WA_LDS4(vb + v_rd[t & 1] + (16 * c + 8 * hf) * D + (t >> 1) * 64));
-        const bf16x4 vb4 = __builtin_bit_cast(bf16x4, vv);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a[4 * hf + e] = vb4[e];
-      }
-      oacc[t] = wa_mfma32(a, pb[c], oacc[t]);
+    for (int r = 0; r < 16; ++r) {
+      const float pv = __builtin_amdgcn_exp2f(fmaf(s[qt][r], scale_log2, -m_i[qt]));
+      if (r & 1) r1 += pv;
+      else r0 += pv;
+      P[2 * PH + (r >> 3)][qt][r & 7] = (bf16_t)pv;
     }
-    if (NI >= PC) {
-#pragma unroll
-      for (int i = c * (NI / PC); i < (c + 1) * (NI / PC); ++i) nt.v(i, w, lane);
-    } else if (c < NI) {
-      nt.v(c, w, lane);
-    }
+    rs[qt] = r0 + r1;
   }
 }
 
-template <int D, int BS>
-__global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2)))
+template <int QT>
+__device__ __forceinline__ bool pipe_check(const float (&rs)[QT]) {
+  bool bad = false;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) bad |= !(rs[qt] <= 65536.f);
+  return __any(bad);
+}
+
+// Unit kernel. A workgroup of NW = BS / (32 QT) waves runs one unit; wave w owns the QT 32-query
+// tiles vw = QT w .. QT w + QT - 1 (query rows [32 vw, 32 vw + 32) of the block). QT = 1: four
+// waves (BS = 128), two workgroups per CU sharing its SIMDs; QT = 2: two waves of 64 queries with
+// up to 512 registers each (one wave per SIMD), so every K / V fragment read feeds two products.
+template <int D, int BS, int QT>
+__global__ void __launch_bounds__(2 * BS / QT) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1)))
 bsa_unit_kernel(FwdParams p) {
-  constexpr int NW = BS / 32;   // waves; wave w owns query rows [32w, 32w + 32)
+  constexpr int NW = BS / (32 * QT);
+  constexpr int NVW = NW * QT;  // 32-query tiles per workgroup
   constexpr int DC = D / 16, DT = D / 32;
   constexpr int TILE = 64 * D;  // elements of one K (or V) step tile
-  // Two K and two V step tiles (64 KiB at D = 128: two workgroups per CU), fed by inline-assembly
-  // direct-to-LDS loads that the compiler does not track (the kernel orders them itself).
-  __shared__ __attribute__((aligned(1024))) bf16_t kr[2 * TILE];
-  __shared__ __attribute__((aligned(1024))) bf16_t vr[2 * TILE];
+  // Two K and two V step tiles (64 KiB at D = 128: two workgroups per CU), one array per stage, fed
+  // by direct-to-LDS loads; and each wave's step table (64 steps x (first row, real keys)).
+  __shared__ __attribute__((aligned(1024))) bf16_t ks0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t ks1[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t vs0[TILE];
+  __shared__ __attribute__((aligned(1024))) bf16_t vs1[TILE];
+  __shared__ int steptab[NW][64][2];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -415,15 +455,21 @@ bsa_unit_kernel(FwdParams p) {
     const int lo1 = split * p.split;
     if (split > 0 && lane < min((int)p.index_width - lo1, 64)) j1 = lrow[lo1 + lane];
   }
-  const int qi = qb * BS + w * 32 + l32;
-  const bool q_ok = qi < p.Lq;
-  // Q^T fragments (B operand): lane holds Q[qi, 16c + 8g .. +8).
-  const bf16_t* qrow = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok ? qi : 0) * p.q_st;
-  bf16x8 qf[DC];
+  // Q^T fragments (B operand): lane holds Q[qi, 16c + 8g .. +8) of each of its tiles.
+  int qi[QT];
+  bool q_ok[QT];
+  const bf16_t* qrow[QT];
+  bf16x8 qf[QT][DC];
 #pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    bf16x8 t = *(const bf16x8*)(qrow + c * 16 + g * 8);
-    qf[c] = q_ok ? t : bf16x8{};
+  for (int qt = 0; qt < QT; ++qt) {
+    qi[qt] = qb * BS + (w * QT + qt) * 32 + l32;
+    q_ok[qt] = qi[qt] < p.Lq;
+    qrow[qt] = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok[qt] ? qi[qt] : 0) * p.q_st;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      bf16x8 t = *(const bf16x8*)(qrow[qt] + c * 16 + g * 8);
+      qf[qt][c] = q_ok[qt] ? t : bf16x8{};
+    }
   }
 
   const int n = p.index ? max(0, min(nraw, (int)p.index_width)) : nraw;
@@ -436,13 +482,12 @@ bsa_unit_kernel(FwdParams p) {
   const bf16_t* kbase = p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
   const bf16_t* vbase = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
 
-  // List entries one per lane, read once: the loop fetches them with readlane and issues no memory
-  // reads besides the tile streams. A row of at most 64 visits is loaded whole and sorted by block
-  // id, and split s of the row's ns units takes the sorted positions s, s + ns, s + 2 ns, ...: every
-  // unit of a head (they run together on one XCD) then sweeps the whole key range in step with the
-  // others, so the units that list a block fetch it at about the same time and share it in L2.
-  // The visit order only changes the summation order. Longer rows keep list order, one contiguous
-  // slice per unit.
+  // List entries one per lane, read once. A row of at most 64 visits is loaded whole and sorted by
+  // block id, and split s of the row's ns units takes the sorted positions s, s + ns, s + 2 ns, ...:
+  // every unit of a head (they run together on one XCD) then sweeps the whole key range in step
+  // with the others, so the units that list a block fetch it at about the same time and share it in
+  // L2. The visit order only changes the summation order. Longer rows keep list order, one
+  // contiguous slice per unit.
   const bool whole = n <= 64;
   const int lo = whole ? 0 : s_begin;
   const int take = whole ? n : s_end - s_begin;
@@ -451,12 +496,31 @@ bsa_unit_kernel(FwdParams p) {
   if (whole) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
   const bool mine = whole ? lane < n && lane % ns == split : lane < take;
   const int my_real = mine ? block_real(p, my_j, BS) : 0;
-  Cursor cur{__ballot(mine && my_real > 0), 0, 0, 0, false};
-  cursor_next<BS>(cur, my_j, my_real);
 
-  // tile streams: this lane's loop-invariant chunk offsets; each tile gets a buffer descriptor that
-  // starts at its first row and ends at the slab's end (rows past the slab read zeros), and a
-  // step past the end of the list an empty one (zeros, no memory traffic)
+  // Step table: this unit's visits in processing order (the lanes with `mine`), each one 64-key
+  // step or, for a block of more than 64 real keys, two. Lane s of tab_* describes step s: the byte
+  // offsets of its first K and V rows in the head's slabs and its real key count (1..64). A unit
+  // has at most 64 steps (split <= 32 visits of 128-key blocks, or 64 of 64-key blocks).
+  const uint64_t vis = __ballot(mine && my_real > 0);
+  const uint64_t two = BS == 128 ? __ballot(mine && my_real > 64) : 0ull;
+  const int T = __popcll(vis) + __popcll(two);
+  if ((vis >> lane) & 1) {
+    const uint64_t below = (1ull << lane) - 1;
+    const int first = __popcll(vis & below) + __popcll(two & below);
+    steptab[w][first][0] = my_j * BS;
+    steptab[w][first][1] = min(my_real, 64);
+    if ((two >> lane) & 1) {
+      steptab[w][first + 1][0] = my_j * BS + 64;
+      steptab[w][first + 1][1] = my_real - 64;
+    }
+  }
+  const int tab_row = lane < T ? steptab[w][lane][0] : 0;
+  const int tab_real = lane < T ? steptab[w][lane][1] : 0;
+  const int tab_koff = tab_row * (int)p.k_st * 2, tab_voff = tab_row * (int)p.v_st * 2;
+
+  // Tile loads: this lane's loop-invariant chunk offsets; each tile gets a buffer descriptor that
+  // starts at its first row and ends at the slab's end (rows past the slab read zeros), and a step
+  // past the end of the table an empty one (zeros, no memory traffic).
   using NT = NextTile<D, NW>;
   int k_off[NT::NI], v_off[NT::NI];
 #pragma unroll
@@ -465,41 +529,23 @@ bsa_unit_kernel(FwdParams p) {
     k_off[i] = (int)(row * p.k_st + (pos ^ k_swizzle<D>(row)) * 8) * 2;
     v_off[i] = (int)(row * p.v_st + (pos ^ v_swizzle(row)) * 8) * 2;
   }
-  auto tile_rs = [&](const Cursor& c, bool is_k) {
-    const bf16_t* base = is_k ? kbase : vbase;
-    int64_t off = 0;
-    int bytes = 0;
-    if (c.valid) {
-      off = (int64_t)(c.j * BS + 64 * c.half) * (is_k ? p.k_st : p.v_st);
-      bytes = (is_k ? p.k_slab_bytes : p.v_slab_bytes) - (int)(off * 2);
-    }
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + off), (short)0, bytes, WA_BUF_DWORD3);
+  auto tile_rs = [&](int s, bool is_k) {
+    const int off = __builtin_amdgcn_readlane(is_k ? tab_koff : tab_voff, s & 63);
+    const bool ok = s < T;
+    const char* base = (const char*)(is_k ? kbase : vbase) + (ok ? off : 0);
+    const int bytes = ok ? (is_k ? p.k_slab_bytes : p.v_slab_bytes) - off : 0;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, WA_BUF_DWORD3);
   };
-  auto tiles = [&](bf16_t* kl, const Cursor& ck, bf16_t* vl, const Cursor& cv) {
-    NT nt;
-    nt.k_rs = tile_rs(ck, true);
-    nt.v_rs = tile_rs(cv, false);
-    nt.k_lds = kl;
-    nt.v_lds = vl;
+  auto load_tile = [&](int s, bool is_k, bf16_t* lds) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rs(s, is_k);
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) {
-      nt.k_off[i] = k_off[i];
-      nt.v_off[i] = v_off[i];
-    }
-    return nt;
+    for (int i = 0; i < NT::NI; ++i) pipe_dma16(rs, lds + (i * NW + w) * NT::RPI * D, is_k ? k_off[i] : v_off[i]);
   };
   // Q fragments in registers before the first tile loads (a later first use would wait for them)
 #pragma unroll
-  for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[c]));
-  // cursor of step t + 1; prologue K(0), V(0)
-  Cursor c1 = cur;
-  cursor_next<BS>(c1, my_j, my_real);
-  if (cur.valid) {
-    const NT a = tiles(kr, cur, vr, cur);
+  for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) a.k(i, w, lane);
-#pragma unroll
-    for (int i = 0; i < NT::NI; ++i) a.v(i, w, lane);
+    for (int c = 0; c < DC; ++c) asm volatile("" : "+v"(qf[qt][c]));
   }
 
   // Per-lane LDS read offsets (elements). K (A operand of S^T = K Q^T): lane reads row kt*32 + l32,
@@ -517,36 +563,117 @@ bsa_unit_kernel(FwdParams p) {
   for (int t = 0; t < 2; ++t)
     v_rd[t] = (4 * (G >> 1) + tr_r) * D + (((4 * t + 2 * (G & 1) + (tr_q >> 1)) ^ (2 * tr_r)) * 8) + 4 * (tr_q & 1);
 
-  f32x16 oacc[DT];
+  f32x16 oacc[QT][DT];
+  float m_i[QT], l_i[QT], neg_m[QT], rs[QT];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) oacc[t] = f32x16{};
-  float m_i = -INFINITY, l_i = 0.f;
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[qt][t] = f32x16{};
+    m_i[qt] = -INFINITY;
+    l_i[qt] = 0.f;
+  }
+  auto set_neg_m = [&]() {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) neg_m[qt] = -m_i[qt];
+  };
+  auto add_l = [&]() {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_i[qt] += rs[qt];
+  };
 
-  // Step t computes on K(t), V(t) in stage t % 2; its QK product streams K(t + 1) and its PV
-  // product V(t + 1) into the other stage. At the top of step t only V(t) may still be in flight
-  // (the last NI loads), and before the PV product (attend_step) only K(t + 1); the barriers extend
-  // each wave's wait to the workgroup and order a stage's refill after every wave's reads of it.
-  // Two steps per iteration (stage 0, then stage 1), so every LDS address is a loop-invariant
-  // register plus an immediate offset.
-  while (cur.valid) {
+  // The pipeline. Step s's K tile lives in stage ks[s % 2] and its V tile in vs[s % 2]. Block b
+  // (1 <= b < T) reads K(b) and V(b - 1) and loads K(b + 1) and V(b) into the stages the previous
+  // block finished reading; its top waits for this wave's loads and then on the workgroup barrier,
+  // so every wave's tiles of the block have landed and every wave is done with the stages being
+  // refilled. Block 0 (QK of step 0) and block T (PV of step T - 1) are the pipeline's ends.
+  // Exponentials run against the running max m_i, which may lag the scores: a slot is accepted
+  // when every lane's sum of exponentials is at most 2^16 (so is each exponential: far from fp32 /
+  // bf16 overflow). Otherwise (the first slot, or scores more than ~11 above m_i) m_i moves to the
+  // half-step's max, the accumulators are rescaled and the half's exponentials recomputed; the
+  // final normalization uses the same m_i, so the result does not depend on how far m_i lags.
+  f32x16 S[2][QT];
+  bf16x8 P[4][QT];
 #pragma unroll
-    for (int vs = 0; vs < 2; ++vs) {
-      if (!cur.valid) break;
-      const int real = cur.real - 64 * cur.half;
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
-      attend_step<D, NW>(kr + vs * TILE, vr + vs * TILE, k_rd, v_rd, qf, oacc, m_i, l_i, real, g, p.scale_log2,
-                         tiles(kr + (vs ^ 1) * TILE, c1, vr + (vs ^ 1) * TILE, c1), w, lane);
-      cur = c1;
-      cursor_next<BS>(c1, my_j, my_real);
+  for (int qt = 0; qt < QT; ++qt) {
+    S[0][qt] = f32x16{};
+    S[1][qt] = f32x16{};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) P[c][qt] = bf16x8{};
+  }
+  const float sl2 = p.scale_log2;
+  const PipeLoad no_load{};
+  if (T > 0) {
+    load_tile(0, true, ks0);
+    load_tile(1, true, ks1);
+    load_tile(0, false, vs0);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NT::NI) : "memory");
+    set_neg_m();
+    pipe_slot<D, NW, QT, 1, false, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
+                                                       k_off, no_load, v_off, w, rs);
+    int real_prev = __builtin_amdgcn_readlane(tab_real, 0);
+    if (real_prev < 32) pipe_mask<0, QT>(S[0], real_prev, g);
+    pipe_slot<D, NW, QT, 0, true, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
+                                                      k_off, no_load, v_off, w, rs);
+    if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 0>(S[0], P, oacc, m_i, l_i, rs, sl2);
+    add_l();
+
+    auto block = [&](auto par, int b) {
+      constexpr int PAR = decltype(par)::value;
+      bf16_t* const kcur = PAR ? ks1 : ks0;
+      bf16_t* const knext = PAR ? ks0 : ks1;
+      bf16_t* const vprev = PAR ? vs0 : vs1;
+      bf16_t* const vcur = PAR ? vs1 : vs0;
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
+      const PipeLoad ldk{tile_rs(b + 1, true), knext}, ldv{tile_rs(b, false), vcur};
+      set_neg_m();
+      pipe_slot<D, NW, QT, 1, true, true, true, true>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, ldk, k_off,
+                                                      ldv, v_off, w, rs);
+      if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
+      add_l();
+      const int real = __builtin_amdgcn_readlane(tab_real, b);
+      if (real < 32) pipe_mask<0, QT>(S[0], real, g);
+      set_neg_m();
+      pipe_slot<D, NW, QT, 0, true, true, true, false>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+                                                       k_off, no_load, v_off, w, rs);
+      if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 0>(S[0], P, oacc, m_i, l_i, rs, sl2);
+      add_l();
+      real_prev = real;
+    };
+    int b = 1;
+    for (; b + 1 < T; b += 2) {
+      block(std::integral_constant<int, 1>{}, b);
+      block(std::integral_constant<int, 0>{}, b + 1);
     }
+    if (b < T) block(std::integral_constant<int, 1>{}, b);
+
+    auto last = [&](auto par) {
+      constexpr int PAR = decltype(par)::value;  // (T - 1) % 2: stage of V(T - 1)
+      bf16_t* const vprev = PAR ? vs1 : vs0;
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
+      set_neg_m();
+      pipe_slot<D, NW, QT, 1, true, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+                                                        k_off, no_load, v_off, w, rs);
+      if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
+      add_l();
+      pipe_slot<D, NW, QT, 0, false, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+                                                         k_off, no_load, v_off, w, rs);
+    };
+    if ((T - 1) & 1) last(std::integral_constant<int, 1>{});
+    else last(std::integral_constant<int, 0>{});
   }
 
-  // the last steps streamed empty tiles: let them land before the workgroup's LDS is freed
+  // every tile load has landed (block T waited for the last ones)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  const float lsum = l_i + __shfl_xor(l_i, 32, 64);
-  float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  // log2-sum-exp of this unit's keys; the row's natural-log lse is this times ln 2
-  float lse2 = lsum > 0.f ? m_i + __log2f(lsum) : -INFINITY;
+  float inv[QT], lse2[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float lsum = l_i[qt] + __shfl_xor(l_i[qt], 32, 64);
+    inv[qt] = lsum > 0.f ? 1.f / lsum : 0.f;
+    // log2-sum-exp of this unit's keys; the row's natural-log lse is this times ln 2
+    lse2[qt] = lsum > 0.f ? m_i[qt] + __log2f(lsum) : -INFINITY;
+  }
   if (ns > 1) {
     // Normalized partial + log2-sum-exp; the row's last unit to arrive merges every partial, in
     // split order (its own is still in registers: the same fp32 values it stored). The row's units
@@ -554,29 +681,35 @@ bsa_unit_kernel(FwdParams p) {
     // written and read with device-scope (sc1) buffer accesses instead of L2-wide write-back and
     // invalidate, and the arrival count is a device-scope atomic taken after this workgroup's
     // partial stores have completed; the last arrival loads the others' partials only after its
-    // count has returned. A partial is stored in accumulator-fragment order (wave, tile, quad,
-    // lane), so every store and load instruction covers 1 KiB of contiguous memory.
+    // count has returned. A partial is stored in accumulator-fragment order (query tile, tile,
+    // quad, lane), so every store and load instruction covers 1 KiB of contiguous memory.
     const int64_t slot0 = row * p.max_splits;
-    const int ql = w * 32 + l32;
     constexpr int SLOT_BYTES = BS * D * 4;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void*)(p.part_o + slot0 * (BS * D)), (short)0, ns * SLOT_BYTES, WA_BUF_DWORD3);
-    auto frag_off = [&](int sp, int t, int rq) { return sp * SLOT_BYTES + (((w * DT + t) * 4 + rq) * 64 + lane) * 16; };
+    auto frag_off = [&](int sp, int vw, int t, int rq) {
+      return sp * SLOT_BYTES + (((vw * DT + t) * 4 + rq) * 64 + lane) * 16;
+    };
     constexpr int SC1 = 16;  // cache policy: device-scope coherent
-    if (g == 0)
-      __hip_atomic_store(p.part_lse + (slot0 + split) * BS + ql, lse2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+    for (int qt = 0; qt < QT; ++qt) {
+      const int vw = w * QT + qt;
+      if (g == 0)
+        __hip_atomic_store(p.part_lse + (slot0 + split) * BS + vw * 32 + l32, lse2[qt], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const f32x4 ov = {oacc[t][rq * 4] * inv, oacc[t][rq * 4 + 1] * inv, oacc[t][rq * 4 + 2] * inv,
-                          oacc[t][rq * 4 + 3] * inv};
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ov), prs, frag_off(split, t, rq), 0, SC1);
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 ov = {oacc[qt][t][rq * 4] * inv[qt], oacc[qt][t][rq * 4 + 1] * inv[qt],
+                            oacc[qt][t][rq * 4 + 2] * inv[qt], oacc[qt][t][rq * 4 + 3] * inv[qt]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ov), prs, frag_off(split, vw, t, rq), 0, SC1);
+        }
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    int* s_last = (int*)kr;  // the K ring is free: every tile load has landed and been read
+    int* s_last = &steptab[0][0][0];  // the step tables are no longer read
     if (tid == 0) {
       const bool last =
           __hip_atomic_fetch_add(p.arrivals + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ns - 1;
@@ -585,78 +718,112 @@ bsa_unit_kernel(FwdParams p) {
     }
     __syncthreads();
     if (!__builtin_amdgcn_readfirstlane(*s_last)) return;  // uniform: one LDS word for every lane
-    // Another unit's partial comes in by direct-to-LDS loads into this wave's 16 KiB of the free
-    // K/V rings (each wave reads back only what it loaded: no workgroup barrier), the first one
-    // together with the first four log2-sum-exps, so a two-unit row merges after one round trip.
-    float* plse = p.part_lse + slot0 * BS + ql;
-    auto load_lse = [&](int sp) {
-      return sp == split ? lse2 : __hip_atomic_load(plse + sp * BS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    constexpr int WPH = (NW + 1) / 2;  // waves staged in each ring
-    static_assert(WPH * DT * 4 * 1024 <= 2 * TILE * 2, "partial staging does not fit the rings");
-    char* wbuf = (w < WPH ? (char*)kr : (char*)vr) + (w % WPH) * (DT * 4 * 1024);
+    // Another unit's partial comes in by direct-to-LDS loads into one free ring stage per query
+    // tile (each wave reads back only what it loaded: no workgroup barrier), the first one together
+    // with the first four log2-sum-exps, so a two-unit row merges after one round trip.
+    static_assert(DT * 4 * 1024 <= TILE * 2 && NVW <= 4, "partial staging does not fit the ring stages");
+    char* wbuf[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int vw = w * QT + qt;
+      wbuf[qt] = (char*)(vw == 0 ? ks0 : vw == 1 ? ks1 : vw == 2 ? vs0 : vs1);
+    }
     auto fetch_part = [&](int sp) {
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
+      for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) lds_dma16_sc1(prs, wbuf + (t * 4 + rq) * 1024, frag_off(sp, t, rq));
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq)
+            lds_dma16_sc1(prs, wbuf[qt] + (t * 4 + rq) * 1024, frag_off(sp, w * QT + qt, t, rq));
+        }
       }
     };
     const int sp_first = split == 0 ? 1 : 0;
     fetch_part(sp_first);
-    const float l0 = load_lse(0), l1 = load_lse(1);
-    const float l2 = ns > 2 ? load_lse(2) : -INFINITY, l3 = ns > 3 ? load_lse(3) : -INFINITY;
-    auto lse_of = [&](int sp) { return sp == 0 ? l0 : sp == 1 ? l1 : sp == 2 ? l2 : sp == 3 ? l3 : load_lse(sp); };
-    float M = -INFINITY;
+    float lsv[QT][4];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const float* plse = p.part_lse + slot0 * BS + (w * QT + qt) * 32 + l32;
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp)
+        lsv[qt][sp] = sp >= ns ? -INFINITY
+                               : sp == split ? lse2[qt]
+                                             : __hip_atomic_load(plse + sp * BS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    auto lse_of = [&](int qt, int sp) {
+      if (sp < 4) return lsv[qt][sp];
+      if (sp == split) return lse2[qt];
+      return __hip_atomic_load(p.part_lse + slot0 * BS + (w * QT + qt) * 32 + l32 + sp * BS, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    };
+    float M[QT], Z[QT];
+    f32x16 acc[QT][DT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      M[qt] = -INFINITY;
 #pragma unroll 1
-    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, lse_of(sp));
-    float Z = 0.f;
-    if (M != -INFINITY) {
+      for (int sp = 0; sp < ns; ++sp) M[qt] = fmaxf(M[qt], lse_of(qt, sp));
+      Z[qt] = 0.f;
+      if (M[qt] != -INFINITY) {
 #pragma unroll 1
-      for (int sp = 0; sp < ns; ++sp) {
-        const float wgt = exp2f(lse_of(sp) - M);
-        if (wgt != 0.f) Z += wgt;
+        for (int sp = 0; sp < ns; ++sp) {
+          const float wgt = exp2f(lse_of(qt, sp) - M[qt]);
+          if (wgt != 0.f) Z[qt] += wgt;
+        }
       }
+#pragma unroll
+      for (int t = 0; t < DT; ++t) acc[qt][t] = f32x16{};
     }
     // sum the weighted partials in split order (zero weights skipped)
-    f32x16 acc[DT];
-#pragma unroll
-    for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
 #pragma unroll 1
     for (int sp = 0; sp < ns; ++sp) {
-      const float wgt = M != -INFINITY ? exp2f(lse_of(sp) - M) : 0.f;
       if (sp == split) {
-        if (wgt != 0.f) {
 #pragma unroll
-          for (int t = 0; t < DT; ++t) {
+        for (int qt = 0; qt < QT; ++qt) {
+          const float wgt = M[qt] != -INFINITY ? exp2f(lse_of(qt, sp) - M[qt]) : 0.f;
+          if (wgt != 0.f) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[t][i] = fmaf(wgt, oacc[t][i] * inv, acc[t][i]);
+            for (int t = 0; t < DT; ++t) {
+#pragma unroll
+              for (int i = 0; i < 16; ++i) acc[qt][t][i] = fmaf(wgt, oacc[qt][t][i] * inv[qt], acc[qt][t][i]);
+            }
           }
         }
         continue;
       }
-      if (sp != sp_first) fetch_part(sp);  // the buffer is free: the previous partial was read
+      if (sp != sp_first) fetch_part(sp);  // the buffers are free: the previous partial was read
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      if (wgt != 0.f) {
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
+      for (int qt = 0; qt < QT; ++qt) {
+        const float wgt = M[qt] != -INFINITY ? exp2f(lse_of(qt, sp) - M[qt]) : 0.f;
+        if (wgt != 0.f) {
 #pragma unroll
-          for (int rq = 0; rq < 4; ++rq) {
-            const f32x4 v = *(const f32x4*)(wbuf + (t * 4 + rq) * 1024 + lane * 16);
+          for (int t = 0; t < DT; ++t) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][rq * 4 + i] = fmaf(wgt, v[i], acc[t][rq * 4 + i]);
+            for (int rq = 0; rq < 4; ++rq) {
+              const f32x4 v = *(const f32x4*)(wbuf[qt] + (t * 4 + rq) * 1024 + lane * 16);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[qt][t][rq * 4 + i] = fmaf(wgt, v[i], acc[qt][t][rq * 4 + i]);
+            }
           }
         }
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next fetch
     }
 #pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] = acc[t];
-    inv = Z > 0.f ? 1.f / Z : 0.f;
-    lse2 = Z > 0.f ? M + log2f(Z) : -INFINITY;
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[qt][t] = acc[qt][t];
+      inv[qt] = Z[qt] > 0.f ? 1.f / Z[qt] : 0.f;
+      lse2[qt] = Z[qt] > 0.f ? M[qt] + log2f(Z[qt]) : -INFINITY;
+    }
   }
-  if (p.lse && g == 0 && q_ok) p.lse[((int64_t)b * p.H + h) * p.Lq + qi] = lse2 * WA_LN2;
-  write_output<D>(p, oacc, inv, qf, qrow, b, h, qi, q_ok, g, l32);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    if (p.lse && g == 0 && q_ok[qt]) p.lse[((int64_t)b * p.H + h) * p.Lq + qi[qt]] = lse2[qt] * WA_LN2;
+    write_output<D>(p, oacc[qt], inv[qt], qf[qt], qrow[qt], b, h, qi[qt], q_ok[qt], g, l32);
+  }
 }
 
 // Merges the ns normalized partials of one row (slot = row * max_splits + split), in split order,
@@ -735,7 +902,10 @@ int launch(const FwdParams& fp, int64_t rows, bool cleared, hipStream_t stream) 
     const int rc = wa_launch_status("bsa_fwd_clear");
     if (rc != WA_OK) return rc;
   }
-  hipLaunchKernelGGL((bsa_unit_kernel<D, BS>), dim3(fp.n_units), dim3(2 * BS), 0, stream, fp);
+  // 32 queries per wave. (64 per wave, QT = 2, halves the LDS reads per product but needs more
+  // than 256 registers: as compiled today its loop moves ~1,600 values between AGPRs and VGPRs.)
+  constexpr int QT = 1;
+  hipLaunchKernelGGL((bsa_unit_kernel<D, BS, QT>), dim3(fp.n_units), dim3(2 * BS / QT), 0, stream, fp);
   return wa_launch_status("bsa_fwd_unit");
 }
 
