@@ -4,8 +4,8 @@
  * Every entry point takes plain device pointers, element strides and sizes, launches on the
  * caller's HIP stream (`stream` is a hipStream_t passed as void*), allocates nothing and keeps no
  * global device state, except wa_bsa_fwd_noalloc, whose workspace is a static device array of the
- * library, and wa_hsa_fwd, which creates a side stream and two events per device on its first call. Inputs, outputs and workspaces are owned by the caller; workspace sizes come from the
- * matching *_workspace_bytes query.
+ * library. Inputs, outputs, workspaces, side streams and events are owned by the caller; workspace
+ * sizes come from the matching *_workspace_bytes query.
  *
  * Return value: WA_OK (0) on success; a negative WA_ERR_* for argument errors; a positive
  * hipError_t for runtime failures. wa_last_error() returns the calling thread's last message.
@@ -265,15 +265,19 @@ int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* args, void* stream);
  * heads' queries and keys (wa_block_mean_pool_n), their top-k routing (wa_route, TOPK; index / num
  * written for the caller), the block-sparse attention of those heads rounded to bf16 (wa_bsa_fwd,
  * PLAIN), the elu(x)+1 state of the linear heads (wa_elu1_state) and their gated readout
- * (wa_elu1_readout, GATED), from one workspace of wa_hsa_fwd_workspace_bytes. The two elu1 calls
- * run on a side stream of the library's, forked from and joined back to `stream` inside the call
- * (created, with two events, on a device's first call that is not under stream capture, and kept
- * until the process ends; before that, and with one kind of head, everything runs on `stream`).
+ * (wa_elu1_readout, GATED), from one workspace of wa_hsa_fwd_workspace_bytes.
  * It replaces the orchestration of hsa_attention, wan/modules/hsa/attention.py:153-259, for the
  * north-star head modes (sparse / linear heads, no head in both branches) with bf16 q / k / v;
  * the result equals those calls made one by one.
  * head_k: [H] top-k budget per global head. units / n_units / max_visits: the unit table of the
- * sparse launch (see wa_bsa_fwd). */
+ * sparse launch (see wa_bsa_fwd).
+ * side_stream / fork_event / join_event (hipStream_t / hipEvent_t, owned by the caller): with a
+ * side stream and both kinds of head, the two elu1 calls run on it, concurrently with the sparse
+ * heads on `stream`: the call records fork_event on `stream` and makes the side stream wait for
+ * it, and at its end records join_event on the side stream and makes `stream` wait for it (so a
+ * graph captured from `stream` holds both branches). NULL side_stream: everything runs on
+ * `stream`. The call keeps no state and takes no lock; concurrent calls need their own side
+ * stream and events. */
 typedef struct wa_hsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;
@@ -288,6 +292,7 @@ typedef struct wa_hsa_fwd_args {
   const void* gate_w; const float* gate_b;
   int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
   void* workspace;
+  void* side_stream; void* fork_event; void* join_event;
 } wa_hsa_fwd_args;
 int64_t wa_hsa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t Lq, int64_t Lkv, int64_t D, int64_t block_size,
                                    int64_t n_sparse, int64_t n_linear, int64_t max_visits);

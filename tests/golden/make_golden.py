@@ -29,6 +29,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 
 def load_reference_hsa(ref_root: str):
+    # the reference tree is read-only: importing it must not leave __pycache__ directories there
+    sys.dont_write_bytecode = True
     pkg_dir = os.path.join(ref_root, "wan", "modules", "hsa")
     spec = importlib.util.spec_from_file_location(
         "_reference_hsa", os.path.join(pkg_dir, "__init__.py"), submodule_search_locations=[pkg_dir])

@@ -84,3 +84,30 @@ def test_argument_errors_return_status_without_a_gpu():
     assert handle.wa_route(ctypes.byref(rargs), None) == -1
     assert handle.wa_map_to_index(None, 1, 1, None, None, None) == -1
     assert handle.wa_route_workspace_bytes(1, 12, 37, 256) >= 12 * 37 * 257 * 4
+
+
+def test_noalloc_rejects_oversized_launches_and_workspaces_without_a_gpu():
+    """wa_bsa_fwd_noalloc refuses, on the host and before any HIP call, a launch whose workspace
+    would not fit the static array and a caller-supplied workspace. The tensor pointers are dummy
+    aligned addresses and there is no stream: nothing is dereferenced or launched."""
+    handle = _lib.lib()
+    fake = 1 << 20
+    h, d, length = 64, 128, 40000
+    args = _lib.BsaFwdArgs()
+    args.q = args.k = args.v = args.o = args.index = args.num = fake
+    for name in ("q", "k", "v", "o"):
+        setattr(args, name + "_sb", length * h * d)
+        setattr(args, name + "_st", h * d)
+        setattr(args, name + "_sh", d)
+    args.o_dtype = _lib.WA_BF16
+    args.index_width = 64
+    args.B, args.H, args.Lq, args.Lkv, args.D, args.block_size = 1, h, length, length, d, 128
+    args.max_visits, args.split_visits = 64, 16
+    # 64 heads x 313 query blocks x 4 split units of partials: far beyond the static array
+    need = handle.wa_bsa_fwd_workspace_bytes(h * 313, 64, 16, 128, d)
+    assert need > _lib.BSA_FWD_NOALLOC_SCRATCH_BYTES
+    assert handle.wa_bsa_fwd_noalloc(ctypes.byref(args), None) == _lib.WA_ERR_ARG
+    assert b"static scratch" in handle.wa_last_error()
+    args.workspace = fake
+    assert handle.wa_bsa_fwd_noalloc(ctypes.byref(args), None) == _lib.WA_ERR_ARG
+    assert b"must be NULL" in handle.wa_last_error()

@@ -555,3 +555,70 @@ def test_native_split_forward_equals_the_python_orchestration():
     sparse = plan.sparse_only
     assert torch.equal(save["route"].index[:, sparse], route.index[:, sparse])
     assert torch.equal(save["route"].num[:, sparse], route.num[:, sparse])
+
+
+def _split_kw(cfg, gate):
+    return dict(k_coarse=None, v_coarse=None, k_proj_mat=None, v_proj_mat=None, gate_lin=gate,
+                block_size=cfg["block_size"], tau_min=0.35, tau_max=1.0, proj_segment_len=cfg["proj_segment_len"],
+                routing=cfg["routing"], topk=cfg["topk"], head_modes=cfg["head_modes"],
+                linear_mode=cfg["linear_mode"])
+
+
+def _trained_gate(d, seed):
+    gen = torch.Generator().manual_seed(seed)
+    gate = torch.nn.Linear(d, d)
+    with torch.no_grad():
+        gate.weight.copy_(torch.randn(d, d, generator=gen) * 0.05)
+        gate.bias.copy_(torch.randn(d, generator=gen) * 0.05)
+    return gate.to(DEV)
+
+
+def test_native_split_forward_concurrent_streams_equal_serial():
+    """Two threads call the one-call forward (wa_hsa_fwd) at the same time, each on its own stream
+    (so each gets its own side stream and fork / join events and nothing is shared between the
+    calls): every result equals the same call made alone."""
+    import threading
+    cfgs = [workloads.cfg2(device=DEV, seed=s) for s in (7, 8)]
+    gates = [_trained_gate(c["q"].shape[-1], 20 + i) for i, c in enumerate(cfgs)]
+    with torch.no_grad():
+        want = [WA.hsa_forward(c["q"], c["k"], c["v"], **_split_kw(c, g)) for c, g in zip(cfgs, gates)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in cfgs]
+    got = [[None] * 4 for _ in cfgs]
+    errors = []
+    barrier = threading.Barrier(len(cfgs))
+
+    def worker(i):
+        try:
+            c = cfgs[i]
+            with torch.no_grad(), torch.cuda.stream(streams[i]):
+                barrier.wait()
+                for r in range(4):
+                    got[i][r] = WA.hsa_forward(c["q"], c["k"], c["v"], **_split_kw(c, gates[i]))
+        except Exception as e:  # reported below, from the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(cfgs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i in range(len(cfgs)):
+        for r in range(4):
+            assert torch.equal(got[i][r], want[i]), f"thread {i} call {r} differs from the serial call"
+
+
+def test_native_split_forward_without_side_stream_is_identical(monkeypatch):
+    """wa_hsa_fwd with a NULL side stream runs both branches on the caller's stream, with the same
+    output bit for bit as the forked call."""
+    cfg = workloads.cfg2(device=DEV, seed=9)
+    gate = _trained_gate(cfg["q"].shape[-1], 30)
+    with torch.no_grad():
+        forked = WA.hsa_forward(cfg["q"], cfg["k"], cfg["v"], **_split_kw(cfg, gate))
+    monkeypatch.setattr(WA, "_fork_join", lambda dev, main: (None, None, None))
+    with torch.no_grad():
+        single = WA.hsa_forward(cfg["q"], cfg["k"], cfg["v"], **_split_kw(cfg, gate))
+    torch.cuda.synchronize()
+    assert torch.equal(single, forked)

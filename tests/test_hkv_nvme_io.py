@@ -82,3 +82,35 @@ def test_a_finished_spill_is_read_back_from_its_file(tmp_path):
     assert torch.equal(got["k"][1], torch.full((1, 37, 2, 16), 6.0))
     assert len(_leaves(got, [])) == 6
     tier.cleanup()
+
+
+def test_a_failed_spill_keeps_the_chunk_in_host_memory_and_raises(tmp_path, monkeypatch):
+    """A spill whose write fails is reported, with the chunk's id, by the next tier call; the chunk
+    stays host-resident with its blob, and its partial file is deleted and forgotten (so a later
+    eviction writes it again instead of trusting a short file)."""
+    import time
+    from worldattention_amd.hkv import tiering
+    tier = HKVTierManager(cpu_max_chunks=1, nvme_enabled=True, nvme_dir=str(tmp_path))
+    tier.put(0, _blob(1))
+    tier.put(1, _blob(2))                          # evicts chunk 0: its spill starts
+    path = tier._files[0]
+    handle = tier._writes[0][0]
+    while _lib.lib().wa_io_done(handle) != 1:
+        time.sleep(0.001)
+    real_call = tiering._lib.call
+
+    def failing(name, *args):
+        if name == "wa_io_wait":
+            real_call(name, *args)                  # release the handle, then report a failure
+            raise OSError("injected write failure")
+        return real_call(name, *args)
+
+    monkeypatch.setattr(tiering._lib, "call", failing)
+    with pytest.raises(OSError, match="chunk 0"):
+        tier.stats()
+    monkeypatch.undo()
+    assert tier.location(0) == "cpu"
+    assert 0 not in tier._files and not os.path.exists(path)
+    got = tier.get(0)
+    assert all(torch.equal(t, torch.full_like(t, float(1 + l))) for l, t in enumerate(got["k"]))
+    tier.cleanup()

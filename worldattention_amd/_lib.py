@@ -174,6 +174,7 @@ HsaFwdArgs = _struct("wa_hsa_fwd_args", [
     ("gate_w", c_void_p), ("gate_b", c_void_p),
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
     ("workspace", c_void_p),
+    ("side_stream", c_void_p), ("fork_event", c_void_p), ("join_event", c_void_p),
 ])
 
 BsaBwdArgs = _struct("wa_bsa_bwd_args", [

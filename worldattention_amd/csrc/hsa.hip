@@ -1,67 +1,22 @@
 // One call for the HSA forward of split heads (host code). It runs the same entry points, with the
 // same arguments, as the Python orchestration of hsa_forward does for heads that take one branch
 // each (top-k sparse heads, elu(x)+1 linear heads), from one workspace:
-//  * the elu1 state pass and the gated readout of the linear heads, on a side stream of the
-//    library's;
+//  * the elu1 state pass and the gated readout of the linear heads, on the caller's side stream
+//    when it passes one (forked from and joined back to its stream with the caller's two events),
+//    else on its stream;
 //  * block pooling of the sparse heads' queries and keys, top-k routing (which also clears the
 //    sparse launch's arrival counters) and the block-sparse launch, on the caller's stream.
 // An eager call then crosses from Python once instead of ~20 times (allocations, argument structs
-// and launches).
+// and launches). The call keeps no state between calls and takes no lock: concurrent calls on
+// different streams (each with its own side stream and events) are independent.
 //
 // Reference semantics: wan/modules/hsa/attention.py:153-259 (hsa_attention) with the north-star
 // head modes; each step follows the entry point it calls.
-#include <mutex>
-
 #include "common.h"
 
 namespace {
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
-
-// The linear heads' kernels run on a side stream of the library's, concurrently with the sparse
-// heads' on the caller's stream. The stream (default priority) and its fork / join events are
-// created on a device's first call outside stream capture and held until the process ends (a call
-// under capture before that runs both branches on the caller's stream); a mutex keeps each call's
-// record / wait sequence whole.
-constexpr int kMaxDevices = 64;
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-SideStream g_side[kMaxDevices];
-std::mutex g_side_mu;
-
-// *out = the current device's side stream, or nullptr when it does not exist yet and `stream` is
-// capturing (nothing is created under capture).
-int side_stream(hipStream_t stream, SideStream** out) {
-  *out = nullptr;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return wa_fail((int)e, "wa_hsa_fwd: hipGetDevice: %s", hipGetErrorString(e));
-  if (dev < 0 || dev >= kMaxDevices) return wa_fail(WA_ERR_ARG, "wa_hsa_fwd: device %d out of range", dev);
-  SideStream& s = g_side[dev];
-  if (!s.stream) {
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if ((e = hipStreamIsCapturing(stream, &st)) != hipSuccess)
-      return wa_fail((int)e, "wa_hsa_fwd: hipStreamIsCapturing: %s", hipGetErrorString(e));
-    if (st != hipStreamCaptureStatusNone) return WA_OK;
-    // published only once all three exist (a failed call leaves the slot empty for the next)
-    hipStream_t st_new = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-    if ((e = hipStreamCreateWithFlags(&st_new, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&fork, hipEventDisableTiming)) != hipSuccess ||
-        (e = hipEventCreateWithFlags(&join, hipEventDisableTiming)) != hipSuccess) {
-      if (fork) (void)hipEventDestroy(fork);
-      if (st_new) (void)hipStreamDestroy(st_new);
-      return wa_fail((int)e, "wa_hsa_fwd: side stream: %s", hipGetErrorString(e));
-    }
-    s.fork = fork;
-    s.join = join;
-    s.stream = st_new;
-  }
-  *out = &s;
-  return WA_OK;
-}
 
 struct HsaLayout {
   int64_t qp, kp, arrivals, thresholds, bsa, elu1, state, zsum, total;
@@ -109,27 +64,25 @@ extern "C" int wa_hsa_fwd(const wa_hsa_fwd_args* a, void* stream) {
                "wa_hsa_fwd: sparse heads need their list, per-head k, routing outputs and the unit table");
   WA_CHECK_ARG(a->n_linear == 0 || a->linear_heads, "wa_hsa_fwd: linear heads need their list");
   WA_CHECK_ARG(wa_aligned16(a->workspace), "wa_hsa_fwd: workspace must be 16-byte aligned");
+  WA_CHECK_ARG(a->side_stream == nullptr || (a->fork_event && a->join_event),
+               "wa_hsa_fwd: a side stream needs its fork and join events");
   if (a->B == 0 || a->Lq == 0) return WA_OK;
   const HsaLayout l =
       hsa_layout(a->B, a->H, a->Lq, a->Lkv, a->D, a->block_size, a->n_sparse, a->n_linear, a->max_visits);
   char* ws = (char*)a->workspace;
-  int rc = WA_OK;
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream* side = nullptr;
-  if (a->n_sparse > 0 && a->n_linear > 0 && (rc = side_stream((hipStream_t)stream, &side)) != WA_OK) return rc;
-  const bool two = side != nullptr;
+  const bool two = a->side_stream != nullptr && a->side_stream != stream && a->n_sparse > 0 && a->n_linear > 0;
+  hipStream_t side = (hipStream_t)a->side_stream;
+  hipEvent_t fork = (hipEvent_t)a->fork_event, join = (hipEvent_t)a->join_event;
   if (two) {
     hipError_t e;
-    if ((e = hipEventRecord(side->fork, (hipStream_t)stream)) != hipSuccess ||
-        (e = hipStreamWaitEvent(side->stream, side->fork, 0)) != hipSuccess)
+    if ((e = hipEventRecord(fork, (hipStream_t)stream)) != hipSuccess || (e = hipStreamWaitEvent(side, fork, 0)) != hipSuccess)
       return wa_fail((int)e, "wa_hsa_fwd: fork: %s", hipGetErrorString(e));
   }
-  rc = hsa_branches(a, l, ws, stream, two ? (void*)side->stream : stream);
+  int rc = hsa_branches(a, l, ws, stream, two ? (void*)side : stream);
   // the caller's stream joins the side stream on every path once forked (a capture must end joined)
   if (two) {
     hipError_t e;
-    if ((e = hipEventRecord(side->join, side->stream)) != hipSuccess ||
-        (e = hipStreamWaitEvent((hipStream_t)stream, side->join, 0)) != hipSuccess)
+    if ((e = hipEventRecord(join, side)) != hipSuccess || (e = hipStreamWaitEvent((hipStream_t)stream, join, 0)) != hipSuccess)
       return rc != WA_OK ? rc : wa_fail((int)e, "wa_hsa_fwd: join: %s", hipGetErrorString(e));
   }
   return rc;

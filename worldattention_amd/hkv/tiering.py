@@ -10,7 +10,8 @@ for it.
 The NVMe tier replaces the reference's synchronous ``torch.save`` / ``torch.load`` with
 asynchronous direct I/O (``wa_io_*``): a spill starts writing the blob's tensors (raw bytes, one
 4 KiB-aligned region each, O_DIRECT where the file system takes it) on a worker thread and returns;
-the blob is released when the write completes. A reload reads into freshly allocated (pinned, when
+the blob is released once the write has completed (checked on every put, get, prefetch and stats
+call); a write that fails leaves the chunk in host memory and raises. A reload reads into freshly allocated (pinned, when
 a GPU is present) tensors of the recorded shapes; :meth:`HKVTierManager.prefetch` starts reloads
 ahead of their ``get``. A chunk requested while its spill is still being written is served from
 memory.
@@ -141,10 +142,26 @@ class HKVTierManager:
         self._reap()
 
     def _reap(self) -> None:
-        """Finish the spills whose writes have completed (releasing their blobs)."""
+        """Finish the spills whose writes have completed, releasing their blobs. A spill that failed
+        leaves its chunk in host memory (without a backup file, which is deleted) and raises
+        ``OSError`` naming the chunk."""
         for cid in [c for c, (h, _, _) in self._writes.items() if _lib.lib().wa_io_done(h) == 1]:
-            handle, _, _ = self._writes.pop(cid)
-            _lib.call("wa_io_wait", handle)
+            handle, blob, _ = self._writes.pop(cid)
+            try:
+                _lib.call("wa_io_wait", handle)
+            except OSError as exc:
+                path = self._files.pop(cid, None)
+                self._specs.pop(cid, None)
+                if path is not None:
+                    try:
+                        os.remove(path)
+                    except OSError:
+                        pass
+                if self._where.get(cid) == _DISK:
+                    self._blobs[cid] = blob
+                    self._where[cid] = _HOST
+                    self.n_spills -= 1
+                raise OSError(f"HKVTierManager: spilling chunk {cid} failed; it stays in host memory: {exc}") from exc
 
     def _read(self, chunk_id: int) -> dict:
         """Reload a spilled chunk: the blob still in memory if its spill is being written, else the
@@ -161,6 +178,7 @@ class HKVTierManager:
 
     def prefetch(self, chunk_ids: Iterable[int]) -> None:
         """Start reading spilled chunks back so later ``get`` calls only wait for them."""
+        self._reap()
         for cid in chunk_ids:
             if self._where.get(cid) == _DISK and cid not in self._reads and cid not in self._writes:
                 blob = _build(self._specs[cid], torch.cuda.is_available())
@@ -182,6 +200,7 @@ class HKVTierManager:
         """The chunk's blob, reloaded from NVMe if it was spilled (None if unknown). With ``wait``
         the copy that filled it has completed; ``wait=False`` suits consumers ordered after that
         copy on the same stream."""
+        self._reap()
         tier = self._where.get(chunk_id)
         if tier is None:
             return None
@@ -207,6 +226,7 @@ class HKVTierManager:
         return self._where.get(chunk_id, "absent")
 
     def stats(self) -> dict:
+        self._reap()
         on_disk = sum(1 for tier in self._where.values() if tier == _DISK)
         return {"cpu_resident": self._host_count(), "nvme_resident": on_disk, "backups": len(self._files),
                 "n_spills": self.n_spills, "n_loads": self.n_loads, "n_drops": self.n_drops}

@@ -310,7 +310,7 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     # (or `lin_tmp`, joined before the fused sparse epilogue reads it). Its kernels are issued
     # first (measured: 3 us per call faster in graph replay than issuing the pooling first).
     main = torch.cuda.current_stream(dev)
-    side = _branch_stream(dev) if plan.linear and plan.sparse else None
+    side = _fork_join(dev, main)[0] if plan.linear and plan.sparse else None
     if side is not None:
         side.wait_stream(main)
 
@@ -359,25 +359,34 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     return out if out.dtype == out_dtype else out.to(out_dtype)
 
 
-_BRANCH_STREAMS: dict = {}
+_FORK_JOIN: dict = {}
 
 
-def _branch_stream(dev: torch.device) -> torch.cuda.Stream:
-    """The per-device side stream of the linear branch (default priority)."""
-    s = _BRANCH_STREAMS.get(dev)
-    if s is None:
-        s = torch.cuda.Stream(device=dev)
-        _BRANCH_STREAMS[dev] = s
-    return s
+def _fork_join(dev: torch.device, main: torch.cuda.Stream):
+    """The side stream of the linear branch for work issued on ``main`` (default priority), with the
+    fork / join events that :func:`_native_split_forward` hands to the library: one set per caller
+    stream, so calls on different streams never wait on each other's linear branch. The events are
+    recorded once here so that they exist before their handles are passed on."""
+    key = (dev.index, main.cuda_stream)
+    ent = _FORK_JOIN.get(key)
+    if ent is None:
+        side = torch.cuda.Stream(device=dev)
+        fork, join = torch.cuda.Event(), torch.cuda.Event()
+        fork.record(side)
+        join.record(side)
+        ent = (side, fork, join)
+        _FORK_JOIN[key] = ent
+    return ent
 
 
 def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len, kv_len, out, save):
     """:func:`hsa_forward` of top-k sparse heads and elu1 linear heads as one library call
     (``wa_hsa_fwd``): the same entry points with the same arguments as the Python orchestration,
-    the linear heads' on a side stream of the library's that the caller's stream forks and joins
-    inside the call (so graph capture records the same two branches). An eager call then pays one
-    crossing into the library instead of ~20 (allocations, argument structs, launches, events):
-    171 -> 48 us of host time, and at cfg 2 the eager call went from 195 to 141 us (GPU-bound)."""
+    the linear heads' on a side stream of the caller's stream (see :func:`_fork_join`) that the
+    call forks and joins inside (so graph capture records the same two branches). An eager call
+    then pays one crossing into the library instead of ~20 (allocations, argument structs,
+    launches, events): 171 -> 48 us of host time, and at cfg 2 the eager call went from 195 to
+    141 us (GPU-bound)."""
     dev = q.device
     bsz, _, heads, d = q.shape
     _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
@@ -389,13 +398,20 @@ def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len,
     num = torch.empty((bsz, heads, nq), dtype=torch.int32, device=dev)
     ws = torch.empty((_lib.lib().wa_hsa_fwd_workspace_bytes(bsz, heads, q_len, kv_len, d, block_size, n_sp, n_lin,
                                                              max_visits),), dtype=torch.uint8, device=dev)
+    main = torch.cuda.current_stream(dev)
+    side, fork, join = _fork_join(dev, main) if n_sp and n_lin else (None, None, None)
     args = _lib.HsaFwdArgs(*_lib.blhd(q), *_lib.blhd(k), *_lib.blhd(v), *_lib.blhd(out), _lib.dtype_code(out),
                            bsz, heads, q_len, kv_len, d, block_size,
                            *_lib.heads_arg(plan.t["sparse_only"]), _lib.head_list(ks, dev).data_ptr(),
                            units.data_ptr(), n_units, max_visits, index.data_ptr(), num.data_ptr(),
                            *_lib.heads_arg(plan.t["linear_only"]), _lib.ptr(gate.w), _lib.ptr(gate.b),
-                           int(gate.pre_bf16), int(gate.out_bf16), int(lin_round), ws.data_ptr())
-    _lib.call("wa_hsa_fwd", args, _lib.stream_ptr(dev))
+                           int(gate.pre_bf16), int(gate.out_bf16), int(lin_round), ws.data_ptr(),
+                           side.cuda_stream if side is not None else None,
+                           fork.cuda_event if fork is not None else None,
+                           join.cuda_event if join is not None else None)
+    # the call ends with the caller's stream waiting for the side stream, so later work on it (and
+    # the allocator's reuse of the workspace) is ordered after the linear branch
+    _lib.call("wa_hsa_fwd", args, main.cuda_stream)
     if save is not None:  # top-k routing has no thresholds (the kernel writes zeros)
         save.update(route=BlockRouting(index=index, num=num, mask=None,
                                        thresholds=torch.zeros((heads,), dtype=torch.float32, device=dev)))
