@@ -20,6 +20,8 @@ Also on the same line:
   side stream) against a plain pinned copy, the re-rope kernel, the HSA forward over the 14-frame
   pool, and the per-layer time with later layers' installs overlapped with attention
   (``apply(wait=False)`` + ``wait_layer``);
+* ``reference_mode``: the reference's own default HSA configuration (block 64, Gini routing,
+  low-rank branch, both branches on every head) on the cfg 2 chunk, through ``HSAAttention``;
 * ``train`` (cfg 5): HSA forward + backward at the cfg 2 shape with top-k 16;
 * ``wan14b`` (cfg 4): 40 layers x 4 denoising steps of QKV projection + HSA + out projection.
 """
@@ -52,8 +54,9 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-calls", type=int, default=12)
-    ap.add_argument("--only", default="cfg2,cfg3,cfg4,cfg5",
-                    help="comma list of the extra configs to run (cfg2, the headline, always runs)")
+    ap.add_argument("--only", default="cfg2,ref,cfg3,cfg4,cfg5",
+                    help="comma list of the extra configs to run (cfg2, the headline, always runs; ref: the "
+                         "reference's default HSA configuration on the cfg2 chunk)")
     ap.add_argument("--hkv-layers", type=int, default=4)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (the reference kernel that scales "
@@ -170,6 +173,57 @@ def gate_and_proj(d: int, dev):
         gate.weight.zero_()
         gate.bias.zero_()
     return gate, torch.zeros(13, 1560, dtype=torch.bfloat16, device=dev)
+
+
+# ---------------------------------------------------------------------------------------------
+# the reference's default configuration on the cfg 2 chunk
+# ---------------------------------------------------------------------------------------------
+def bench_reference_mode(args, dev):
+    """``HSAAttention(block_size=64, tau_min=0.35, tau_max=1.0, proj_segment_len=1560)`` as the
+    reference's DiT builds it (Gini routing, low-rank branch, both branches on every head), called
+    through the module on the cfg 2 chunk: ms per call (eager and graph replay) and the routing it
+    produced (mean listed blocks per row, useful sparse FLOP)."""
+    from worldattention_amd import workloads
+    from worldattention_amd.hsa import attention as WA
+
+    cfg = workloads.cfg2_reference_mode(device=dev, seed=args.seed)
+    q, k, v, mod = cfg["q"], cfg["k"], cfg["v"], cfg["module"]
+    d = q.shape[-1]
+
+    def step():
+        with torch.no_grad():
+            return mod(q, k, v)
+
+    save = {}
+    with torch.no_grad():
+        WA.hsa_forward(q, k, v, k_coarse=None, v_coarse=None, k_proj_mat=mod.k_proj_mat, v_proj_mat=mod.v_proj_mat,
+                       gate_lin=mod.gate_lin, block_size=mod.block_size, tau_min=mod.tau_min, tau_max=mod.tau_max,
+                       proj_segment_len=mod.proj_segment_len, routing="gini", topk=None, head_modes=None,
+                       linear_mode="lowrank", save=save)
+    route = save["route"]
+    useful, tiles = workloads.sparse_flops(route.num, route.index, q.shape[1], k.shape[1], mod.block_size, d)
+    steps = max(args.steps // 2, 10)
+    for _ in range(max(args.warmup // 4, 5)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    graph_ms = graph_time_ms(step, 5, steps)
+    nkv = -(-k.shape[1] // mod.block_size)
+    log(f"reference mode: {ms:.4f} ms/call (eager; graph replay {graph_ms:.4f}), mean blocks per row "
+        f"{route.num.float().mean().item():.1f} of {nkv}")
+    return {"workload": "the reference's default HSAAttention(block_size=64, tau_min=0.35, tau_max=1.0, "
+                        "proj_segment_len=1560) (Gini routing, low-rank branch, both branches on all 12 heads) "
+                        "on the cfg2 chunk (B=1 H=12 D=128 Lq=4680 Lkv=32760), bf16, block-averaging "
+                        "projections and a seeded gate",
+            "ms_per_call": round(ms, 4), "ms_per_call_graph": round(graph_ms, 4),
+            "mean_blocks_per_row": round(route.num.float().mean().item(), 2), "key_blocks": nkv,
+            "gini_thresholds": [round(x, 4) for x in route.thresholds.tolist()],
+            "sparse_useful_gflop": round(useful / 1e9, 3),
+            "effective_sparse_tflops": round(useful / (ms * 1e-3) / 1e12, 2)}
 
 
 # ---------------------------------------------------------------------------------------------
@@ -772,6 +826,9 @@ def main():
         result["cpu_baseline"] = cpu_baseline(args, cfg, proj, c2["useful_flop"])
     del cfg
     torch.cuda.empty_cache()
+    if "ref" in extras:
+        result["reference_mode"] = bench_reference_mode(args, dev)
+        torch.cuda.empty_cache()
     if "cfg3" in extras:
         result["hkv"] = bench_cfg3(args, dev)
     if "cfg5" in extras:

@@ -30,32 +30,54 @@ def assert_close(got, want, max_abs=2e-2, mean_abs=2e-3, what=""):
     assert diff.mean().item() <= mean_abs, f"{what}: mean-abs {diff.mean().item():.3e} > {mean_abs}"
 
 
-def check_topk_routing(route, parts, ks, heads, what, tie_rel=1e-5, max_tie_rows=0.01):
-    """The fused route kernel scores the pooled blocks itself, in its own fp32 summation order, so
-    two blocks whose oracle probabilities agree to ~1e-7 may trade places. Every listed position must
-    hold the oracle's block, or a block whose oracle probability is within ``tie_rel`` of it; rows
-    with such swaps must be rare. Separately, the selection from identical scores (the oracle's own
-    map through the GPU top-k) must equal the oracle's exactly."""
+def ulps_apart(a: float, b: float) -> int:
+    """Distance of two positive fp32 values in units in the last place."""
+    ia = torch.tensor([a], dtype=torch.float32).view(torch.int32).item()
+    ib = torch.tensor([b], dtype=torch.float32).view(torch.int32).item()
+    return abs(ia - ib)
+
+
+def check_near_ties(got_idx, want_idx, lengths, amap, heads, what, max_ulps=2, max_tie_rows=0.05):
+    """Each row's first ``lengths`` listed blocks: the GPU's routing kernels score the pooled blocks
+    themselves, in their own fp32 summation order, so their map can differ from the oracle's in the
+    last bit (at the reference mode's shape, 37% of entries differ, by at most 7e-10), and two
+    blocks the oracle scores within an ulp or two of each other (or exactly equal) may then trade
+    places. Every listed position must hold the oracle's block or one whose oracle probability is
+    within ``max_ulps`` fp32 ulps of it, and at most ``max_tie_rows`` of the rows may show such a
+    swap. Returns (rows with a swap, rows)."""
+    rows = swapped = 0
+    for h in heads:
+        p = amap[0, h]
+        for i in range(got_idx.shape[2]):
+            n = int(lengths[0, h, i])
+            g, r = got_idx[0, h, i, :n], want_idx[0, h, i, :n]
+            rows += 1
+            if torch.equal(g, r):
+                continue
+            swapped += 1
+            for m in torch.nonzero(g != r).flatten().tolist():
+                pg, pr = p[i, g[m]].item(), p[i, r[m]].item()
+                assert ulps_apart(pg, pr) <= max_ulps, (
+                    f"{what}: head {h} row {i} slot {m}: block {int(g[m])} (p={pg:.9g}) vs oracle "
+                    f"{int(r[m])} (p={pr:.9g})")
+    assert swapped <= max_tie_rows * rows, f"{what}: {swapped} of {rows} rows differ by near-ties"
+    print(f"{what}: {swapped} of {rows} rows hold near-tie swaps (<= {max_ulps} ulp)")
+    return swapped, rows
+
+
+def check_topk_routing(route, parts, ks, heads, what):
+    """The selection from identical scores (the oracle's own map through the GPU top-k) must equal
+    the oracle's exactly; the end-to-end routing (the fused kernel scoring the pooled blocks itself)
+    may differ from it only by near-ties (:func:`check_near_ties`)."""
     amap = parts["attn_map"]
     want = parts["routing"]
     got_idx, got_num = route.index.cpu(), route.num.cpu()
-    rows, swapped = 0, 0
     for h in heads:
-        k = ks[h]
         assert torch.equal(got_num[:, h], want.num[:, h]), f"{what}: num of head {h}"
-        g, r = got_idx[0, h, :, :k], want.index[0, h, :, :k]
-        p = amap[0, h]
-        for i in range(g.shape[0]):
-            rows += 1
-            if torch.equal(g[i], r[i]):
-                continue
-            swapped += 1
-            for m in torch.nonzero(g[i] != r[i]).flatten().tolist():
-                pg, pr = p[i, g[i, m]].item(), p[i, r[i, m]].item()
-                assert abs(pg - pr) <= tie_rel * pr, (
-                    f"{what}: head {h} row {i} slot {m}: block {int(g[i, m])} (p={pg:.9g}) vs oracle "
-                    f"{int(r[i, m])} (p={pr:.9g})")
-    assert swapped <= max_tie_rows * rows, f"{what}: {swapped} of {rows} rows differ by near-ties"
+    lengths = torch.zeros_like(want.num)
+    for h in heads:
+        lengths[:, h] = ks[h]
+    swapped, _ = check_near_ties(got_idx, want.index, lengths, amap, heads, what)
     same_scores = W.build_topk_routing(amap.to(DEV), ks)
     for h in heads:
         k = ks[h]
@@ -208,3 +230,60 @@ def test_cfg3_hkv_page_geometry_through_the_cache_api():
     assert route.index.shape[-1] == 171
     check_topk_routing(route, parts, cfg["topk"], sparse, "cfg3")
     assert_close(got, want, what="cfg3 HSA over the page pool")
+
+
+def test_reference_default_mode_at_the_wan_shape():
+    """The reference's own configuration (block 64, Gini routing, low-rank branch, both branches on
+    every head; causal_model.py:100-107) on the cfg 2 chunk through HSAAttention. Routing
+    (thresholds, counts and each row's selected blocks) equals the oracle's bit for bit on all 12
+    heads x 74 query blocks from the oracle's own map, and end to end up to near-ties (blocks the
+    oracle scores within 2 ulp of each other); outputs of sampled query blocks (first, middle, partial last) of three
+    heads are within the bf16 tolerance of the oracle's per-row attention + low-rank branch + gate."""
+    import torch.nn.functional as F
+    from worldattention_amd import _lib
+    from worldattention_amd.hsa import routing as WR
+    cfg = workloads.cfg2_reference_mode(device=DEV, seed=0)
+    q, k, v, mod = cfg["q"], cfg["k"], cfg["v"], cfg["module"]
+    b, lq, h, d = q.shape
+    lkv, bs = k.shape[1], mod.block_size
+    save = {}
+    with torch.no_grad():
+        got = WA.hsa_forward(q, k, v, k_coarse=None, v_coarse=None, k_proj_mat=mod.k_proj_mat,
+                             v_proj_mat=mod.v_proj_mat, gate_lin=mod.gate_lin, block_size=bs, tau_min=mod.tau_min,
+                             tau_max=mod.tau_max, proj_segment_len=mod.proj_segment_len, routing="gini", topk=None,
+                             head_modes=None, linear_mode="lowrank", save=save)
+        assert torch.equal(got, mod(q, k, v))              # the module call is the same path
+    torch.cuda.synchronize()
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    qpl, kpl, nq, nkv = O.block_counts(lq, lkv, bs)
+    q_p = O.pad_to_len(qc, qpl).transpose(1, 2).contiguous()
+    k_p = O.pad_to_len(kc, kpl).transpose(1, 2).contiguous()
+    v_p = O.pad_to_len(vc, kpl).transpose(1, 2).contiguous()
+    amap = O.block_attention_map(O.block_mean_pool(q_p, lq, nq, bs), O.block_mean_pool(k_p, lkv, nkv, bs))
+    want_route = O.build_block_routing(amap, mod.tau_min, mod.tau_max)
+    # from identical scores (the oracle's map), the GPU's Gini routing is the oracle's bit for bit
+    same, _ = WR._route(amap.to(DEV), None, None, mode=_lib.WA_ROUTE_GINI, tau_min=mod.tau_min, tau_max=mod.tau_max)
+    assert torch.equal(same.thresholds.cpu(), want_route.thresholds)
+    assert torch.equal(same.num.cpu(), want_route.num)
+    assert torch.equal(same.index.cpu(), want_route.index)
+    # end to end (the routing kernel scores the pooled blocks itself): the same thresholds and
+    # counts, and the same lists up to near-ties
+    route = save["route"]
+    assert torch.equal(route.thresholds.cpu(), want_route.thresholds)
+    assert torch.equal(route.num.cpu(), want_route.num)
+    check_near_ties(route.index.cpu(), want_route.index, want_route.num, amap, range(h), "reference mode")
+    sizes = O.variable_block_sizes(lkv, kpl, bs)
+    kcomp, vcomp = O.compress_kv(kc.transpose(1, 2), vc.transpose(1, 2), segment_len=mod.proj_segment_len,
+                                 k_proj_mat=mod.k_proj_mat.cpu(), v_proj_mat=mod.v_proj_mat.cpu(), block_size=bs)
+    w, bias = mod.gate_lin.weight.cpu(), mod.gate_lin.bias.cpu()
+    for hh in (0, 5, 11):
+        for i in (0, nq // 2, nq - 1):
+            rows = slice(i * bs, min((i + 1) * bs, lq))
+            sparse = O.block_sparse_attention(q_p[:, hh:hh + 1, i * bs:(i + 1) * bs], k_p[:, hh:hh + 1],
+                                              v_p[:, hh:hh + 1], want_route.index[:, hh:hh + 1, i:i + 1],
+                                              want_route.num[:, hh:hh + 1, i:i + 1], sizes, bs)
+            sparse = sparse[0, 0, :rows.stop - rows.start]
+            lin = O.linear_branch_lowrank(qc[:, rows, hh].unsqueeze(1), kcomp[:, hh:hh + 1], vcomp[:, hh:hh + 1])[0, 0]
+            gate = torch.sigmoid(F.linear(qc[0, rows, hh].to(w.dtype), w, bias)).to(lin.dtype)
+            want = torch.addcmul(sparse.to(lin.dtype), lin, gate).to(q.dtype)
+            assert_close(got[0, rows, hh], want, what=f"head {hh} query block {i}")

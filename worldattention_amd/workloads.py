@@ -98,6 +98,28 @@ def cfg2(device="cpu", seed: int = 0, dtype=torch.bfloat16) -> dict:
                 proj_segment_len=FRAME_TOKENS)
 
 
+def cfg2_reference_mode(device="cpu", seed: int = 0, dtype=torch.bfloat16) -> dict:
+    """The reference's own default HSA configuration on the cfg 2 chunk: the DiT's
+    ``HSAAttention(block_size=64, tau_min=0.35, tau_max=1.0, proj_segment_len=1560)``
+    (``wan/modules/causal_model.py:100-107``), i.e. Gini routing, the low-rank linear branch and
+    both branches on every head. Projections from the block-averaging initializer
+    (``trainer/hsa_stage.py:43-82``) and a seeded, trained-looking fusion gate. Returns the inputs
+    and the module (on ``device``, in ``dtype``)."""
+    from .hsa.attention import HSAAttention
+    from .hsa_stage import init_hsa_parameters
+
+    _, q, k, v = _wan_chunk(seed, dtype=dtype, device=device)
+    heads, d = q.shape[2], q.shape[3]
+    module = HSAAttention(num_heads=heads, head_dim=d, block_size=64, tau_min=0.35, tau_max=1.0,
+                          proj_segment_len=FRAME_TOKENS)
+    init_hsa_parameters(module)
+    gen = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        module.gate_lin.weight.copy_(torch.randn(d, d, generator=gen) * 0.05)
+        module.gate_lin.bias.copy_(torch.randn(d, generator=gen) * 0.05)
+    return dict(q=q, k=k, v=v, module=module.to(device=device, dtype=dtype))
+
+
 def cfg5(device="cpu", seed: int = 0, dtype=torch.bfloat16) -> dict:
     g, q, k, v = _wan_chunk(seed, dtype=dtype, device=device)
     modes = head_split(g, 12, 4)
