@@ -210,7 +210,8 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  *   PLAIN: o = attn;  FUSE: o = attn + g * x;  GATED: o = g * attn
  * — the gated fusion of attention.py:246-254 done in registers.
  *
- * Work is split into units of at most split_visits consecutive list entries (0 = default) per
+ * Work is split into units of at most split_visits consecutive list entries (0 = the default:
+ * WA_BSA_DEFAULT_SPLIT for 128-key blocks, WA_BSA_DEFAULT_SPLIT_64 for 64-key blocks) per
  * (row = b, head, query block). A row with one unit is written by it; the units of a longer row
  * leave normalized partials in `workspace`, and the row's last unit to finish merges them in split
  * order (results do not depend on scheduling). max_visits (0 = index_width) must bound every
@@ -224,6 +225,7 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * used them) and are 0 again when the launch completes. NULL: the launch clears counters in
  * `workspace` with one extra small kernel. Launches that overlap must not share arrivals. */
 #define WA_BSA_DEFAULT_SPLIT 16
+#define WA_BSA_DEFAULT_SPLIT_64 64
 typedef struct wa_bsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;

@@ -118,7 +118,13 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
     ("max_visits", c_int64), ("split_visits", c_int32), ("arrivals", c_void_p),
 ])
 
-BSA_DEFAULT_SPLIT = 16
+BSA_DEFAULT_SPLIT = 16      # WA_BSA_DEFAULT_SPLIT (128-key blocks)
+BSA_DEFAULT_SPLIT_64 = 64   # WA_BSA_DEFAULT_SPLIT_64 (64-key blocks)
+
+
+def bsa_default_split(block_size: int) -> int:
+    """wa_bsa_fwd's default visits per unit for this block size."""
+    return BSA_DEFAULT_SPLIT_64 if block_size == 64 else BSA_DEFAULT_SPLIT
 BSA_FWD_NOALLOC_SCRATCH_BYTES = 64 << 20   # WA_BSA_FWD_NOALLOC_SCRATCH_BYTES
 
 CompressArgs = _struct("wa_compress_args", [

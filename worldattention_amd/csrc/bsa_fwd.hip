@@ -916,6 +916,13 @@ int64_t partial_bytes(int64_t rows, int64_t max_splits, int64_t block_size, int6
   return max_splits > 1 ? (rows * max_splits * block_size * (D + 1) * 4 + 255) / 256 * 256 : 0;
 }
 
+// Default visits per unit: 16 for 128-key blocks (cfg 2: 8-32 listed blocks per row); 64 for
+// 64-key blocks, whose Gini rows list ~180 blocks at the Wan shape (fewer, longer units and merges:
+// 0.65 ms for that launch against 0.76 at 16).
+int64_t default_split(int64_t block_size) {
+  return block_size == 64 ? WA_BSA_DEFAULT_SPLIT_64 : WA_BSA_DEFAULT_SPLIT;
+}
+
 int64_t max_splits_of(int64_t max_visits, int64_t split) {
   return max_visits > 0 ? (max_visits + split - 1) / split : 1;
 }
@@ -926,7 +933,7 @@ int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream);
 
 extern "C" int64_t wa_bsa_fwd_workspace_bytes(int64_t rows, int64_t max_visits, int64_t split, int64_t block_size,
                                               int64_t D) {
-  if (split <= 0) split = WA_BSA_DEFAULT_SPLIT;
+  if (split <= 0) split = default_split(block_size);
   return partial_bytes(rows, max_splits_of(max_visits, split), block_size, D) + (rows * 4 + 255) / 256 * 256;
 }
 
@@ -984,7 +991,7 @@ extern "C" int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* a, void* stream) {
   const int64_t nkv = (a->Lkv + a->block_size - 1) / a->block_size;
   const int64_t nh = a->heads ? a->n_heads : a->H;
   const int64_t rows = a->B * nh * nq;
-  const int64_t split = a->split_visits > 0 ? a->split_visits : WA_BSA_DEFAULT_SPLIT;
+  const int64_t split = a->split_visits > 0 ? a->split_visits : default_split(a->block_size);
   const int64_t width = a->index ? a->index_width : nkv;
   const int64_t max_visits = a->max_visits > 0 ? (a->max_visits < width ? a->max_visits : width) : width;
   const int64_t need = wa_bsa_fwd_workspace_bytes(rows, max_visits, split, a->block_size, a->D);
@@ -1030,7 +1037,7 @@ int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream) {
   const int64_t nh = a->heads ? a->n_heads : a->H;
   WA_CHECK_ARG(nh >= 0 && nh <= a->H, "wa_bsa_fwd: bad head count");
   const int64_t rows = a->B * nh * nq;
-  const int64_t split = a->split_visits > 0 ? a->split_visits : WA_BSA_DEFAULT_SPLIT;
+  const int64_t split = a->split_visits > 0 ? a->split_visits : default_split(a->block_size);
   WA_CHECK_ARG(split <= 64 && (a->block_size == 64 || split <= 32),
                "wa_bsa_fwd: split_visits %lld exceeds %d", (long long)split, a->block_size == 64 ? 64 : 32);
   const int64_t width = a->index ? a->index_width : nkv;

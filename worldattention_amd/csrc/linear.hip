@@ -6,8 +6,10 @@
 // operand is staged through LDS transposed ([channel][token]).
 // The north-star elu(x)+1 linear branch lives in elu1.hip.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
+#include "tile.h"
 
 namespace {
 
@@ -27,6 +29,7 @@ struct CompressParams {
   const void* proj; int proj_dtype; int proj_rank, proj_len;
   int L, H, D, seg, block;
   void* out; int64_t o_sb, o_st, o_sh; int o_dtype;
+  int64_t x_slab;   // bytes of one (batch, head) x slab: first row to the last row's end
 };
 
 template <int D>
@@ -110,6 +113,107 @@ __global__ void __launch_bounds__(256) compress_kernel(CompressParams p) {
         }
       }
     }
+  }
+}
+
+// =============================================================================================
+// compress_kv for bf16 x with 16-byte aligned rows, as out^T[d, r] = sum_t x^T[d, t] E^T[t, r]:
+// the segment's x rows stream global -> LDS in 64-token tiles (direct-to-LDS loads, a 4-stage
+// ring, three tiles in flight; inline-assembly loads that the kernel orders itself, so the
+// compiler adds no waits of its own), each with the 32 x 64 slice of E it needs; wave w takes the A
+// operand of its 32 channels by transpose reads of the row-major x tile and the B operand (lane =
+// row r of E, 8 consecutive tokens) by one 16-byte read of the E slice. Rows of E past this
+// segment's rank and rows of x past the tensor's end read zeros (buffer range); tokens past the
+// segment's end get zero weights in its last tile. One workgroup per (segment, head, batch): the
+// compress of a tensor streams at HBM speed instead of one memory round trip per 64 tokens.
+// =============================================================================================
+template <int D>
+__global__ void __launch_bounds__(2 * D) compress_stream_kernel(CompressParams p) {
+  constexpr int NW = D / 32, TILE = 64 * D, SS = TILE + 32 * 64;  // stage: x tile, then E slice
+  constexpr int CPR = D / 8, RPI = 64 / CPR, NI = 64 / (RPI * NW);  // x tile: NI loads per wave
+  constexpr int EI = 4 / NW;                                         // E slice: EI loads per wave
+  __shared__ __attribute__((aligned(1024))) bf16_t st0[SS];
+  __shared__ __attribute__((aligned(1024))) bf16_t st1[SS];
+  __shared__ __attribute__((aligned(1024))) bf16_t st2[SS];
+  __shared__ __attribute__((aligned(1024))) bf16_t st3[SS];
+  const int sidx = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, l32 = lane & 31;
+  const int start = sidx * p.seg;
+  const int seg_len = min(p.seg, p.L - start);
+  const int rank = min(p.proj_rank, (seg_len + p.block - 1) / p.block);
+  const int row0 = sidx * min(p.proj_rank, (p.seg + p.block - 1) / p.block);
+  const int nt = (seg_len + 63) / 64;
+
+  // x tile i = segment tokens 64 i .. 64 i + 63: lane L of wave instruction k writes row
+  // (k NW + w) RPI + L / CPR, chunk slot L % CPR (dual swizzle)
+  const char* xbase = (const char*)p.x + ((int64_t)b * p.x_sb + (int64_t)h * p.x_sh) * 2;
+  int xoff[NI];
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    const int row = (k * NW + w) * RPI + lane / CPR, pos = lane % CPR;
+    xoff[k] = (int)(row * p.x_st * 2) + (pos ^ dual_swizzle<D>(row)) * 16;
+  }
+  // E slice of tile i: rank rows 0..31 x tokens 64 i .. +63 (128 bytes a row); lane L of wave
+  // instruction k writes row (k NW + w) 8 + L / 8, chunk slot L % 8 holding chunk slot ^ (row & 7)
+  int eoff[EI];
+#pragma unroll
+  for (int k = 0; k < EI; ++k) {
+    const int row = (k * NW + w) * 8 + lane / 8, pos = lane % 8;
+    eoff[k] = row < rank ? row * p.proj_len * 2 + ((pos ^ (row & 7)) * 16) : 0x7fff0000;  // past the range: 0
+  }
+  auto issue = [&](bf16_t* stage, int i) {
+    if (i >= nt) return;  // uniform
+    const int64_t o = (int64_t)(start + 64 * i) * p.x_st * 2;
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(xbase + o), (short)0, (int)(p.x_slab - o), WA_BUF_DWORD3);
+#pragma unroll
+    for (int k = 0; k < NI; ++k) lds_dma16(xrs, stage + (k * NW + w) * RPI * D, xoff[k]);
+    const __amdgpu_buffer_rsrc_t ers = __builtin_amdgcn_make_buffer_rsrc((void*)((const char*)p.proj + 128 * i), (short)0,
+                                                                         p.proj_rank * p.proj_len * 2 - 128 * i, WA_BUF_DWORD3);
+#pragma unroll
+    for (int k = 0; k < EI; ++k) lds_dma16(ers, stage + TILE + (k * NW + w) * 512, eoff[k]);
+  };
+  issue(st0, 0);
+  issue(st1, 1);
+  issue(st2, 2);
+  f32x16 acc = f32x16{};
+  // tile i computes on stage i % 4; every tile issues the same NI + EI loads per wave, so tile i has
+  // landed once at most that many per later tile remain in flight
+  auto step = [&](bf16_t* stage, bf16_t* refill, int i) {
+    const int ahead = min(2, nt - 1 - i);
+    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * (NI + EI)) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NI + EI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    bf16x8 ef[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ef[c] = *(const bf16x8*)(stage + TILE + l32 * 64 + (((2 * c + g) ^ (l32 & 7)) * 8));
+    if (64 * i + 64 > seg_len) {  // uniform: the segment's partial last tile
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ef[c][e] = 64 * i + 16 * c + 8 * g + e < seg_len ? ef[c][e] : (bf16_t)0.f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc = wa_mfma32(tile_tr8n<D>(stage, c, 32 * w, lane), ef[c], acc);
+    // the stage of tile i - 1, which every wave had read before the barrier above (issued after
+    // this tile's reads, so that no read of this stage waits for it)
+    issue(refill, i + 3);
+  };
+  for (int i = 0; i < nt; i += 4) {
+    step(st0, st3, i);
+    if (i + 1 < nt) step(st1, st0, i + 1);
+    if (i + 2 < nt) step(st2, st1, i + 2);
+    if (i + 3 < nt) step(st3, st2, i + 3);
+  }
+  // lane l32 holds rank row r = l32, channels d = 32 w + 8 (i / 4) + 4 g + i % 4
+  if (l32 >= rank) return;
+  const int64_t o0 = (int64_t)b * p.o_sb + (int64_t)(row0 + l32) * p.o_st + (int64_t)h * p.o_sh + 32 * w + 4 * g;
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wa_store_f(p.out, o0 + 8 * rq + i, acc[rq * 4 + i], p.o_dtype);
   }
 }
 
@@ -356,6 +460,19 @@ extern "C" int wa_compress_kv(const wa_compress_args* a, void* stream) {
                     a->out, a->o_sb, a->o_st, a->o_sh, a->o_dtype};
   dim3 grid((unsigned)nseg, (unsigned)a->H, (unsigned)a->B);
   hipStream_t s = (hipStream_t)stream;
+  // bf16 x with 16-byte aligned rows (and a rank of at most 32): the streaming kernel
+  const int64_t slab = ((a->L - 1) * a->x_st + a->D) * 2;
+  const int64_t rank_used = std::min<int64_t>(a->proj_rank, (std::min<int64_t>(a->segment_len, a->L) + a->block_size - 1) /
+                                                                a->block_size);
+  if ((a->D == 128 || a->D == 64) && a->x_dtype == WA_BF16 && wa_aligned16(a->x) && a->x_sb % 8 == 0 &&
+      a->x_st % 8 == 0 && a->x_sh % 8 == 0 && slab < ((int64_t)1 << 31) && rank_used <= 32 &&
+      a->proj_dtype == WA_BF16 && (((uintptr_t)a->proj) & 3) == 0 && a->proj_len % 2 == 0 &&
+      a->proj_rank * a->proj_len * 2 < ((int64_t)1 << 31)) {
+    cp.x_slab = slab;
+    if (a->D == 128) hipLaunchKernelGGL(compress_stream_kernel<128>, grid, dim3(256), 0, s, cp);
+    else hipLaunchKernelGGL(compress_stream_kernel<64>, grid, dim3(128), 0, s, cp);
+    return wa_launch_status("compress_kv");
+  }
   if (a->D == 128) hipLaunchKernelGGL(compress_kernel<128>, grid, dim3(256), 0, s, cp);
   else if (a->D == 64) hipLaunchKernelGGL(compress_kernel<64>, grid, dim3(256), 0, s, cp);
   else hipLaunchKernelGGL(compress_kernel<32>, grid, dim3(256), 0, s, cp);

@@ -391,7 +391,7 @@ def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len,
     bsz, _, heads, d = q.shape
     _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
     vis = [min(ks[h], nkv) for h in plan.sparse_only]
-    units, n_units = unit_table(bsz, vis, nq, _lib.BSA_DEFAULT_SPLIT, dev)
+    units, n_units = unit_table(bsz, vis, nq, _lib.bsa_default_split(block_size), dev)
     max_visits = max(max(vis), 1)
     n_sp, n_lin = len(plan.sparse_only), len(plan.linear_only)
     index = torch.empty((bsz, heads, nq, nkv), dtype=torch.int32, device=dev)

@@ -103,7 +103,7 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
     n_slots = heads.numel() if heads is not None else nheads
     if n_slots == 0:
         return out, lse
-    split = int(split or _lib.BSA_DEFAULT_SPLIT)
+    split = int(split or _lib.bsa_default_split(block_size))
     units, n_units, max_visits = None, 0, width
     if visits is not None:
         vis = [max(0, min(int(n), width)) for n in visits]
