@@ -57,7 +57,9 @@ __device__ __forceinline__ float round_to(float x) {
 }
 
 // Multiplies the complex pairs of f (channels d0 .. d0 + VEC of a head) that lie in the temporal
-// band (pair < nt) by the factor row, in fp32, and rounds each result to T.
+// band (pair < nt) by the factor row, in fp32, and rounds each result to T. The products and sums
+// round separately (no fused multiply-add the compiler may or may not form), so every kernel that
+// rotates keys gives the same bits.
 template <typename T, int VEC>
 __device__ __forceinline__ void rotate_band(float (&f)[VEC], int d0, const float2* frow, int nt) {
   static_assert(VEC % 2 == 0, "rotation works on whole complex pairs");
@@ -66,8 +68,8 @@ __device__ __forceinline__ void rotate_band(float (&f)[VEC], int d0, const float
     const int pr = (d0 + e) >> 1;
     if (pr < nt) {
       const float2 w = frow[pr];
-      const float re = f[e] * w.x - f[e + 1] * w.y;
-      const float im = f[e] * w.y + f[e + 1] * w.x;
+      const float re = wa_sub_rn(wa_mul_rn(f[e], w.x), wa_mul_rn(f[e + 1], w.y));
+      const float im = wa_add_rn(wa_mul_rn(f[e], w.y), wa_mul_rn(f[e + 1], w.x));
       f[e] = round_to<T>(re);
       f[e + 1] = round_to<T>(im);
     }
@@ -329,10 +331,16 @@ __global__ void __launch_bounds__(256) rerope_kernel(RopeParams p) {
 
 // =============================================================================================
 // Gather + rotate: key pages read straight from pinned host memory (through the device mapping)
-// into the cache, the temporal band rotated on the way; one factor row per page. One thread per
-// VEC-channel run of one (b, token, head); up to GR_MAX pages per launch.
+// into the cache, the temporal band rotated on the way; one factor row per page. Work item = one
+// VEC-channel run of one (b, token, head); up to GR_MAX pages per launch. The grid is small and
+// fixed (GR_BLOCKS workgroups striding over the items, each thread with GR_UNROLL host reads in
+// flight before it rotates and stores any): the host link stays saturated while the install holds
+// only a few CUs, so attention kernels running beside it keep the rest. (One thread per item made
+// ~9,400 workgroups per cfg 3 layer, each waiting on host reads and together holding every CU.)
 // =============================================================================================
 constexpr int GR_MAX = 32;
+constexpr int GR_BLOCKS = 128;
+constexpr int GR_UNROLL = 8;
 struct GRPage {
   const void* src; int64_t s_sb, s_st, s_sh;
   int tokens, dst_token;
@@ -349,24 +357,38 @@ struct GatherRotParams {
 
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256) gather_rotate_kernel(GatherRotParams p) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= p.total) return;
-  int j = 0;
-  while (j + 1 < p.n && gid >= p.pg[j + 1].start) ++j;
-  const GRPage& g = p.pg[j];
-  int64_t r = gid - g.start;
-  const int run = (int)(r % p.runs);
-  r /= p.runs;
-  const int h = (int)(r % p.H);
-  r /= p.H;
-  const int tl = (int)(r % g.tokens);
-  const int b = (int)(r / g.tokens);
-  const int d0 = run * VEC;
-  float f[VEC];
-  load_vec<T, VEC>((const T*)g.src + (int64_t)b * g.s_sb + (int64_t)tl * g.s_st + (int64_t)h * g.s_sh + d0, f);
-  if (p.factors && d0 < 2 * p.nt) rotate_band<T, VEC>(f, d0, p.factors + (int64_t)j * p.nt, p.nt);
-  store_vec<T, VEC>((T*)p.dst + (int64_t)b * p.d_sb + (int64_t)(g.dst_token + tl) * p.d_st + (int64_t)h * p.d_sh + d0,
-                    f);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t base = (int64_t)blockIdx.x * 256 + threadIdx.x; base < p.total; base += stride * GR_UNROLL) {
+    float f[GR_UNROLL][VEC];
+    int64_t dst[GR_UNROLL];
+    int page[GR_UNROLL], d0[GR_UNROLL];
+#pragma unroll
+    for (int u = 0; u < GR_UNROLL; ++u) {
+      const int64_t gid = base + u * stride;
+      page[u] = -1;
+      if (gid >= p.total) continue;
+      int j = 0;
+      while (j + 1 < p.n && gid >= p.pg[j + 1].start) ++j;
+      const GRPage& g = p.pg[j];
+      int64_t r = gid - g.start;
+      const int run = (int)(r % p.runs);
+      r /= p.runs;
+      const int h = (int)(r % p.H);
+      r /= p.H;
+      const int tl = (int)(r % g.tokens);
+      const int b = (int)(r / g.tokens);
+      page[u] = j;
+      d0[u] = run * VEC;
+      dst[u] = (int64_t)b * p.d_sb + (int64_t)(g.dst_token + tl) * p.d_st + (int64_t)h * p.d_sh + d0[u];
+      load_vec<T, VEC>((const T*)g.src + (int64_t)b * g.s_sb + (int64_t)tl * g.s_st + (int64_t)h * g.s_sh + d0[u], f[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < GR_UNROLL; ++u) {
+      if (page[u] < 0) continue;
+      if (p.factors && d0[u] < 2 * p.nt) rotate_band<T, VEC>(f[u], d0[u], p.factors + (int64_t)page[u] * p.nt, p.nt);
+      store_vec<T, VEC>((T*)p.dst + dst[u], f[u]);
+    }
+  }
 }
 
 bool fits_int(int64_t v) { return v >= 0 && v <= (int64_t)0x7fffffff; }
@@ -555,8 +577,7 @@ extern "C" int wa_hkv_gather_rotate(const wa_hkv_gather_rotate_args* a, void* st
                    "wa_hkv_gather_rotate: empty pages are not allowed with a factor table");
       p.factors = (const float2*)a->factors + p0 * a->n_temporal;
     }
-    const int64_t blocks = (total + 255) / 256;
-    WA_CHECK_ARG(blocks <= 0x7fffffff, "wa_hkv_gather_rotate: grid too large");
+    const int64_t blocks = std::min<int64_t>(GR_BLOCKS, (total + 256 * GR_UNROLL - 1) / (256 * GR_UNROLL));
     if (a->dtype == WA_BF16) {
       if (vec8) gather_rotate_kernel<bf16_t, 8><<<(unsigned)blocks, 256, 0, s>>>(p);
       else gather_rotate_kernel<bf16_t, 2><<<(unsigned)blocks, 256, 0, s>>>(p);

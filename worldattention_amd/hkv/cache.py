@@ -12,8 +12,10 @@ optional ``k_coarse`` / ``v_coarse``). What moves to the GPU path:
 * ``retrieve``: stage-1 and stage-2 scoring + top-k in ``wa_hkv_score_topk``.
 * ``apply``: per layer, on the side stream, the selected key pages are read from the pinned tier
   by one kernel that writes them into the online cache already re-rotated
-  (``wa_hkv_gather_rotate``, one factor per page from the reference's move plan), the value pages
-  are DMA copies (``wa_hkv_gather_async``, adjacent pages of a chunk merged into one copy), the
+  (``wa_hkv_gather_rotate``, one factor per page from the reference's move plan) when the caller
+  waits for the install; with ``wait=False`` they are DMA copies re-rotated in HBM by one short
+  pass (``wa_rerope``), which leaves the CUs to the attention that overlaps the install. The value
+  pages are DMA copies (``wa_hkv_gather_async``, adjacent pages of a chunk merged into one copy), the
   compressed tier is rebuilt (``wa_compress_kv``) and a per-layer event recorded; the caller's stream
   waits for the last one (or, with ``wait=False``, per layer through :meth:`wait_layer`, so layer
   l's attention overlaps the gather of the layers after it).
@@ -71,8 +73,12 @@ class HKVCache:
         self.topk_pages = int(topk_pages)
         self.stage1_topk_chunks = int(stage1_topk_chunks)
         self.rerope = bool(rerope)
-        # keys installed by the gather + re-rope kernel (False: DMA copies, then the rotation pass)
-        self.fused_install = True
+        # How apply installs keys. None: by the gather + re-rope kernel when apply waits for the
+        # install (the fastest install alone), and by DMA copies followed by the in-HBM rotation
+        # pass with wait=False, where the install overlaps attention: the copy engines leave every
+        # CU to the attention kernels (the gather kernel's workgroups compete with them for CUs).
+        # True / False force one path.
+        self.fused_install: Optional[bool] = None
         self._tier_kwargs = dict(cpu_max_chunks=cpu_max_chunks, nvme_enabled=nvme_enabled, nvme_dir=nvme_dir)
         self._side_stream: Optional[torch.cuda.Stream] = None
         self._inflight: list = []   # (event, objects) kept alive until the event completes
@@ -267,7 +273,8 @@ class HKVCache:
                     block["k_coarse"].zero_()
                     block["v_coarse"].zero_()
                 if total > 0:
-                    fused = self._gather_layer(block_idx, installed, blobs, kc, vc, total, keep, factors)
+                    fused = self._gather_layer(block_idx, installed, blobs, kc, vc, total, keep, factors,
+                                               use_kernel=wait if self.fused_install is None else self.fused_install)
                     if factors is not None and not fused:
                         rotate_temporal(kc, factors, rows=rows, t0=0, t1=total)
                     if has_coarse:
@@ -283,13 +290,13 @@ class HKVCache:
             main.wait_event(self.layer_events[-1])
         return total
 
-    def _gather_layer(self, block_idx, installed, blobs, kc, vc, total, keep, factors=None) -> bool:
-        """Pinned-tier pages of one layer -> cache tokens [0, total). Keys of the cache's dtype are
-        read by one kernel that also applies each page's re-rope factors (returns True); otherwise
-        they are DMA copies like the values (neighbouring pages of a chunk coalesce) and the caller
-        rotates afterwards."""
+    def _gather_layer(self, block_idx, installed, blobs, kc, vc, total, keep, factors=None, use_kernel=True) -> bool:
+        """Pinned-tier pages of one layer -> cache tokens [0, total). With ``use_kernel``, keys of the
+        cache's dtype are read by one kernel that also applies each page's re-rope factors (returns
+        True); otherwise they are DMA copies like the values (neighbouring pages of a chunk
+        coalesce) and the caller rotates afterwards."""
         k_srcs = [blobs[cid]["k"][block_idx] for cid, _, _ in installed]
-        fused = self.fused_install and all(src.dtype == kc.dtype for src in k_srcs)
+        fused = use_kernel and all(src.dtype == kc.dtype for src in k_srcs)
         if fused:
             pages, off = [], 0
             for (cid, s, e), src in zip(installed, k_srcs):
