@@ -279,7 +279,15 @@ int wa_bsa_fwd_noalloc(const wa_bsa_fwd_args* args, void* stream);
  * it, and at its end records join_event on the side stream and makes `stream` wait for it (so a
  * graph captured from `stream` holds both branches). NULL side_stream: everything runs on
  * `stream`. The call keeps no state and takes no lock; concurrent calls need their own side
- * stream and events. */
+ * stream and events.
+ * Training outputs (all optional; NULL for an inference call), what wa_hsa_bwd takes back:
+ * lse: [B, H, Lq] fp32 natural-log log-sum-exp of the sparse heads (wa_bsa_fwd's lse);
+ * state / zsum: where the elu1 state of the linear heads goes ([B, n_linear, D, D] and
+ * [B, n_linear, D] fp32; NULL: the workspace);
+ * lin / gate (fp32 BLHD, given together with lin_modes, a device int32[H] of head modes, 2 for a
+ * linear head and 0 otherwise): the linear heads' readout is written unfused into lin
+ * (wa_elu1_readout, PLAIN) and wa_hsa_fuse_fwd forms their gate (into gate) and output, as the
+ * autograd forward does (the output is the same as the GATED readout's). */
 typedef struct wa_hsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;
@@ -295,10 +303,56 @@ typedef struct wa_hsa_fwd_args {
   int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
   void* workspace;
   void* side_stream; void* fork_event; void* join_event;
+  float* lse;
+  float* state; float* zsum;
+  float* lin; int64_t lin_sb, lin_st, lin_sh;
+  float* gate; int64_t gate_sb, gate_st, gate_sh;
+  const int32_t* lin_modes;
 } wa_hsa_fwd_args;
 int64_t wa_hsa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t Lq, int64_t Lkv, int64_t D, int64_t block_size,
                                    int64_t n_sparse, int64_t n_linear, int64_t max_visits);
 int wa_hsa_fwd(const wa_hsa_fwd_args* args, void* stream);
+
+/* The HSA backward of heads that take one branch each, in one call: the gradients of wa_hsa_fwd's
+ * output (given its training outputs lse, state, zsum, lin and gate, its routing index / num, and
+ * the sparse heads' output o, which the forward wrote rounded to bf16 into its output).
+ * Sparse heads: wa_bsa_bwd (dq, dk, dv written). Linear heads: wa_hsa_fuse_bwd (dlin = dout * gate
+ * into the workspace, the gate path written into dq, dgate_w / dgate_b written when gate_w is
+ * given) then wa_elu1_bwd (added into dq; dk, dv written). Every gradient element of a listed
+ * head is written (no accumulation, no prior fill needed); unlisted heads are not touched.
+ * dq: fp32 or bf16 (dq_dtype; bf16: the sparse heads' dq kernel rounds its fp32 result once, the
+ * linear heads' fp32 sum in the workspace is rounded by a final pass). dk / dv: fp32 or bf16
+ * (dkv_dtype). side_stream / fork_event / join_event as in wa_hsa_fwd: the linear heads run on
+ * the side stream, concurrently with the sparse heads. Results equal those calls made one by one.
+ * Replaces the autograd of hsa_attention (wan/modules/hsa/attention.py:153-259) with the Triton
+ * backward, wan/modules/hsa/block_sparse_triton.py:353-368, for the north-star head modes. */
+typedef struct wa_hsa_bwd_args {
+  const void* q; int64_t q_sb, q_st, q_sh;
+  const void* k; int64_t k_sb, k_st, k_sh;
+  const void* v; int64_t v_sb, v_st, v_sh;
+  const void* o; int64_t o_sb, o_st, o_sh; int32_t o_dtype;
+  const void* dout; int64_t d_sb, d_st, d_sh; int32_t dout_dtype;
+  int64_t B, H, Lq, Lkv, D, block_size;
+  const int32_t* sparse_heads; int64_t n_sparse;
+  const int32_t* index; const int32_t* num;
+  const float* lse;
+  const int32_t* linear_heads; int64_t n_linear;
+  const int32_t* lin_modes;
+  const float* lin; int64_t lin_sb, lin_st, lin_sh;
+  const float* gate; int64_t gate_sb, gate_st, gate_sh;
+  const float* state; const float* zsum;
+  const void* gate_w; const float* gate_b;
+  int32_t gate_pre_bf16, gate_out_bf16, lin_round_bf16;
+  void* dq; int64_t dq_sb, dq_st, dq_sh; int32_t dq_dtype;
+  void* dk; int64_t dk_sb, dk_st, dk_sh;
+  void* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dkv_dtype;
+  float* dgate_w; float* dgate_b;
+  void* workspace;
+  void* side_stream; void* fork_event; void* join_event;
+} wa_hsa_bwd_args;
+int64_t wa_hsa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Lq, int64_t Lkv, int64_t D, int64_t block_size,
+                                   int64_t n_sparse, int64_t n_linear);
+int wa_hsa_bwd(const wa_hsa_bwd_args* args, void* stream);
 
 /* Backward of wa_bsa_fwd: dQ, dK, dV (fp32, BLHD) of the block-sparse attention output o.
  * Replaces _bwd_preprocess/_bwd_kernel/_backward, wan/modules/hsa/block_sparse_triton.py:142-368
@@ -330,6 +384,7 @@ typedef struct wa_bsa_bwd_args {
   void* dv; int64_t dv_sb, dv_st, dv_sh; int32_t dv_accumulate;
   void* workspace;
   int32_t dkv_dtype;  /* WA_F32 or WA_BF16 */
+  int32_t dq_dtype;   /* WA_F32, or WA_BF16 (rounded to nearest even once; requires dq_accumulate off) */
 } wa_bsa_bwd_args;
 int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_t Lq, int64_t Lkv, int64_t D,
                                    int64_t block_size);

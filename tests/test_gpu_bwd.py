@@ -329,3 +329,39 @@ def test_training_step_graph_replays_equal_eager_steps():
         torch.cuda.synchronize()
         for name, t, w in zip(("dq", "dk", "dv", "dW", "db"), params, want):
             assert torch.equal(t.grad, w), f"eager step after replay {i}: {name} differs"
+
+
+@pytest.mark.parametrize("which", ["cfg1", "cfg5"])
+def test_one_call_backward_equals_the_composed_calls(which, monkeypatch):
+    """Split top-k / elu1 heads with bf16 inputs train through wa_hsa_fwd (with its training
+    outputs) and wa_hsa_bwd, two library calls with the linear heads on a side stream. With the
+    one-call path switched off the same step runs the composed path (a dozen launches on one
+    stream, dq in fp32 then rounded): output and dQ, dK, dV, dW, db must agree bit for bit."""
+    cfg = workloads.cfg5(device=DEV, seed=6) if which == "cfg5" else workloads.cfg1(device=DEV)
+    if which == "cfg1":
+        cfg["q"], cfg["k"], cfg["v"] = (t * 8 for t in (cfg["q"], cfg["k"], cfg["v"]))
+    q0, k0, v0 = (cfg[n].to(DEV, torch.bfloat16) for n in ("q", "k", "v"))
+    d = q0.shape[-1]
+    gate = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        gate.weight.normal_(0, 0.05)
+        gate.bias.normal_(0, 0.05)
+    do = torch.randn(q0.shape, generator=torch.Generator().manual_seed(3)).to(DEV, torch.bfloat16)
+    kw = dict(k_proj_mat=None, v_proj_mat=None, gate_lin=gate, block_size=cfg["block_size"], routing="topk",
+              topk=cfg["topk"], head_modes=cfg["head_modes"], linear_mode="elu1",
+              proj_segment_len=cfg["proj_segment_len"])
+    results = []
+    for one_call in (True, False):
+        monkeypatch.setattr(WA, "ONE_CALL", one_call)
+        q, k, v = (t.clone().requires_grad_() for t in (q0, k0, v0))
+        gate.weight.grad = gate.bias.grad = None
+        out = W.hsa_attention(q, k, v, **kw)
+        out.backward(do)
+        results.append((out.detach().clone(), q.grad, k.grad, v.grad, gate.weight.grad.clone(),
+                        gate.bias.grad.clone()))
+    torch.cuda.synchronize()
+    one, composed = results
+    assert one[1].dtype == one[2].dtype == one[3].dtype == torch.bfloat16
+    for name, a, b in zip(("out", "dq", "dk", "dv", "dW", "db"), one, composed):
+        assert a.dtype == b.dtype, name
+        assert torch.equal(a, b), f"{which} {name}: one-call path differs from the composed calls"

@@ -181,6 +181,35 @@ HsaFwdArgs = _struct("wa_hsa_fwd_args", [
     ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
     ("workspace", c_void_p),
     ("side_stream", c_void_p), ("fork_event", c_void_p), ("join_event", c_void_p),
+    ("lse", c_void_p), ("state", c_void_p), ("zsum", c_void_p),
+    ("lin", c_void_p), ("lin_sb", c_int64), ("lin_st", c_int64), ("lin_sh", c_int64),
+    ("gate", c_void_p), ("gate_sb", c_int64), ("gate_st", c_int64), ("gate_sh", c_int64),
+    ("lin_modes", c_void_p),
+])
+
+HsaBwdArgs = _struct("wa_hsa_bwd_args", [
+    ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+    ("k", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+    ("v", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+    ("o", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64), ("o_dtype", c_int32),
+    ("dout", c_void_p), ("d_sb", c_int64), ("d_st", c_int64), ("d_sh", c_int64), ("dout_dtype", c_int32),
+    ("B", c_int64), ("H", c_int64), ("Lq", c_int64), ("Lkv", c_int64), ("D", c_int64), ("block_size", c_int64),
+    ("sparse_heads", c_void_p), ("n_sparse", c_int64),
+    ("index", c_void_p), ("num", c_void_p),
+    ("lse", c_void_p),
+    ("linear_heads", c_void_p), ("n_linear", c_int64),
+    ("lin_modes", c_void_p),
+    ("lin", c_void_p), ("lin_sb", c_int64), ("lin_st", c_int64), ("lin_sh", c_int64),
+    ("gate", c_void_p), ("gate_sb", c_int64), ("gate_st", c_int64), ("gate_sh", c_int64),
+    ("state", c_void_p), ("zsum", c_void_p),
+    ("gate_w", c_void_p), ("gate_b", c_void_p),
+    ("gate_pre_bf16", c_int32), ("gate_out_bf16", c_int32), ("lin_round_bf16", c_int32),
+    ("dq", c_void_p), ("dq_sb", c_int64), ("dq_st", c_int64), ("dq_sh", c_int64), ("dq_dtype", c_int32),
+    ("dk", c_void_p), ("dk_sb", c_int64), ("dk_st", c_int64), ("dk_sh", c_int64),
+    ("dv", c_void_p), ("dv_sb", c_int64), ("dv_st", c_int64), ("dv_sh", c_int64), ("dkv_dtype", c_int32),
+    ("dgate_w", c_void_p), ("dgate_b", c_void_p),
+    ("workspace", c_void_p),
+    ("side_stream", c_void_p), ("fork_event", c_void_p), ("join_event", c_void_p),
 ])
 
 BsaBwdArgs = _struct("wa_bsa_bwd_args", [
@@ -199,7 +228,7 @@ BsaBwdArgs = _struct("wa_bsa_bwd_args", [
     ("dk", c_void_p), ("dk_sb", c_int64), ("dk_st", c_int64), ("dk_sh", c_int64), ("dk_accumulate", c_int32),
     ("dv", c_void_p), ("dv_sb", c_int64), ("dv_st", c_int64), ("dv_sh", c_int64), ("dv_accumulate", c_int32),
     ("workspace", c_void_p),
-    ("dkv_dtype", c_int32),
+    ("dkv_dtype", c_int32), ("dq_dtype", c_int32),
 ])
 
 Elu1BwdArgs = _struct("wa_elu1_bwd_args", [
@@ -300,6 +329,8 @@ SIGNATURES = {
     "wa_elu1_readout": (c_int, [POINTER(Elu1ReadoutArgs), c_void_p]),
     "wa_hsa_fwd_workspace_bytes": (c_int64, [c_int64] * 9),
     "wa_hsa_fwd": (c_int, [POINTER(HsaFwdArgs), c_void_p]),
+    "wa_hsa_bwd_workspace_bytes": (c_int64, [c_int64] * 8),
+    "wa_hsa_bwd": (c_int, [POINTER(HsaBwdArgs), c_void_p]),
     "wa_bsa_bwd_workspace_bytes": (c_int64, [c_int64] * 6),
     "wa_bsa_bwd": (c_int, [POINTER(BsaBwdArgs), c_void_p]),
     "wa_elu1_bwd_workspace_bytes": (c_int64, [c_int64] * 4),
@@ -412,6 +443,12 @@ def kernel_ready(t: torch.Tensor, dtype=torch.bfloat16, align_elems: int = 8) ->
         if t.data_ptr() % 16 or any(s % align_elems for s in t.stride()[:-1]):
             t = t.clone(memory_format=torch.contiguous_format)
     return t
+
+
+def is_kernel_ready(t: torch.Tensor, dtype=torch.bfloat16, align_elems: int = 8) -> bool:
+    """Whether :func:`kernel_ready` would return ``t`` itself (no cast, no copy)."""
+    return (t.dtype == dtype and t.stride(-1) == 1 and not any(s % align_elems for s in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0)
 
 
 _HEAD_CACHE: dict = {}

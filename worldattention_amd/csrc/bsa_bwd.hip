@@ -39,6 +39,7 @@ struct BwdParams {
   int64_t q_slab, k_slab, v_slab;  // bytes of one (batch, head) Q / K / V slab: first row to last row's end
   float scale, scale_log2;
   float* dq; int64_t dq_sb, dq_st, dq_sh; int dq_acc;
+  int dq_bf16;   // dq is bf16 (written once, rounded from the fp32 result) instead of fp32
   void* dk; int64_t dk_sb, dk_st, dk_sh; int dk_acc;
   void* dv; int64_t dv_sb, dv_st, dv_sh; int dv_acc;
   int dkv_bf16;  // dk / dv are bf16 (written once) instead of fp32
@@ -441,7 +442,20 @@ __global__ void __launch_bounds__(2 * BS) __attribute__((amdgpu_waves_per_eu(2))
   // accumulator lane (d = 32t + l32, g) holds rows q = 32w + 8(r/4) + 4g + r%4. With accumulation
   // every previous value of a tile is read before any store, so the reads overlap (a store may
   // alias a later read, which would otherwise serialize each read-add-write round trip).
-  float* dq_col = p.dq + (int64_t)b * p.dq_sb + (int64_t)h * p.dq_sh + l32;
+  const int64_t dq_off = (int64_t)b * p.dq_sb + (int64_t)h * p.dq_sh + l32;
+  if (p.dq_bf16) {
+    bf16_t* dq_out = (bf16_t*)p.dq + dq_off;
+#pragma unroll
+    for (int tt = 0; tt < DT; ++tt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int q = qb * BS + w * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (q < p.Lq) dq_out[(int64_t)q * p.dq_st + 32 * tt] = (bf16_t)(dqacc[tt][r] * p.scale);
+      }
+    }
+    return;
+  }
+  float* dq_col = p.dq + dq_off;
 #pragma unroll
   for (int tt = 0; tt < DT; ++tt) {
     float prev[16];
@@ -855,6 +869,8 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(a->dq || (a->dk && a->dv), "wa_bsa_bwd: nothing to compute");
   WA_CHECK_ARG(a->dkv_dtype == WA_F32 || (a->dkv_dtype == WA_BF16 && !a->dk_accumulate && !a->dv_accumulate),
                "wa_bsa_bwd: dkv_dtype must be WA_F32, or WA_BF16 without accumulation");
+  WA_CHECK_ARG(a->dq_dtype == WA_F32 || (a->dq_dtype == WA_BF16 && !a->dq_accumulate),
+               "wa_bsa_bwd: dq_dtype must be WA_F32, or WA_BF16 without accumulation");
   WA_CHECK_ARG(wa_aligned16(a->q) && wa_aligned16(a->k) && wa_aligned16(a->v) && wa_aligned16(a->workspace),
                "wa_bsa_bwd: q/k/v/workspace must be 16-byte aligned");
   WA_CHECK_ARG(a->q_sb % 8 == 0 && a->q_st % 8 == 0 && a->q_sh % 8 == 0 && a->k_sb % 8 == 0 && a->k_st % 8 == 0 &&
@@ -893,6 +909,7 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   bp.scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)a->D);
   bp.scale_log2 = bp.scale * WA_LOG2E;
   bp.dq = a->dq; bp.dq_sb = a->dq_sb; bp.dq_st = a->dq_st; bp.dq_sh = a->dq_sh; bp.dq_acc = a->dq_accumulate;
+  bp.dq_bf16 = a->dq_dtype == WA_BF16;
   bp.dk = a->dk; bp.dk_sb = a->dk_sb; bp.dk_st = a->dk_st; bp.dk_sh = a->dk_sh; bp.dk_acc = a->dk_accumulate;
   bp.dv = a->dv; bp.dv_sb = a->dv_sb; bp.dv_st = a->dv_st; bp.dv_sh = a->dv_sh; bp.dv_acc = a->dv_accumulate;
   bp.dkv_bf16 = a->dkv_dtype == WA_BF16;

@@ -14,6 +14,7 @@ import torch
 
 from .. import _lib
 from ._bwd import bsa_backward
+from .attention import _fork_join
 from .block_sparse import bsa_forward
 from .routing import _route, block_counts, pool_for_routing
 
@@ -142,16 +143,25 @@ def compress_autograd(x, proj, segment_len, block_size):
 # ----------------------------------------------------------------------------------------------
 # hsa_attention under autograd
 # ----------------------------------------------------------------------------------------------
+class _GateParams:
+    """The gate layer's weight and bias as the autograd function receives them."""
+    __slots__ = ("weight", "bias")
+
+    def __init__(self, weight, bias):
+        self.weight, self.bias = weight, bias
+
+
 class _HSA(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b, cfg):
-        from .attention import GateSpec, HeadPlan, _compress, _per_head_k, elu1_readout, elu1_state
+        from .attention import (GateSpec, _compress, _native_split_forward, _per_head_k, elu1_readout, elu1_state,
+                                head_plan, native_split_eligible)
 
         block_size, routing, topk, linear_mode = cfg["block_size"], cfg["routing"], cfg["topk"], cfg["linear_mode"]
         bsz, q_len, heads, d = q.shape
         kv_len = k.shape[1]
         dev = _lib.require_gpu(q, k, v, k_coarse, v_coarse)
-        plan = HeadPlan(heads, cfg["head_modes"], dev)
+        plan = head_plan(heads, cfg["head_modes"], dev)
         if linear_mode == "lowrank":
             comp = v_coarse.dtype if v_coarse is not None else v.dtype
         else:
@@ -159,17 +169,28 @@ class _HSA(torch.autograd.Function):
         if comp not in (torch.float32, torch.bfloat16):
             comp = torch.float32
 
-        class _Gate:
-            pass
-        gate_lin = None
-        if gate_w is not None:
-            gate_lin = _Gate()
-            gate_lin.weight, gate_lin.bias = gate_w, gate_b
-        spec = GateSpec(gate_lin, comp)
+        spec = GateSpec(_GateParams(gate_w, gate_b) if gate_w is not None else None, comp)
         lin_round = comp == torch.bfloat16
         modes = [(MODE_SPARSE if h in plan.sparse else 0) | (MODE_LINEAR if h in plan.linear else 0)
                  for h in range(heads)]
         modes_t = _lib.head_list(modes, dev)
+
+        ctx.cfg = cfg
+        ctx.has_coarse = k_coarse is not None
+        ctx.dtypes = tuple(t.dtype if t is not None else None
+                           for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b))
+        if native_split_eligible(q, k, v, plan, routing, linear_mode, cfg["k_block_sums"], cfg["k_pooled"]):
+            # one library call (wa_hsa_fwd with its training outputs); the backward is wa_hsa_bwd
+            out = torch.empty((bsz, q_len, heads, d), dtype=comp, device=dev)
+            tr = {}
+            _native_split_forward(q, k, v, plan, _per_head_k(topk, heads), spec, lin_round, block_size, q_len,
+                                  kv_len, out, None, train=tr)
+            ctx.native = True
+            ctx.extra = dict(plan=plan, spec=spec, lin_round=lin_round, lin_modes=tr["lin_modes"])
+            ctx.save_for_backward(q, k, v, out, tr["lse"], tr["state"], tr["zsum"], tr["lin"], tr["gate"],
+                                  tr["index"], tr["num"])
+            return out if out.dtype == q.dtype else out.to(q.dtype)
+        ctx.native = False
 
         qb, kb, vb = _lib.kernel_ready(q), _lib.kernel_ready(k), _lib.kernel_ready(v)
         f32 = dict(dtype=torch.float32, device=dev)
@@ -228,11 +249,7 @@ class _HSA(torch.autograd.Function):
             fuse_forward(qb, sparse, lin, modes_t, gate, spec, out, attn_round=True, lin_round=lin_round)
         sparse_o = out if split else sparse  # the sparse heads' O for the backward
 
-        ctx.cfg = cfg
         ctx.extra = saved
-        ctx.has_coarse = k_coarse is not None
-        ctx.dtypes = tuple(t.dtype if t is not None else None
-                           for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b))
         ctx.save_for_backward(q, k, v, qb, kb, vb, sparse_o if plan.sparse else None, lin, gate, lse_s, lse_l, kc,
                               vc, kcb, vcb, state, zsum,
                               route.index if route is not None else None,
@@ -241,6 +258,8 @@ class _HSA(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
+        if ctx.native:
+            return _native_split_backward(ctx, dout)
         (q, k, v, qb, kb, vb, sparse, lin, gate, lse_s, lse_l, kc, vc, kcb, vcb, state, zsum, index, num,
          k_proj_mat, v_proj_mat) = ctx.saved_tensors
         cfg, ex = ctx.cfg, ctx.extra
@@ -294,6 +313,50 @@ class _HSA(torch.autograd.Function):
         return (cast(dq, qd), cast(dk, kd), cast(dv, vd),
                 cast(dkc, kcd) if ctx.has_coarse else None, cast(dvc, vcd) if ctx.has_coarse else None,
                 cast(dEk, ekd), cast(dEv, evd), cast(dgw, gwd), cast(dgb, gbd), None)
+
+
+def _native_split_backward(ctx, dout):
+    """The backward of the one-call forward in one library call (``wa_hsa_bwd``): the sparse heads'
+    ``wa_bsa_bwd`` on the caller's stream, the linear heads' gate and elu1 backward on its side
+    stream (:func:`_fork_join`); dq, dk and dv are written once, in bf16 when their inputs are."""
+    q, k, v, out, lse, state, zsum, lin, gate, index, num = ctx.saved_tensors
+    cfg, ex = ctx.cfg, ctx.extra
+    plan, spec = ex["plan"], ex["spec"]
+    dev = q.device
+    bsz, q_len, heads, d = q.shape
+    kv_len = k.shape[1]
+    dout = dout if dout.stride(-1) == 1 and dout.dtype in (torch.float32, torch.bfloat16) else dout.float().contiguous()
+    qd, kd, vd = ctx.dtypes[:3]
+    dq = torch.empty(q.shape, dtype=torch.bfloat16 if qd == torch.bfloat16 else torch.float32, device=dev)
+    kv_dt = torch.bfloat16 if kd == vd == torch.bfloat16 else torch.float32
+    dk = torch.empty(k.shape, dtype=kv_dt, device=dev)
+    dv = torch.empty(v.shape, dtype=kv_dt, device=dev)
+    dgw = dgb = None
+    if spec.w is not None:
+        dgw = torch.empty((d, d), dtype=torch.float32, device=dev)
+        dgb = torch.empty((d,), dtype=torch.float32, device=dev)
+    n_sp, n_lin = len(plan.sparse_only), len(plan.linear_only)
+    block_size = cfg["block_size"]
+    ws = torch.empty((_lib.lib().wa_hsa_bwd_workspace_bytes(bsz, heads, q_len, kv_len, d, block_size, n_sp, n_lin),),
+                     dtype=torch.uint8, device=dev)
+    main = torch.cuda.current_stream(dev)
+    side, fork, join = _fork_join(dev, main)
+    args = _lib.HsaBwdArgs(
+        *_lib.blhd(q), *_lib.blhd(k), *_lib.blhd(v), *_lib.blhd(out), _lib.dtype_code(out),
+        *_lib.blhd(dout), _lib.dtype_code(dout),
+        bsz, heads, q_len, kv_len, d, block_size,
+        *_lib.heads_arg(plan.t["sparse_only"]), index.data_ptr(), num.data_ptr(), lse.data_ptr(),
+        *_lib.heads_arg(plan.t["linear_only"]), ex["lin_modes"].data_ptr(), *_lib.blhd(lin), *_lib.blhd(gate),
+        state.data_ptr(), zsum.data_ptr(),
+        _lib.ptr(spec.w), _lib.ptr(spec.b), int(spec.pre_bf16), int(spec.out_bf16), int(ex["lin_round"]),
+        *_lib.blhd(dq), _lib.dtype_code(dq), *_lib.blhd(dk), *_lib.blhd(dv), _lib.dtype_code(dk),
+        _lib.ptr(dgw), _lib.ptr(dgb), ws.data_ptr(), side.cuda_stream, fork.cuda_event, join.cuda_event)
+    _lib.call("wa_hsa_bwd", args, main.cuda_stream)
+    qd, kd, vd, kcd, vcd, ekd, evd, gwd, gbd = ctx.dtypes
+
+    def cast(t, dt):
+        return None if t is None or dt is None else t.to(dt)
+    return (cast(dq, qd), cast(dk, kd), cast(dv, vd), None, None, None, None, cast(dgw, gwd), cast(dgb, gbd), None)
 
 
 def hsa_attention_autograd(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,

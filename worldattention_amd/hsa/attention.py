@@ -184,6 +184,18 @@ class HeadPlan:
                                     ("linear", self.linear))}
 
 
+_PLAN_CACHE: dict = {}
+
+
+def head_plan(heads: int, head_modes: Optional[Sequence[str]], device) -> HeadPlan:
+    """:class:`HeadPlan` of a head-mode list, cached per (heads, modes, device)."""
+    key = (heads, tuple(head_modes) if head_modes is not None else None, str(device))
+    plan = _PLAN_CACHE.get(key)
+    if plan is None:
+        plan = _PLAN_CACHE[key] = HeadPlan(heads, head_modes, device)
+    return plan
+
+
 def elu1_state(k: torch.Tensor, v: torch.Tensor, heads_t: torch.Tensor):
     """``S^T`` ([B, n, D, D], fp32) and ``z`` ([B, n, D]) of the listed heads (``wa_elu1_state``)."""
     dev = _lib.require_gpu(k, v)
@@ -281,7 +293,7 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
         raise ValueError(f"routing must be one of {_ROUTING_MODES}")
     if linear_mode not in _LINEAR_MODES:
         raise ValueError(f"linear_mode must be one of {_LINEAR_MODES}")
-    plan = HeadPlan(heads, head_modes, dev)
+    plan = head_plan(heads, head_modes, dev)
 
     out_dtype = q.dtype
     if linear_mode == "lowrank":
@@ -293,16 +305,14 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     gate = GateSpec(gate_lin, comp_dtype)
     lin_round = comp_dtype == torch.bfloat16
 
-    qb = _lib.kernel_ready(q)
-    kb = _lib.kernel_ready(k)
-    vb = _lib.kernel_ready(v)
     out = torch.empty((bsz, q_len, heads, head_dim), dtype=comp_dtype, device=dev)
-    if (routing == "topk" and linear_mode == "elu1" and plan.sparse_only and plan.linear_only and not plan.both
-            and k_block_sums is None and k_pooled is None and qb is q and kb is k and vb is v
-            and q.dtype == torch.bfloat16):
+    if native_split_eligible(q, k, v, plan, routing, linear_mode, k_block_sums, k_pooled):
         _native_split_forward(q, k, v, plan, _per_head_k(topk, heads), gate, lin_round, block_size, q_len, kv_len,
                               out, save)
         return out if out.dtype == out_dtype else out.to(out_dtype)
+    qb = _lib.kernel_ready(q)
+    kb = _lib.kernel_ready(k)
+    vb = _lib.kernel_ready(v)
     lin_tmp = torch.empty_like(out) if plan.both else None
 
     # With both branches present the linear branch runs on a side stream, concurrently with
@@ -379,14 +389,32 @@ def _fork_join(dev: torch.device, main: torch.cuda.Stream):
     return ent
 
 
-def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len, kv_len, out, save):
+# Whether calls the one-call library path covers take it. False runs the same entry points one
+# launch at a time from Python (the same results; a reference point for comparisons).
+ONE_CALL = True
+
+
+def native_split_eligible(q, k, v, plan, routing, linear_mode, k_block_sums=None, k_pooled=None) -> bool:
+    """Whether the one-call library path (``wa_hsa_fwd`` / ``wa_hsa_bwd``) covers this call: top-k
+    sparse heads and elu1 linear heads, no head in both branches, bf16 q / k / v that the kernels
+    read in place, routing from pooled keys."""
+    return (ONE_CALL and routing == "topk" and linear_mode == "elu1" and bool(plan.sparse_only) and bool(plan.linear_only)
+            and not plan.both and k_block_sums is None and k_pooled is None
+            and all(_lib.is_kernel_ready(t) for t in (q, k, v)))
+
+
+def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len, kv_len, out, save, train=None):
     """:func:`hsa_forward` of top-k sparse heads and elu1 linear heads as one library call
     (``wa_hsa_fwd``): the same entry points with the same arguments as the Python orchestration,
     the linear heads' on a side stream of the caller's stream (see :func:`_fork_join`) that the
     call forks and joins inside (so graph capture records the same two branches). An eager call
     then pays one crossing into the library instead of ~20 (allocations, argument structs,
     launches, events): 171 -> 48 us of host time, and at cfg 2 the eager call went from 195 to
-    141 us (GPU-bound)."""
+    141 us (GPU-bound).
+
+    ``train`` (a dict): the call also writes what the one-call backward takes back (the sparse
+    heads' log-sum-exp, the elu1 state, the unfused linear readout and its gate), stored in it with
+    the routing and the linear heads' mode list."""
     dev = q.device
     bsz, _, heads, d = q.shape
     _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
@@ -400,6 +428,16 @@ def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len,
                                                              max_visits),), dtype=torch.uint8, device=dev)
     main = torch.cuda.current_stream(dev)
     side, fork, join = _fork_join(dev, main) if n_sp and n_lin else (None, None, None)
+    extra = ()
+    if train is not None:
+        f32 = dict(dtype=torch.float32, device=dev)
+        lin = torch.empty((bsz, q_len, heads, d), **f32)
+        train.update(lse=torch.empty((bsz, heads, q_len), **f32), state=torch.empty((bsz, n_lin, d, d), **f32),
+                     zsum=torch.empty((bsz, n_lin, d), **f32), lin=lin, gate=torch.empty_like(lin),
+                     lin_modes=_lib.head_list([2 if h in plan.linear else 0 for h in range(heads)], dev),
+                     index=index, num=num)
+        extra = (train["lse"].data_ptr(), train["state"].data_ptr(), train["zsum"].data_ptr(), *_lib.blhd(lin),
+                 *_lib.blhd(train["gate"]), train["lin_modes"].data_ptr())
     args = _lib.HsaFwdArgs(*_lib.blhd(q), *_lib.blhd(k), *_lib.blhd(v), *_lib.blhd(out), _lib.dtype_code(out),
                            bsz, heads, q_len, kv_len, d, block_size,
                            *_lib.heads_arg(plan.t["sparse_only"]), _lib.head_list(ks, dev).data_ptr(),
@@ -408,7 +446,7 @@ def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len,
                            int(gate.pre_bf16), int(gate.out_bf16), int(lin_round), ws.data_ptr(),
                            side.cuda_stream if side is not None else None,
                            fork.cuda_event if fork is not None else None,
-                           join.cuda_event if join is not None else None)
+                           join.cuda_event if join is not None else None, *extra)
     # the call ends with the caller's stream waiting for the side stream, so later work on it (and
     # the allocator's reuse of the workspace) is ordered after the linear branch
     _lib.call("wa_hsa_fwd", args, main.cuda_stream)
