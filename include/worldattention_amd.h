@@ -109,6 +109,9 @@ typedef struct wa_route_args {
   int64_t k_sum_len, block_size;
   int32_t k_sum_bf16;
   int64_t k_pooled_blocks;
+  /* scale (0: D^-1/2): the logit scale of the map. A caller that pads the head dim passes the
+   * scale of its original head dim (routing.py:66 scales by the pooled vectors' own length). */
+  float scale;
 } wa_route_args;
 int64_t wa_route_workspace_bytes(int64_t B, int64_t H, int64_t Nq, int64_t Nkv);
 int wa_route(const wa_route_args* args, void* stream);
@@ -148,7 +151,10 @@ int wa_kv_append(const wa_kv_append_args* args, void* stream);
  * w_dtype bf16 or fp32; both NULL: no norm): x * rsqrt(mean(x^2) + eps) over a token's H * D
  * channels in fp32, summed in torch's CPU order, rounded to the dtype, times the weight in the wider
  * of the two dtypes. With k_sums (fp32 [B, H, ceil(cap / block_size), D], no reference
- * counterpart) the key block sums of the written blocks are then refreshed as wa_kv_append does. */
+ * counterpart) the key block sums of the written blocks are then refreshed as wa_kv_append does.
+ * sample_grids (optional, HOST int64 [B][3]): each sample's own (f, h, w), as the reference's
+ * per-sample loop over grid_sizes (causal_model.py:43) takes them; grid_f / grid_h / grid_w are then
+ * ignored. Samples whose grids differ run in separate launches. */
 typedef struct wa_qkv_epilogue_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;
@@ -163,6 +169,7 @@ typedef struct wa_qkv_epilogue_args {
   int64_t grid_f, grid_h, grid_w, start_frame;
   const void* q_norm_w; const void* k_norm_w; int32_t w_dtype; float eps;
   float* k_sums; int64_t block_size;
+  const int64_t* sample_grids;
 } wa_qkv_epilogue_args;
 int wa_qkv_epilogue(const wa_qkv_epilogue_args* args, void* stream);
 

@@ -36,13 +36,28 @@ def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float) -> tor
     return normed * weight
 
 
+def _grids(grid, batch: int):
+    """Per-sample ``(f, h, w)`` rows: a triple is shared by the batch, a ``[B, 3]`` list / tensor
+    gives each sample its own (``grid_sizes`` of ``causal_model.py:43``)."""
+    rows = grid.tolist() if isinstance(grid, torch.Tensor) else grid
+    if len(rows) and isinstance(rows[0], (list, tuple)):
+        if len(rows) != batch:
+            raise ValueError(f"{len(rows)} grids for a batch of {batch}")
+        return [tuple(int(v) for v in r) for r in rows]
+    return [tuple(int(v) for v in rows)] * batch
+
+
 def causal_rope(x: torch.Tensor, grid, freqs: torch.Tensor, start_frame: int) -> torch.Tensor:
-    """3-D RoPE of ``[B, L, H, D]`` (grid ``(f, h, w)`` shared by the batch); tokens past
-    ``f * h * w`` pass through (``causal_model.py:34-62``)."""
-    f, h, w = grid
-    seq = f * h * w
-    rot = OK.rope_apply_3d(x[:, :seq], freqs, f, h, w, start_frame=start_frame)
-    return torch.cat([rot, x[:, seq:]], dim=1) if seq < x.shape[1] else rot
+    """3-D RoPE of ``[B, L, H, D]``; ``grid``: one ``(f, h, w)`` for the batch or one per sample;
+    each sample's tokens past its ``f * h * w`` pass through (``causal_model.py:34-62``, which loops
+    over the samples)."""
+    out = []
+    for i, (f, h, w) in enumerate(_grids(grid, x.shape[0])):
+        seq = f * h * w
+        xi = x[i:i + 1]
+        rot = OK.rope_apply_3d(xi[:, :seq], freqs, f, h, w, start_frame=start_frame)
+        out.append(torch.cat([rot, xi[:, seq:]], dim=1) if seq < x.shape[1] else rot)
+    return torch.cat(out, dim=0)
 
 
 def cache_step(kv_cache: dict, q, k, v, *, grid, freqs, current_start: int, sink_size: int,
@@ -58,7 +73,8 @@ def cache_step(kv_cache: dict, q, k, v, *, grid, freqs, current_start: int, sink
     b, n_tok, heads, d = q.shape  # the norms run over a token's H * D channels, before the head view
     q = rms_norm(q.reshape(b, n_tok, heads * d), norm_q, eps).reshape(b, n_tok, heads, d)
     k = rms_norm(k.reshape(b, n_tok, heads * d), norm_k, eps).reshape(b, n_tok, heads, d)
-    frame_seqlen = grid[1] * grid[2]
+    g0 = _grids(grid, b)[0]  # the frame length of sample 0, as causal_model.py:269 takes it
+    frame_seqlen = g0[1] * g0[2]
     start_frame = current_start // frame_seqlen
     roped_q = causal_rope(q, grid, freqs, start_frame).type_as(v)
     roped_k = causal_rope(k, grid, freqs, start_frame).type_as(v)

@@ -104,6 +104,25 @@ def test_qkv_epilogue_matches_oracle(dtype, w_dtype, d):
         _close(got_means, means[:, :, first:], 1e-5, 1e-6, "block sums / count")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qkv_epilogue_with_one_grid_per_sample_matches_oracle(dtype):
+    """grid_sizes with a grid of its own per sample (``causal_model.py:43`` loops over them): three
+    samples, the first two sharing a grid (one launch) and the third with another (a second
+    launch); each sample's tokens past its grid pass through unrotated. No norm: bit-exact."""
+    torch.manual_seed(7)
+    b, h, d, n = 3, 2, 64, 80
+    grids = [[2, 4, 8], [2, 4, 8], [3, 5, 5]]   # 64, 64 and 75 tokens
+    q, k, v = (torch.randn(b, n, h, d).to(dtype) * 3 for _ in range(3))
+    freqs = OK.rope_freqs(64, d)
+    cache = {"k": torch.zeros(b, 128, h, d, dtype=dtype, device=DEV),
+             "v": torch.zeros(b, 128, h, d, dtype=dtype, device=DEV)}
+    got_q = KV.qkv_epilogue(q.to(DEV), k.to(DEV), v.to(DEV), cache, grid_sizes=torch.tensor(grids), freqs=freqs,
+                            start_frame=5, write_start=20, src_offset=0, write_len=n)
+    _equal(got_q, OC.causal_rope(q, grids, freqs, 5).to(dtype), "roped q, per-sample grids")
+    _equal(cache["k"][:, 20:20 + n], OC.causal_rope(k, grids, freqs, 5).to(dtype), "cache k, per-sample grids")
+    _equal(cache["v"][:, 20:20 + n], v, "cache v")
+
+
 def test_qkv_epilogue_rejects_bad_arguments():
     d, h = 64, 2
     q = torch.randn(1, 10, h, d, device=DEV).bfloat16()
@@ -114,8 +133,13 @@ def test_qkv_epilogue_rejects_bad_arguments():
         KV.qkv_epilogue(q, q, q, cache, grid_sizes=(1, 2, 5), freqs=freqs, start_frame=0, write_start=10)
     with pytest.raises(ValueError, match="rows of the RoPE table"):
         KV.qkv_epilogue(q, q, q, cache, grid_sizes=(1, 2, 5), freqs=freqs, start_frame=8, write_start=0)
-    with pytest.raises(ValueError, match="one grid"):
+    with pytest.raises(ValueError, match="grids for a batch"):
         KV.qkv_epilogue(q, q, q, cache, grid_sizes=[[1, 2, 5], [2, 1, 5]], freqs=freqs, start_frame=0,
+                        write_start=0)
+    q2 = torch.randn(2, 10, h, d, device=DEV).bfloat16()
+    cache2 = {n: torch.zeros(2, 16, h, d, dtype=torch.bfloat16, device=DEV) for n in ("k", "v")}
+    with pytest.raises(ValueError, match="rows of the RoPE table"):  # checked for every sample
+        KV.qkv_epilogue(q2, q2, q2, cache2, grid_sizes=[[1, 2, 5], [1, 1, 9]], freqs=freqs, start_frame=0,
                         write_start=0)
     with pytest.raises(ValueError, match="both RMSNorm"):
         KV.qkv_epilogue(q, q, q, cache, grid_sizes=(1, 2, 5), freqs=freqs, start_frame=0, write_start=0,
@@ -210,3 +234,37 @@ def test_cache_step_sequence_matches_oracle(sink_size, max_frames):
             _, p_got = _route(None, qp2, held, mode=_lib.WA_ROUTE_TOPK, head_k=[4] * h, want_probs=True,
                               **key_args)
             _equal(p_got, p_want, f"{what}: routing from the kept sums")
+
+
+def test_cache_step_with_one_grid_per_sample_matches_oracle():
+    """A batch of two whose samples have their own grids (the second holds two frames of the
+    three-frame chunk, so its last frame's tokens pass through unrotated): four chunks through a
+    five-frame cache with a one-frame sink (inserts, then rolls), with RMSNorm; the frame length and
+    the cache indices come from sample 0, as the reference's step takes them."""
+    torch.manual_seed(21)
+    b, h, d, gh, gw = 2, 2, 64, 4, 32
+    fs = gh * gw
+    grids = [[3, gh, gw], [2, gh, gw]]
+    chunk, cap = 3 * fs, 5 * fs
+    freqs = OK.rope_freqs(1024, d)
+    wq, wk = (torch.rand(h * d) + 0.5).bfloat16(), (torch.rand(h * d) + 0.5).bfloat16()
+    gpu = {"k": torch.zeros(b, cap, h, d, dtype=torch.bfloat16, device=DEV),
+           "v": torch.zeros(b, cap, h, d, dtype=torch.bfloat16, device=DEV),
+           "global_end_index": torch.tensor([0], device=DEV), "local_end_index": torch.tensor([0], device=DEV)}
+    cpu = {key: t.cpu().clone() for key, t in gpu.items()}
+    kw = dict(sink_size=1, local_attn_size=5, max_attention_size=5 * fs, eps=1e-6)
+    for step, start in enumerate(i * chunk for i in range(4)):
+        q, k, v = (torch.randn(b, chunk, h, d).bfloat16() for _ in range(3))
+        rq, ak, av, _, _, info = KV.cache_step(gpu, q.to(DEV), k.to(DEV), v.to(DEV), grid_sizes=torch.tensor(grids),
+                                               freqs=freqs, current_start=start, norm_q=wq.to(DEV),
+                                               norm_k=wk.to(DEV), **kw)
+        oq, ok_, ov, _, _, oinfo = OC.cache_step(cpu, q, k, v, grid=grids, freqs=freqs, current_start=start,
+                                                 norm_q=wq, norm_k=wk, **kw)
+        what = f"step {step} (start {start})"
+        for key in ("write_start_index", "write_end_index", "local_end_index", "num_evicted_tokens"):
+            assert info[key] == oinfo[key], f"{what}: {key} {info[key]} vs {oinfo[key]}"
+        _within_pair_ulp(rq, oq, f"{what}: roped q")
+        _within_pair_ulp(ak, ok_, f"{what}: window k")
+        _equal(av, ov, f"{what}: window v")
+        _within_pair_ulp(gpu["k"], cpu["k"], f"{what}: cache k")
+        _equal(gpu["v"], cpu["v"], f"{what}: cache v")

@@ -60,6 +60,22 @@ def test_causal_rope_matches_a_per_element_rotation(d):
     assert torch.equal(got[:, 24:], x[:, 24:])  # past the grid: unrotated
 
 
+def test_causal_rope_with_one_grid_per_sample_matches_a_per_element_rotation():
+    """A batch whose samples have different grids (``causal_model.py:43`` loops over them): each
+    sample rotates by its own grid and passes the tokens past it through."""
+    torch.manual_seed(3)
+    d = 64
+    x = torch.randn(2, 30, 2, d, dtype=torch.float64)
+    freqs = OK.rope_freqs(64, d)
+    grids = [(2, 3, 4), (1, 5, 5)]
+    got = OC.causal_rope(x, grids, freqs, start_frame=3)
+    for i, (f, h, w) in enumerate(grids):
+        seq = f * h * w
+        want = _brute_rope(x[i:i + 1, :seq], f, h, w, 3)
+        torch.testing.assert_close(got[i:i + 1, :seq], want, rtol=1e-12, atol=1e-12)
+        assert torch.equal(got[i, seq:], x[i, seq:])
+
+
 def _ids(n, h, d, start):
     """Tokens whose every channel holds the token's global index (exact in fp32)."""
     t = torch.arange(start, start + n, dtype=torch.float32).view(1, n, 1, 1)

@@ -43,7 +43,7 @@ RouteArgs = _struct("wa_route_args", [
     ("index", c_void_p), ("num", c_void_p), ("thresholds", c_void_p), ("mask", c_void_p),
     ("probs_out", c_void_p), ("workspace", c_void_p), ("clear", c_void_p), ("n_clear", c_int64),
     ("k_sum_len", c_int64), ("block_size", c_int64), ("k_sum_bf16", c_int32),
-    ("k_pooled_blocks", c_int64),
+    ("k_pooled_blocks", c_int64), ("scale", c_float),
 ])
 
 KvAppendArgs = _struct("wa_kv_append_args", [
@@ -71,6 +71,7 @@ QkvEpilogueArgs = _struct("wa_qkv_epilogue_args", [
     ("grid_f", c_int64), ("grid_h", c_int64), ("grid_w", c_int64), ("start_frame", c_int64),
     ("q_norm_w", c_void_p), ("k_norm_w", c_void_p), ("w_dtype", c_int32), ("eps", c_float),
     ("k_sums", c_void_p), ("block_size", c_int64),
+    ("sample_grids", POINTER(c_int64)),
 ])
 
 KvRollArgs = _struct("wa_kv_roll_args", [

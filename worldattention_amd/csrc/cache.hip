@@ -282,13 +282,22 @@ extern "C" int wa_qkv_epilogue(const wa_qkv_epilogue_args* a, void* stream) {
                "wa_qkv_epilogue: write of %lld tokens from %lld to cache token %lld does not fit (n %lld, cap %lld)",
                (long long)a->write_len, (long long)a->src_offset, (long long)a->write_start, (long long)a->n,
                (long long)a->cap);
-  WA_CHECK_ARG(a->grid_f >= 0 && a->grid_h > 0 && a->grid_w > 0 && a->start_frame >= 0,
-               "wa_qkv_epilogue: bad grid");
-  const int64_t seq_len = a->grid_f * a->grid_h * a->grid_w;
-  WA_CHECK_ARG(seq_len <= a->n, "wa_qkv_epilogue: grid of %lld tokens exceeds the %lld tokens given",
-               (long long)seq_len, (long long)a->n);
-  WA_CHECK_ARG(a->start_frame + a->grid_f <= a->f_rows && a->grid_h <= a->f_rows && a->grid_w <= a->f_rows,
-               "wa_qkv_epilogue: grid positions beyond the %lld rows of the RoPE table", (long long)a->f_rows);
+  // the grid of sample b (every sample's when sample_grids is NULL)
+  auto grid_of = [&](int64_t b, int64_t* g) {
+    const int64_t* src = a->sample_grids ? a->sample_grids + 3 * b : nullptr;
+    g[0] = src ? src[0] : a->grid_f;
+    g[1] = src ? src[1] : a->grid_h;
+    g[2] = src ? src[2] : a->grid_w;
+  };
+  for (int64_t b = 0; b < (a->sample_grids ? a->B : 1); ++b) {
+    int64_t g[3];
+    grid_of(b, g);
+    WA_CHECK_ARG(g[0] >= 0 && g[1] > 0 && g[2] > 0 && a->start_frame >= 0, "wa_qkv_epilogue: bad grid");
+    WA_CHECK_ARG(g[0] * g[1] * g[2] <= a->n, "wa_qkv_epilogue: grid of %lld tokens exceeds the %lld tokens given",
+                 (long long)(g[0] * g[1] * g[2]), (long long)a->n);
+    WA_CHECK_ARG(a->start_frame + g[0] <= a->f_rows && g[1] <= a->f_rows && g[2] <= a->f_rows,
+                 "wa_qkv_epilogue: grid positions beyond the %lld rows of the RoPE table", (long long)a->f_rows);
+  }
   WA_CHECK_ARG(((uintptr_t)a->freqs & 15u) == 0, "wa_qkv_epilogue: freqs must be 16-byte aligned");
   const bool norm = a->q_norm_w || a->k_norm_w;
   WA_CHECK_ARG(!norm || (a->q_norm_w && a->k_norm_w && (a->w_dtype == WA_BF16 || a->w_dtype == WA_F32)),
@@ -316,23 +325,50 @@ extern "C" int wa_qkv_epilogue(const wa_qkv_epilogue_args* a, void* stream) {
   p.B = (int)a->B; p.n = (int)a->n; p.H = (int)a->H; p.D = (int)a->D; p.HD = (int)HD;
   p.write_start = (int)a->write_start; p.src_offset = (int)a->src_offset; p.write_len = (int)a->write_len;
   p.freqs = a->freqs;
-  p.gf = (int)a->grid_f; p.gh = (int)a->grid_h; p.gw = (int)a->grid_w; p.start_frame = (int)a->start_frame;
-  p.seq_len = (int)seq_len;
+  p.start_frame = (int)a->start_frame;
   const int half = (int)(a->D / 2);
   p.ct = half - 2 * (half / 3); p.ch = half / 3;
   p.qw = a->q_norm_w; p.kw = a->k_norm_w; p.w_bf16 = a->w_dtype == WA_BF16; p.eps = a->eps;
   p.TT = TT;
   p.q_tiles = (int)((a->n + TT - 1) / TT);
   p.kv_tiles = (int)((a->write_len + TT - 1) / TT);
-  const int64_t jobs = a->B * (p.q_tiles + p.kv_tiles);
-  WA_CHECK_ARG(jobs < ((int64_t)1 << 31), "wa_qkv_epilogue: too many tokens for one launch");
+  WA_CHECK_ARG(a->B * (p.q_tiles + p.kv_tiles) < ((int64_t)1 << 31), "wa_qkv_epilogue: too many tokens for one launch");
   const size_t lds = norm ? (size_t)TT * HD * es + (size_t)TT * 9 * sizeof(float) : 16;
   hipStream_t s = (hipStream_t)stream;
-  if (a->dtype == WA_BF16)
-    hipLaunchKernelGGL(qkv_epilogue_kernel<bf16_t>, dim3((unsigned)jobs), dim3(256), lds, s, p);
-  else
-    hipLaunchKernelGGL(qkv_epilogue_kernel<float>, dim3((unsigned)jobs), dim3(256), lds, s, p);
-  int rc = wa_launch_status("qkv_epilogue");
+  // one launch per run of consecutive samples that share a grid (the whole batch without
+  // sample_grids): pointers moved to the run's first sample, B = its length
+  const int64_t el = es;
+  int rc = WA_OK;
+  for (int64_t b0 = 0; b0 < a->B && rc == WA_OK;) {
+    int64_t g[3], gn[3];
+    grid_of(b0, g);
+    int64_t b1 = b0 + 1;
+    if (a->sample_grids) {
+      for (; b1 < a->B; ++b1) {
+        grid_of(b1, gn);
+        if (gn[0] != g[0] || gn[1] != g[1] || gn[2] != g[2]) break;
+      }
+    } else {
+      b1 = a->B;
+    }
+    EpiParams pr = p;
+    pr.q = (const char*)a->q + b0 * a->q_sb * el;
+    pr.k = (const char*)a->k + b0 * a->k_sb * el;
+    pr.v = (const char*)a->v + b0 * a->v_sb * el;
+    pr.qo = (char*)a->q_out + b0 * a->qo_sb * el;
+    pr.ck = (char*)a->cache_k + b0 * a->ck_sb * el;
+    pr.cv = (char*)a->cache_v + b0 * a->cv_sb * el;
+    pr.B = (int)(b1 - b0);
+    pr.gf = (int)g[0]; pr.gh = (int)g[1]; pr.gw = (int)g[2];
+    pr.seq_len = (int)(g[0] * g[1] * g[2]);
+    const int64_t jobs = (b1 - b0) * (p.q_tiles + p.kv_tiles);
+    if (a->dtype == WA_BF16)
+      hipLaunchKernelGGL(qkv_epilogue_kernel<bf16_t>, dim3((unsigned)jobs), dim3(256), lds, s, pr);
+    else
+      hipLaunchKernelGGL(qkv_epilogue_kernel<float>, dim3((unsigned)jobs), dim3(256), lds, s, pr);
+    rc = wa_launch_status("qkv_epilogue");
+    b0 = b1;
+  }
   if (rc != WA_OK || !a->k_sums || a->write_len == 0) return rc;
   WA_CHECK_ARG(a->block_size > 0, "wa_qkv_epilogue: k_sums needs a block size");
   const int64_t L = a->write_start + a->write_len, first = a->write_start / a->block_size;

@@ -855,7 +855,7 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   rp.B = (int)a->B; rp.H = (int)a->H; rp.Nq = (int)a->Nq; rp.Nkv = (int)a->Nkv; rp.D = (int)a->D;
   rp.NP = (int)(next_pow2(a->Nkv) < 256 ? 256 : next_pow2(a->Nkv));
   rp.mode = a->mode; rp.tau_min = a->tau_min; rp.tau_span = a->tau_span;
-  rp.scale = (float)pow((double)a->D, -0.5);
+  rp.scale = a->scale > 0.f ? a->scale : (float)pow((double)a->D, -0.5);
   rp.head_k = a->head_k; rp.heads = a->heads; rp.n_heads = (int)nh;
   rp.index = a->index; rp.num = a->num; rp.thresholds = a->thresholds; rp.mask = a->mask;
   rp.probs_out = a->probs_out;

@@ -179,7 +179,9 @@ class _HSA(torch.autograd.Function):
         ctx.has_coarse = k_coarse is not None
         ctx.dtypes = tuple(t.dtype if t is not None else None
                            for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b))
-        if native_split_eligible(q, k, v, plan, routing, linear_mode, cfg["k_block_sums"], cfg["k_pooled"]):
+        scale = cfg.get("scale", 0.0)
+        if not scale and native_split_eligible(q, k, v, plan, routing, linear_mode, cfg["k_block_sums"],
+                                               cfg["k_pooled"]):
             # one library call (wa_hsa_fwd with its training outputs); the backward is wa_hsa_bwd
             out = torch.empty((bsz, q_len, heads, d), dtype=comp, device=dev)
             tr = {}
@@ -221,7 +223,7 @@ class _HSA(torch.autograd.Function):
                     kc, vc = k_coarse, v_coarse
                 kcb, vcb = _lib.kernel_ready(kc), _lib.kernel_ready(vc)
                 _, lse_l = bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
-                                       heads=lt, out=lin, lq=q_len, want_lse=True)
+                                       heads=lt, out=lin, lq=q_len, want_lse=True, scale=scale)
         if plan.sparse:
             _, _, nq, nkv = block_counts(q_len, kv_len, block_size)
             st = plan.t["sparse"]
@@ -232,15 +234,16 @@ class _HSA(torch.autograd.Function):
             arrivals = torch.empty((bsz * len(plan.sparse) * nq,), dtype=torch.int32, device=dev)
             if routing == "gini":
                 route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=cfg["tau_min"],
-                                  tau_max=cfg["tau_max"], heads=st, clear=arrivals, **key_args)
+                                  tau_max=cfg["tau_max"], heads=st, clear=arrivals, scale=scale, **key_args)
             else:
                 ks = _per_head_k(topk, heads)
                 route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=st, clear=arrivals,
-                                  **key_args)
+                                  scale=scale, **key_args)
                 visits = [min(ks[h], nkv) for h in plan.sparse]
             _, lse_s = bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size,
                                    layout="blhd", heads=st, out=out if split else sparse, lq=q_len, lkv=kv_len,
-                                   want_lse=True, visits=visits, attn_round_bf16=split, arrivals=arrivals)
+                                   want_lse=True, visits=visits, attn_round_bf16=split, arrivals=arrivals,
+                                   scale=scale)
         if split:
             if plan.linear:  # gate and gated output of the linear heads; the sparse heads are written
                 lin_modes = _lib.head_list([MODE_LINEAR if h in plan.linear else 0 for h in range(heads)], dev)
@@ -291,7 +294,7 @@ class _HSA(torch.autograd.Function):
         if plan.sparse:
             bsa_backward(qb, kb, vb, sparse, lse_s, dout, index=index, num=num, block_size=block_size,
                          layout="blhd", heads=plan.t["sparse"], lq=q_len, lkv=kv_len, dq=dq, dk=dk, dv=dv,
-                         accumulate=not fresh)
+                         accumulate=not fresh, scale=cfg.get("scale", 0.0))
         if plan.linear:
             lt = plan.t["linear"]
             if cfg["linear_mode"] == "elu1":
@@ -302,7 +305,8 @@ class _HSA(torch.autograd.Function):
                 dkc = torch.zeros((bsz, lc, heads, d), **f32)
                 dvc = torch.zeros((bsz, lc, heads, d), **f32)
                 bsa_backward(qb, kcb, vcb, lin, lse_l, dlin, index=None, num=None, block_size=block_size,
-                             layout="blhd", heads=lt, lq=q_len, lkv=lc, dq=dq, dk=dkc, dv=dvc, accumulate=True)
+                             layout="blhd", heads=lt, lq=q_len, lkv=lc, dq=dq, dk=dkc, dv=dvc, accumulate=True,
+                             scale=cfg.get("scale", 0.0))
                 if not ctx.has_coarse:
                     _, dEk = _compress_backward(dkc, k, k_proj_mat, cfg["proj_segment_len"], block_size, dx=dk)
                     _, dEv = _compress_backward(dvc, v, v_proj_mat, cfg["proj_segment_len"], block_size, dx=dv)
@@ -361,7 +365,7 @@ def _native_split_backward(ctx, dout):
 
 def hsa_attention_autograd(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
                            tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, k_block_sums=None,
-                           k_pooled=None):
+                           k_pooled=None, scale=0.0):
     """Differentiable :func:`hsa_attention` (q, k, v, coarse caches, projections and gate)."""
     if block_size not in (64, 128) or q.shape[-1] not in (64, 128):
         raise ValueError("block_size and head_dim must each be 64 or 128 for the gfx950 kernels")
@@ -369,5 +373,5 @@ def hsa_attention_autograd(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_ma
     gate_b = getattr(gate_lin, "bias", None) if gate_lin is not None else None
     cfg = dict(block_size=block_size, tau_min=tau_min, tau_max=tau_max, proj_segment_len=proj_segment_len,
                routing=routing, topk=topk, head_modes=head_modes, linear_mode=linear_mode,
-               k_block_sums=k_block_sums, k_pooled=k_pooled)
+               k_block_sums=k_block_sums, k_pooled=k_pooled, scale=scale)
     return _HSA.apply(q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_w, gate_b, cfg)

@@ -13,11 +13,12 @@ __all__ = ["bsa_backward"]
 
 
 def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_sizes=None, layout="bhld",
-                 heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None, accumulate=False):
+                 heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None, accumulate=False, scale=0.0):
     """``(dq, dk, dv)`` of :func:`bsa_forward` in ``layout`` (fp32; given ``dk`` / ``dv`` may be bf16).
 
     ``out`` is the forward's attention output (fp32 preferred, it sets ``delta``), ``lse`` its
-    natural-log log-sum-exp ``[B, H, Lq]``. Given ``dq`` / ``dk`` / ``dv`` buffers are written, or
+    natural-log log-sum-exp ``[B, H, Lq]``; ``scale`` the forward's logit scale (0: ``D ** -0.5``).
+    Given ``dq`` / ``dk`` / ``dv`` buffers are written, or
     added to with ``accumulate`` (fp32 only); only the heads in ``heads`` (device int32) are touched.
     """
     dev = _lib.require_gpu(q, k, v, out, grad_out)
@@ -53,7 +54,7 @@ def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_s
         *strides(grad_out), _lib.dtype_code(grad_out),
         lse.data_ptr(), _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
         *_lib.heads_arg(heads),
-        bsz, nheads, lq, lkv, d, block_size, 0.0,
+        bsz, nheads, lq, lkv, d, block_size, float(scale),
         *strides(dq), int(accumulate), *strides(dk), int(accumulate), *strides(dv), int(accumulate),
         ws.data_ptr(), _lib.dtype_code(dk))
     _lib.call("wa_bsa_bwd", args, _lib.stream_ptr(dev))

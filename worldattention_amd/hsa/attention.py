@@ -29,7 +29,7 @@ import torch.nn as nn
 
 from .. import _lib
 from . import distill
-from .block_sparse import bsa_forward, unit_table
+from .block_sparse import bsa_forward, padded_head_dim, unit_table
 from .routing import BlockRouting, _route, block_counts, pool_for_routing
 
 __all__ = [
@@ -47,6 +47,9 @@ _HEAD_MODES = ("both", "sparse", "linear")
 _LINEAR_MODES = ("lowrank", "elu1")
 _ROUTING_MODES = ("gini", "topk")
 SUPPORTED_BLOCK_SIZES = (64, 128)
+# Value of a key's padding channels: the queries' padding is zero, so q . k is unchanged, and the
+# elu(x)+1 feature of the padding, exp(-200), is 0 in fp32 (exactly representable in bf16).
+PAD_KEY_VALUE = -200.0
 
 
 def resolve_backend(backend: str) -> str:
@@ -77,15 +80,31 @@ def coarse_length(kv_len: int, segment_len: int, proj_rank: int, block_size: int
     return total
 
 
+def _pad_channels(t: Optional[torch.Tensor], d_to: int, value: float = 0.0) -> Optional[torch.Tensor]:
+    """``t`` with its last dim padded to ``d_to`` with ``value`` (differentiable)."""
+    if t is None or t.shape[-1] == d_to:
+        return t
+    return torch.nn.functional.pad(t, (0, d_to - t.shape[-1]), value=value)
+
+
 def _compress(x: torch.Tensor, proj: torch.Tensor, *, segment_len: int, block_size: int, layout: str,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``out`` (optional): a view of the destination rows (same layout, dtype of ``x``), e.g. slots
-    of a compressed cache, written in place."""
+    of a compressed cache, written in place. Head dims the kernel lacks run zero-padded (the
+    projection acts on each channel alone)."""
     dev = _lib.require_gpu(x, proj)
     if layout == "bhld":
         bsz, heads, length, d = x.shape
     else:
         bsz, length, heads, d = x.shape
+    if d not in (32, 64, 128):
+        dp = padded_head_dim(d, (32, 64, 128))
+        res = _compress(_pad_channels(x, dp), proj, segment_len=segment_len, block_size=block_size, layout=layout)
+        res = res[..., :d]
+        if out is None:
+            return res.contiguous()
+        out.copy_(res)
+        return out
     if segment_len <= 0:
         segment_len = length
     for start in range(0, length, segment_len):
@@ -130,11 +149,16 @@ def compress_kv(k: torch.Tensor, v: torch.Tensor, *, segment_len: int, k_proj_ma
 
 
 def _linear_branch(q: torch.Tensor, k_coarse: torch.Tensor, v_coarse: torch.Tensor) -> torch.Tensor:
-    """Softmax attention of ``[B, H, L, D]`` queries over compressed keys (``attention.py:113-118``)."""
-    block = 128 if q.shape[-1] == 128 else 64
-    out, _ = bsa_forward(_lib.kernel_ready(q), _lib.kernel_ready(k_coarse), _lib.kernel_ready(v_coarse),
-                         index=None, num=None, block_size=block, out_dtype=v_coarse.dtype)
-    return out
+    """Softmax attention of ``[B, H, L, D]`` queries over compressed keys (``attention.py:113-118``);
+    other head dims than 64 / 128 run zero-padded at the original scale."""
+    d = q.shape[-1]
+    dp = padded_head_dim(d)
+    block = 128 if dp == 128 else 64
+    qx, kx, vx = (_pad_channels(t, dp) for t in (q, k_coarse, v_coarse))
+    out, _ = bsa_forward(_lib.kernel_ready(qx), _lib.kernel_ready(kx), _lib.kernel_ready(vx),
+                         index=None, num=None, block_size=block, out_dtype=v_coarse.dtype,
+                         scale=d ** -0.5 if dp != d else 0.0)
+    return out[..., :d].contiguous() if dp != d else out
 
 
 # ----------------------------------------------------------------------------------------------
@@ -280,8 +304,10 @@ def _per_head_k(topk, heads: int):
 
 def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin, block_size, tau_min,
                 tau_max, proj_segment_len, routing, topk, head_modes, linear_mode, k_block_sums=None,
-                k_pooled=None, save=None):
-    """Forward of HSA on the GPU; ``save`` (a dict) receives what the backward needs."""
+                k_pooled=None, save=None, scale=0.0):
+    """Forward of HSA on the GPU; ``save`` (a dict) receives what the backward needs. ``scale``:
+    the logit scale of routing and of both softmax branches (0: ``head_dim ** -0.5``; a caller
+    that pads the head dim passes its original one's)."""
     bsz, q_len, heads, head_dim = q.shape
     kv_len = k.shape[1]
     dev = _lib.require_gpu(q, k, v, k_coarse, v_coarse)
@@ -306,7 +332,7 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     lin_round = comp_dtype == torch.bfloat16
 
     out = torch.empty((bsz, q_len, heads, head_dim), dtype=comp_dtype, device=dev)
-    if native_split_eligible(q, k, v, plan, routing, linear_mode, k_block_sums, k_pooled):
+    if not scale and native_split_eligible(q, k, v, plan, routing, linear_mode, k_block_sums, k_pooled):
         _native_split_forward(q, k, v, plan, _per_head_k(topk, heads), gate, lin_round, block_size, q_len, kv_len,
                               out, save)
         return out if out.dtype == out_dtype else out.to(out_dtype)
@@ -327,7 +353,7 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
     # ---- linear branch -------------------------------------------------------------------
     with torch.cuda.stream(side) if side is not None else contextlib.nullcontext():
         _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat,
-                          proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save)
+                          proj_segment_len, block_size, q_len, out, lin_tmp, gate, lin_round, save, scale)
 
     # ---- sparse branch: block pooling -----------------------------------------------------
     if plan.sparse:
@@ -344,11 +370,11 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
         arrivals = torch.empty((rows_only + rows_both,), dtype=torch.int32, device=dev)
         if routing == "gini":
             route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_GINI, tau_min=tau_min, tau_max=tau_max, heads=sp_t,
-                              clear=arrivals, **key_args)
+                              clear=arrivals, scale=scale, **key_args)
         else:
             ks = _per_head_k(topk, heads)
             route, _ = _route(None, qp, kp, mode=_lib.WA_ROUTE_TOPK, head_k=ks, heads=sp_t, clear=arrivals,
-                              **key_args)
+                              scale=scale, **key_args)
         if save is not None:
             save.update(route=route)
         # top-k routing fixes every row's visit count on the host: launch exactly those units
@@ -356,14 +382,14 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
         if plan.sparse_only:
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
                         heads=plan.t["sparse_only"], out=out, lq=q_len, lkv=kv_len, attn_round_bf16=True,
-                        visits=vis_of(plan.sparse_only), arrivals=arrivals[:rows_only])
+                        visits=vis_of(plan.sparse_only), arrivals=arrivals[:rows_only], scale=scale)
         if plan.both:
             if side is not None:
                 main.wait_stream(side)
             bsa_forward(qb, kb, vb, index=route.index, num=route.num, block_size=block_size, layout="blhd",
                         heads=plan.t["both"], out=out, lq=q_len, lkv=kv_len, epilogue=_lib.WA_EPI_FUSE,
                         x=lin_tmp, attn_round_bf16=True, visits=vis_of(plan.both), arrivals=arrivals[rows_only:],
-                        **gate.kwargs())
+                        scale=scale, **gate.kwargs())
     if side is not None:
         main.wait_stream(side)
     return out if out.dtype == out_dtype else out.to(out_dtype)
@@ -456,7 +482,7 @@ def _native_split_forward(q, k, v, plan, ks, gate, lin_round, block_size, q_len,
 
 
 def _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj_mat, v_proj_mat, proj_segment_len,
-                      block_size, q_len, out, lin_tmp, gate, lin_round, save):
+                      block_size, q_len, out, lin_tmp, gate, lin_round, save, scale=0.0):
     """Linear-branch heads of :func:`hsa_forward`: linear-only heads straight into ``out`` with the
     gate applied, heads that also run the sparse branch into ``lin_tmp``."""
     if plan.linear:
@@ -471,11 +497,11 @@ def _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj
                 save.update(kc=kc, vc=vc)
             if plan.both:
                 bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
-                            heads=plan.t["both"], out=lin_tmp, lq=q_len)
+                            heads=plan.t["both"], out=lin_tmp, lq=q_len, scale=scale)
             if plan.linear_only:
                 bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
                             heads=plan.t["linear_only"], out=out, lq=q_len, epilogue=_lib.WA_EPI_GATED,
-                            attn_round_bf16=lin_round, **gate.kwargs())
+                            attn_round_bf16=lin_round, scale=scale, **gate.kwargs())
         else:
             if plan.both:
                 s_b, z_b = elu1_state(k, v, plan.t["both"])
@@ -518,6 +544,12 @@ def hsa_attention(
     ``k.shape[1]`` tokens are ``k``; ``k_pooled``: fp32 block means of exactly ``k`` (the routing
     pool of ``routing.py:45-61``). With either, routing pools only the queries; the result is
     identical to pooling ``k``.
+
+    Head dims other than 64 and 128 (the reference's functional API takes any) run padded to the
+    next of them: queries, values, coarse caches and the gate layer with zeros, keys with
+    ``PAD_KEY_VALUE``, routing and both softmax branches at the original ``head_dim ** -0.5``; the
+    padding changes no logit, no elu(x)+1 feature and no gate of a real channel, and the output is
+    cut back to ``head_dim`` (gradients flow through the padding to the unpadded tensors).
     """
     if (k_coarse is None) != (v_coarse is None):
         raise ValueError("k_coarse and v_coarse must be provided together")
@@ -534,21 +566,42 @@ def hsa_attention(
         if v_coarse.shape != k_coarse.shape:
             raise ValueError("v_coarse must have the same shape as k_coarse")
     resolve_backend(backend)
-    cfg = dict(k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=k_proj_mat, v_proj_mat=v_proj_mat,
-               gate_lin=gate_lin, block_size=block_size, tau_min=tau_min, tau_max=tau_max,
-               proj_segment_len=proj_segment_len, routing=routing, topk=topk, head_modes=head_modes,
-               linear_mode=linear_mode, k_block_sums=k_block_sums, k_pooled=k_pooled)
     needs_grad = torch.is_grad_enabled() and (
         any(t is not None and t.requires_grad for t in (q, k, v, k_coarse, v_coarse, k_proj_mat, v_proj_mat))
         or (gate_lin is not None and any(p.requires_grad for p in gate_lin.parameters())))
+    dp = padded_head_dim(head_dim)
+    qx, kx, vx, scale = q, k, v, 0.0
+    if dp != head_dim:
+        scale = head_dim ** -0.5
+        qx, kx, vx = _pad_channels(q, dp), _pad_channels(k, dp, PAD_KEY_VALUE), _pad_channels(v, dp)
+        k_coarse, v_coarse = _pad_channels(k_coarse, dp), _pad_channels(v_coarse, dp)
+        k_block_sums, k_pooled = _pad_channels(k_block_sums, dp), _pad_channels(k_pooled, dp)
+        gate_lin = _PaddedGate(gate_lin, dp) if gate_lin is not None else None
+    cfg = dict(k_coarse=k_coarse, v_coarse=v_coarse, k_proj_mat=k_proj_mat, v_proj_mat=v_proj_mat,
+               gate_lin=gate_lin, block_size=block_size, tau_min=tau_min, tau_max=tau_max,
+               proj_segment_len=proj_segment_len, routing=routing, topk=topk, head_modes=head_modes,
+               linear_mode=linear_mode, k_block_sums=k_block_sums, k_pooled=k_pooled, scale=scale)
     if needs_grad:
         from ._autograd import hsa_attention_autograd
-        output = hsa_attention_autograd(q, k, v, **cfg)
+        output = hsa_attention_autograd(qx, kx, vx, **cfg)
     else:
-        output = hsa_forward(q, k, v, **cfg)
+        output = hsa_forward(qx, kx, vx, **cfg)
+    if dp != head_dim:
+        output = output[..., :head_dim].contiguous()
     if distill.distill_enabled() and torch.is_grad_enabled():
         distill.record_against_dense(output, q, k, v)
     return output
+
+
+class _PaddedGate:
+    """A gate layer's weight ``[D, D]`` and bias ``[D]`` zero-padded to ``dp`` channels (padding
+    channels get sigmoid(0) and gate nothing: their linear-branch output is zero)."""
+
+    def __init__(self, gate_lin: nn.Module, dp: int):
+        w = gate_lin.weight
+        self.weight = torch.nn.functional.pad(w, (0, dp - w.shape[1], 0, dp - w.shape[0]))
+        b = getattr(gate_lin, "bias", None)
+        self.bias = _pad_channels(b, dp) if b is not None else None
 
 
 class HSAAttention(nn.Module):

@@ -63,7 +63,7 @@ def unit_table(bsz: int, visits_per_slot, nq: int, split: int, device) -> tuple[
 def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=None, heads=None,
                 out=None, out_dtype=None, want_lse=False, epilogue=_lib.WA_EPI_PLAIN, x=None, gate_w=None,
                 gate_b=None, gate_pre_bf16=False, gate_out_bf16=False, attn_round_bf16=False, lq=None,
-                lkv=None, visits=None, split=None, arrivals=None, noalloc=False):
+                lkv=None, visits=None, split=None, arrivals=None, noalloc=False, scale=0.0):
     """Launch ``wa_bsa_fwd`` on bf16 q/k/v in ``layout`` ("bhld" = [B, H, L, D], "blhd" = [B, L, H, D]).
 
     ``index=None`` attends densely to every key block. ``visits`` (optional) gives each launched
@@ -71,8 +71,9 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
     then covers exactly the needed (row, split) units. ``arrivals`` (optional): an int32 tensor of
     at least ``B * n_heads * ceil(lq / block_size)`` zeros (left zero), which spares the launch
     clearing its own. ``noalloc``: launch ``wa_bsa_fwd_noalloc`` instead, whose workspace is the
-    library's static device array (no workspace tensor; ``arrivals`` must be None). An empty
-    ``heads`` list launches nothing. Returns ``(out, lse)``.
+    library's static device array (no workspace tensor; ``arrivals`` must be None). ``scale``:
+    the logit scale (0: ``D ** -0.5``). An empty ``heads`` list launches nothing. Returns
+    ``(out, lse)``.
     """
     dev = _lib.require_gpu(q, k, v)
     strides = _lib.bhld if layout == "bhld" else _lib.blhd
@@ -127,12 +128,37 @@ def bsa_forward(q, k, v, *, index, num, block_size, layout="bhld", block_sizes=N
         op, o_sb, o_st, o_sh, _lib.dtype_code(out), _lib.ptr(lse),
         _lib.ptr(index), _lib.ptr(num), width, _lib.ptr(block_sizes),
         *_lib.heads_arg(heads),
-        bsz, nheads, lq, lkv, d, block_size, 0.0, epilogue,
+        bsz, nheads, lq, lkv, d, block_size, float(scale), epilogue,
         xp, x_sb, x_st, x_sh, x_dt, _lib.ptr(gate_w), _lib.ptr(gate_b),
         int(gate_pre_bf16), int(gate_out_bf16), int(attn_round_bf16),
         _lib.ptr(ws), _lib.ptr(units), n_units, max_visits, split, _lib.ptr(arrivals))
     _lib.call("wa_bsa_fwd_noalloc" if noalloc else "wa_bsa_fwd", args, _lib.stream_ptr(dev))
     return out, lse
+
+
+# Head dims the kernels take; any other head dim up to 128 runs zero-padded to the next one at
+# its own scale (zero channels add nothing to q . k, and the output's padding is cut off).
+KERNEL_HEAD_DIMS = (64, 128)
+
+
+def padded_head_dim(d: int, dims=KERNEL_HEAD_DIMS) -> int:
+    """The kernel head dim a head dim of ``d`` runs at: the smallest of ``dims`` not below it."""
+    for kd in dims:
+        if d <= kd:
+            return kd
+    raise ValueError(f"head_dim must be at most {dims[-1]} for the gfx950 kernels, got {d}")
+
+
+def _pad_qkv(q, k, v):
+    """``(q, k, v, d, scale)`` with the head dim zero-padded to a kernel head dim (differentiable);
+    ``scale`` is 0 (the kernel default) when no padding was needed."""
+    d = q.shape[-1]
+    dp = padded_head_dim(d)
+    if dp == d:
+        return q, k, v, d, 0.0
+    pad = (0, dp - d)
+    return (torch.nn.functional.pad(q, pad), torch.nn.functional.pad(k, pad), torch.nn.functional.pad(v, pad), d,
+            d ** -0.5)
 
 
 def _check_padded(q, k, index, num, block_size):
@@ -153,13 +179,14 @@ class _BlockSparseAttention(torch.autograd.Function):
     """Differentiable block-sparse attention (reference ``block_sparse_triton.py:353-368``)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, index, num, block_sizes, block_size):
+    def forward(ctx, q, k, v, index, num, block_sizes, block_size, scale=0.0):
         qb, kb, vb = _prep(q), _prep(k), _prep(v)
         # fp32 output: the backward's delta = rowsum(o * do) uses it unrounded
         out, lse = bsa_forward(qb, kb, vb, index=index, num=num, block_size=block_size,
-                               block_sizes=block_sizes, out_dtype=torch.float32, want_lse=True)
+                               block_sizes=block_sizes, out_dtype=torch.float32, want_lse=True, scale=scale)
         ctx.save_for_backward(qb, kb, vb, out, lse, index, num, block_sizes)
         ctx.block_size = block_size
+        ctx.scale = scale
         ctx.dtypes = (q.dtype, k.dtype, v.dtype)
         return out.to(q.dtype)
 
@@ -167,18 +194,18 @@ class _BlockSparseAttention(torch.autograd.Function):
     def backward(ctx, grad_out):
         qb, kb, vb, out, lse, index, num, block_sizes = ctx.saved_tensors
         dq, dk, dv = bsa_backward(qb, kb, vb, out, lse, grad_out, index=index, num=num,
-                                  block_size=ctx.block_size, block_sizes=block_sizes)
+                                  block_size=ctx.block_size, block_sizes=block_sizes, scale=ctx.scale)
         qd, kd, vd = ctx.dtypes
-        return dq.to(qd), dk.to(kd), dv.to(vd), None, None, None, None
+        return dq.to(qd), dk.to(kd), dv.to(vd), None, None, None, None, None
 
 
 def bsa_backward(q, k, v, out, lse, grad_out, *, index, num, block_size, block_sizes=None, layout="bhld",
-                 heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None):
+                 heads=None, lq=None, lkv=None, dq=None, dk=None, dv=None, scale=0.0):
     """Gradients of :func:`bsa_forward` (``wa_bsa_bwd``)."""
     from . import _bwd
     return _bwd.bsa_backward(q, k, v, out, lse, grad_out, index=index, num=num, block_size=block_size,
                              block_sizes=block_sizes, layout=layout, heads=heads, lq=lq, lkv=lkv,
-                             dq=dq, dk=dk, dv=dv)
+                             dq=dq, dk=dk, dv=dv, scale=scale)
 
 
 def block_sparse_attention(q, k, v, *, block_sizes, q2k_index=None, q2k_num=None, block_map=None):
@@ -192,8 +219,10 @@ def block_sparse_attention(q, k, v, *, block_sizes, q2k_index=None, q2k_num=None
     if block_map is not None:
         index, num = map_to_index(block_map)
         _check_padded(q, k, index, num, block_size)
-        return _BlockSparseAttention.apply(q, k, v, index, num, block_sizes.to(torch.int32).contiguous(),
-                                           block_size)
+        qx, kx, vx, d, scale = _pad_qkv(q, k, v)
+        out = _BlockSparseAttention.apply(qx, kx, vx, index, num, block_sizes.to(torch.int32).contiguous(),
+                                          block_size, scale)
+        return out[..., :d].contiguous() if scale else out
     if q2k_index is None or q2k_num is None:
         raise ValueError("provide either block_map or both q2k_index and q2k_num")
     return block_sparse_attention_reference(q, k, v, q2k_index, q2k_num, block_sizes, block_size)
@@ -211,9 +240,12 @@ def block_sparse_attention_reference(q, k, v, q2k_index, q2k_num, block_sizes, b
     num = q2k_num.to(torch.int32).contiguous()
     _check_padded(q, k, index, num, block_size)
     sizes = block_sizes.to(device=q.device, dtype=torch.int32).contiguous()
+    qx, kx, vx, d, scale = _pad_qkv(q, k, v)
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
-        return _BlockSparseAttention.apply(q, k, v, index, num, sizes, block_size)
-    out_dtype = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
-    out, _ = bsa_forward(_prep(q), _prep(k), _prep(v), index=index, num=num, block_size=block_size,
-                         block_sizes=sizes, out_dtype=out_dtype)
-    return out.to(q.dtype)
+        out = _BlockSparseAttention.apply(qx, kx, vx, index, num, sizes, block_size, scale)
+    else:
+        out_dtype = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
+        out, _ = bsa_forward(_prep(qx), _prep(kx), _prep(vx), index=index, num=num, block_size=block_size,
+                             block_sizes=sizes, out_dtype=out_dtype, scale=scale)
+        out = out.to(q.dtype)
+    return out[..., :d].contiguous() if scale else out

@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _lib
-from .block_sparse import bsa_forward
+from .block_sparse import bsa_forward, padded_head_dim
 
 __all__ = ["enable_distill", "distill_enabled", "pop_distill_losses", "record_distill_loss",
            "dense_attention", "record_against_dense"]
@@ -64,16 +64,18 @@ def record_distill_loss(loss: torch.Tensor) -> None:
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Softmax attention of ``[B, Lq, H, D]`` queries over all ``[B, Lkv, H, D]`` keys, scale
     ``D ** -0.5``, no mask: the target HSA is distilled towards. Runs the dense flash kernel on
-    bf16 copies of the operands (head dim 64 or 128); the result has ``q``'s dtype."""
+    bf16 copies of the operands (head dims other than 64 and 128 zero-padded to the next one, with
+    the original scale); the result has ``q``'s dtype."""
     d = q.shape[-1]
-    if d not in (64, 128):
-        raise ValueError(f"the dense teacher kernel needs head dim 64 or 128, got {d}")
+    dp = padded_head_dim(d)
     if k.shape != v.shape or k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]:
         raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)} and v {tuple(v.shape)} do not match")
-    block = 128 if d == 128 else 64
-    qb, kb, vb = (_lib.kernel_ready(t.detach()) for t in (q, k, v))
+    block = 128 if dp == 128 else 64
+    qb, kb, vb = (_lib.kernel_ready(F.pad(t.detach(), (0, dp - d)) if dp != d else t.detach()) for t in (q, k, v))
     out, _ = bsa_forward(qb, kb, vb, index=None, num=None, block_size=block, layout="blhd",
-                         out_dtype=q.dtype if q.dtype in (torch.float32, torch.bfloat16) else torch.float32)
+                         out_dtype=q.dtype if q.dtype in (torch.float32, torch.bfloat16) else torch.float32,
+                         scale=d ** -0.5 if dp != d else 0.0)
+    out = out[..., :d].contiguous() if dp != d else out
     return out if out.dtype == q.dtype else out.to(q.dtype)
 
 

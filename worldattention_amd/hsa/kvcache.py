@@ -19,6 +19,7 @@ what attention sees, so the writes here go to the cache itself.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Sequence
 
@@ -135,17 +136,18 @@ def kv_append(kv_cache: dict, k_new: torch.Tensor, v_new: torch.Tensor, *, write
     }
 
 
-def _grid3(grid_sizes):
-    """``(f, h, w)`` from a ``[B, 3]`` tensor / nested list / triple; every sample must share it."""
+def _grid_rows(grid_sizes, batch: int):
+    """Per-sample ``(f, h, w)`` rows from a ``[B, 3]`` tensor / nested list (one per sample, as the
+    reference's ``grid_sizes``) or one triple for the whole batch."""
     if isinstance(grid_sizes, torch.Tensor):
         rows = grid_sizes.reshape(-1, 3).tolist()
     elif len(grid_sizes) and isinstance(grid_sizes[0], (list, tuple)):
         rows = [list(r) for r in grid_sizes]
     else:
-        rows = [list(grid_sizes)]
-    if any(r != rows[0] for r in rows):
-        raise ValueError(f"the fused epilogue needs one grid for the whole batch, got {rows}")
-    return tuple(int(x) for x in rows[0])
+        return [tuple(int(x) for x in grid_sizes)] * batch
+    if len(rows) != batch:
+        raise ValueError(f"grid_sizes holds {len(rows)} grids for a batch of {batch}")
+    return [tuple(int(x) for x in r) for r in rows]
 
 
 def _table(freqs: torch.Tensor, dev) -> torch.Tensor:
@@ -180,7 +182,10 @@ def qkv_epilogue(q, k, v, kv_cache: dict, *, grid_sizes, freqs, start_frame: int
     ready = [_lib.kernel_ready(t, dtype) for t in (q, k, v)]
     q_out = torch.empty((bsz, n, heads, d), dtype=dtype, device=dev)
     table = _table(freqs, dev)
-    f, gh, gw = _grid3(grid_sizes)
+    rows = _grid_rows(grid_sizes, bsz)
+    f, gh, gw = rows[0]
+    # samples with grids of their own (the reference loops over grid_sizes per sample)
+    per_sample = (ctypes.c_int64 * (3 * bsz))(*[x for r in rows for x in r]) if len(set(rows)) > 1 else None
     wlen = n - src_offset if write_len is None else int(write_len)
     sums = None
     if block_size is not None:
@@ -203,7 +208,7 @@ def qkv_epilogue(q, k, v, kv_cache: dict, *, grid_sizes, freqs, start_frame: int
     args = _lib.QkvEpilogueArgs(*qq, *kk, *vv, _lib.dtype_code(kc), bsz, n, heads, d, *qo, *ck, *cv,
                                 kc.shape[1], int(write_start), int(src_offset), wlen, table.data_ptr(),
                                 table.shape[0], f, gh, gw, int(start_frame), _lib.ptr(wq), _lib.ptr(wk), w_dtype,
-                                float(eps), _lib.ptr(sums), int(block_size or 0))
+                                float(eps), _lib.ptr(sums), int(block_size or 0), per_sample)
     _lib.call("wa_qkv_epilogue", args, _lib.stream_ptr(dev))
     return q_out
 
@@ -265,8 +270,8 @@ def cache_step(kv_cache: dict, q, k, v, *, grid_sizes, freqs, current_start: int
     ``"k_block_sums"`` is the tensor to pass to ``hsa_attention`` (None unless the window is the
     cache's first tokens and sums are kept).
     """
-    f, gh, gw = _grid3(grid_sizes)
-    frame_seqlen = gh * gw
+    rows = _grid_rows(grid_sizes, q.shape[0])
+    frame_seqlen = rows[0][1] * rows[0][2]  # sample 0's frame, as causal_model.py:269 takes it
     start_frame = current_start // frame_seqlen
     n = q.shape[1]
     current_end = current_start + n
@@ -295,7 +300,7 @@ def cache_step(kv_cache: dict, q, k, v, *, grid_sizes, freqs, current_start: int
     if roll:
         kv_roll(kv_cache, sink_tokens=sink, num_evicted=evicted, num_rolled=rolled, block_size=block_size,
                 hsa_module=hsa_module if coarse else None)
-    roped_q = qkv_epilogue(q, k, v, kv_cache, grid_sizes=(f, gh, gw), freqs=freqs, start_frame=start_frame,
+    roped_q = qkv_epilogue(q, k, v, kv_cache, grid_sizes=rows, freqs=freqs, start_frame=start_frame,
                            write_start=write_start, src_offset=offset, write_len=write_len, norm_q=norm_q,
                            norm_k=norm_k, eps=eps, block_size=block_size)
     kc, vc = kv_cache["k"], kv_cache["v"]

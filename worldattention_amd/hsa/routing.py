@@ -169,10 +169,11 @@ def pool_for_routing(q, k, q_len: int, kv_len: int, block_size: int, heads=None,
 
 def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=None,
            return_mask=False, want_probs=False, clear=None, nkv=None, k_pooled_blocks=0, k_sum_len=0,
-           block_size=0, k_sum_bf16=False):
+           block_size=0, k_sum_bf16=False, scale=0.0):
     """``clear`` (optional): a contiguous int32 device tensor the launch zeroes (the arrivals of
     the block-sparse launch that follows). ``nkv`` / ``k_pooled_blocks`` / ``k_sum_len`` /
-    ``block_size`` / ``k_sum_bf16``: cached key blocks (:func:`pool_for_routing`)."""
+    ``block_size`` / ``k_sum_bf16``: cached key blocks (:func:`pool_for_routing`). ``scale``: the
+    map's logit scale (0: the pooled vectors' ``D ** -0.5``)."""
     src = probs if probs is not None else qp
     dev = _lib.require_gpu(src, kp)
     if probs is not None:
@@ -204,7 +205,7 @@ def _route(probs, qp, kp, *, mode, tau_min=0.0, tau_max=1.0, head_k=None, heads=
                           index.data_ptr(), num.data_ptr(),
                           thresholds.data_ptr(), _lib.ptr(mask), _lib.ptr(probs_out), _lib.ptr(ws),
                           _lib.ptr(clear), 0 if clear is None else clear.numel(), int(k_sum_len),
-                          int(block_size), int(bool(k_sum_bf16)), int(k_pooled_blocks))
+                          int(block_size), int(bool(k_sum_bf16)), int(k_pooled_blocks), float(scale))
     _lib.call("wa_route", args, _lib.stream_ptr(dev))
     return BlockRouting(index=index, num=num, mask=mask, thresholds=thresholds), probs_out
 
