@@ -58,6 +58,9 @@ def parse():
                     help="comma list of the extra configs to run (cfg2, the headline, always runs; ref: the "
                          "reference's default HSA configuration on the cfg2 chunk)")
     ap.add_argument("--hkv-layers", type=int, default=4)
+    ap.add_argument("--kernel-source-fingerprint", action="store_true",
+                    help="only print the fingerprint of the sparse kernel's sources (what a counter summary "
+                         "under profiles/ records)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (the reference kernel that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters of the traffic measurement)")
@@ -75,17 +78,40 @@ def copy_calibration(dev) -> None:
                       "launches": 5}), flush=True)
 
 
+# The sources the sparse forward kernel is built from: a counter summary under profiles/ records
+# their fingerprint, and its figures are used only while the sources still match it.
+SPARSE_KERNEL_SOURCES = ("worldattention_amd/csrc/bsa_fwd.hip", "worldattention_amd/csrc/tile.h",
+                         "worldattention_amd/csrc/common.h")
+
+
+def kernel_source_fingerprint(files=SPARSE_KERNEL_SOURCES) -> str:
+    """First 16 hex digits of the SHA-256 of the given source files' bytes, in order."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in files:
+        with open(os.path.join(ROOT, f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
     """HBM bytes per launch of the sparse kernel from the committed counter summary (FETCH_SIZE and
-    WRITE_SIZE runs scaled by a plain-copy calibration), or None when it is absent."""
+    WRITE_SIZE runs scaled by a plain-copy calibration), or None when it is absent or was measured
+    on other kernel sources than the ones here (its ``kernel_source_fingerprint`` line differs)."""
     path = os.path.join(ROOT, "profiles", "bsa_fwd_cfg2_traffic.md")
+    traffic = fingerprint = None
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+                traffic = int(line.split(":", 1)[1])
+            elif line.startswith("kernel_source_fingerprint:"):
+                fingerprint = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None
+    if fingerprint != kernel_source_fingerprint():
+        log("profiles/bsa_fwd_cfg2_traffic.md was measured on other sparse-kernel sources: traffic = null")
+        return None
+    return traffic
 
 
 def log(msg: str) -> None:
@@ -784,6 +810,9 @@ def cpu_baseline(args, cfg, proj, useful_flop):
 
 def main():
     args = parse()
+    if args.kernel_source_fingerprint:
+        print(kernel_source_fingerprint())
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (the path shards by "
                                    "head across GPUs by design, but no multi-GPU run is part of it)"}))
