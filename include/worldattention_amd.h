@@ -356,6 +356,10 @@ typedef struct wa_hsa_bwd_args {
   float* dgate_w; float* dgate_b;
   void* workspace;
   void* side_stream; void* fork_event; void* join_event;
+  /* dq_stream / dq_fork_event / dq_join_event (optional, caller-owned, another stream than the two
+   * above): the sparse heads' dQ pass runs there, forked after their preprocess, concurrently with
+   * their dK/dV pass (and the linear heads), and joined back before the call returns. */
+  void* dq_stream; void* dq_fork_event; void* dq_join_event;
 } wa_hsa_bwd_args;
 int64_t wa_hsa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t Lq, int64_t Lkv, int64_t D, int64_t block_size,
                                    int64_t n_sparse, int64_t n_linear);

@@ -211,6 +211,7 @@ HsaBwdArgs = _struct("wa_hsa_bwd_args", [
     ("dgate_w", c_void_p), ("dgate_b", c_void_p),
     ("workspace", c_void_p),
     ("side_stream", c_void_p), ("fork_event", c_void_p), ("join_event", c_void_p),
+    ("dq_stream", c_void_p), ("dq_fork_event", c_void_p), ("dq_join_event", c_void_p),
 ])
 
 BsaBwdArgs = _struct("wa_bsa_bwd_args", [

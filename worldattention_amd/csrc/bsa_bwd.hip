@@ -802,8 +802,12 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
   }
 }
 
+// The launches of one backward on stream s; with a second stream sq (and its fork / join events)
+// the dQ pass runs on sq once the preprocess is done (it reads delta, lse2 and the bf16 dO copy, not
+// the transposed lists), concurrently with the transposed lists and the dK/dV pass on s, and s
+// waits for it at the end (also on an error path once forked, so a capture ends joined).
 template <int D, int BS>
-int launch_bwd(const BwdParams& bp, hipStream_t s) {
+int launch_bwd(const BwdParams& bp, hipStream_t s, hipStream_t sq, hipEvent_t fork, hipEvent_t join) {
   const int nh = bp.n_heads;
   const dim3 pre_grid((unsigned)((bp.Lq + (256 / (D / 8)) - 1) / (256 / (D / 8))), nh, bp.B);
   // 8-element row vectors: a 16-byte aligned base and strides in multiples of 8 elements
@@ -824,13 +828,31 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     hipLaunchKernelGGL((bwd_pre_kernel<D>), pre_grid, dim3(256), 0, s, bp);
   int rc = wa_launch_status("bsa_bwd_pre");
   if (rc) return rc;
+  const bool split = bp.dq && sq && sq != s;
+  if (split) {
+    hipError_t e;
+    if ((e = hipEventRecord(fork, s)) != hipSuccess || (e = hipStreamWaitEvent(sq, fork, 0)) != hipSuccess)
+      return wa_fail((int)e, "wa_bsa_bwd: fork: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3((unsigned)(bp.Nq * nh * bp.B)), dim3(2 * BS), 0, sq, bp);
+    rc = wa_launch_status("bsa_bwd_dq");
+    if ((e = hipEventRecord(join, sq)) != hipSuccess) return rc ? rc : wa_fail((int)e, "wa_bsa_bwd: join: %s", hipGetErrorString(e));
+    if (rc) {
+      hipStreamWaitEvent(s, join, 0);
+      return rc;
+    }
+  }
+  auto joined = [&](int code) {
+    if (!split) return code;
+    const hipError_t e = hipStreamWaitEvent(s, join, 0);
+    return code != WA_OK ? code : e != hipSuccess ? wa_fail((int)e, "wa_bsa_bwd: join: %s", hipGetErrorString(e)) : WA_OK;
+  };
   if (bp.index && bp.Nq <= K2Q_COUNT_NQ)
     hipLaunchKernelGGL(k2q_count_kernel, dim3((bp.Nkv + K2Q_COUNT_KB - 1) / K2Q_COUNT_KB, nh, bp.B), dim3(256), 0, s,
                        bp);
   else
     hipLaunchKernelGGL(k2q_kernel, dim3((bp.Nkv + 255) / 256, nh, bp.B), dim3(256), 0, s, bp);
-  if ((rc = wa_launch_status("bsa_bwd_k2q"))) return rc;
-  if (bp.dq) {
+  if ((rc = wa_launch_status("bsa_bwd_k2q"))) return joined(rc);
+  if (bp.dq && !split) {
     hipLaunchKernelGGL((bwd_dq_kernel<D, BS>), dim3((unsigned)(bp.Nq * nh * bp.B)), dim3(2 * BS), 0, s, bp);
     if ((rc = wa_launch_status("bsa_bwd_dq"))) return rc;
   }
@@ -838,14 +860,14 @@ int launch_bwd(const BwdParams& bp, hipStream_t s) {
     BwdParams kp = bp;
     if (bp.Nq < KV_ORDER_T) {
       hipLaunchKernelGGL(kv_order_kernel, dim3((unsigned)(bp.B * nh)), dim3(KV_ORDER_T), 0, s, bp);
-      if ((rc = wa_launch_status("bsa_bwd_kv_order"))) return rc;
+      if ((rc = wa_launch_status("bsa_bwd_kv_order"))) return joined(rc);
     } else {
       kp.kv_info = nullptr;
     }
     hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(4 * BS), 0, s, kp);
-    if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return rc;
+    if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return joined(rc);
   }
-  return WA_OK;
+  return joined(WA_OK);
 }
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -859,8 +881,17 @@ extern "C" int64_t wa_bsa_bwd_workspace_bytes(int64_t B, int64_t n_heads, int64_
          align256(B * n_heads * nkv * nq * 4) + align256(B * n_heads * nkv * 4) + align256(B * n_heads * nkv * 16);
 }
 
+// wa_bsa_bwd with its dQ pass on a second stream (NULL: one stream), forked from `stream` after the
+// preprocess with fork_event and joined back with join_event; the one-call backward (hsa.hip) uses it.
+int wa_bsa_bwd_streams(const wa_bsa_bwd_args* a, void* stream, void* dq_stream, void* fork_event, void* join_event);
+
 extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
+  return wa_bsa_bwd_streams(a, stream, nullptr, nullptr, nullptr);
+}
+
+int wa_bsa_bwd_streams(const wa_bsa_bwd_args* a, void* stream, void* dq_stream, void* fork_event, void* join_event) {
   WA_CHECK_ARG(a != nullptr, "wa_bsa_bwd: null args");
+  WA_CHECK_ARG(dq_stream == nullptr || (fork_event && join_event), "wa_bsa_bwd: a dQ stream needs fork and join events");
   WA_CHECK_ARG(a->D == 64 || a->D == 128, "wa_bsa_bwd: head dim %lld not in {64, 128}", (long long)a->D);
   WA_CHECK_ARG(a->block_size == 64 || a->block_size == 128, "wa_bsa_bwd: block size %lld not in {64, 128}",
                (long long)a->block_size);
@@ -928,9 +959,10 @@ extern "C" int wa_bsa_bwd(const wa_bsa_bwd_args* a, void* stream) {
   ws += align256(a->B * nh * nkv * 4);
   bp.kv_info = (int4*)ws;
 
-  hipStream_t s = (hipStream_t)stream;
-  if (a->D == 64 && a->block_size == 64) return launch_bwd<64, 64>(bp, s);
-  if (a->D == 64 && a->block_size == 128) return launch_bwd<64, 128>(bp, s);
-  if (a->D == 128 && a->block_size == 64) return launch_bwd<128, 64>(bp, s);
-  return launch_bwd<128, 128>(bp, s);
+  hipStream_t s = (hipStream_t)stream, sq = (hipStream_t)dq_stream;
+  hipEvent_t fe = (hipEvent_t)fork_event, je = (hipEvent_t)join_event;
+  if (a->D == 64 && a->block_size == 64) return launch_bwd<64, 64>(bp, s, sq, fe, je);
+  if (a->D == 64 && a->block_size == 128) return launch_bwd<64, 128>(bp, s, sq, fe, je);
+  if (a->D == 128 && a->block_size == 64) return launch_bwd<128, 64>(bp, s, sq, fe, je);
+  return launch_bwd<128, 128>(bp, s, sq, fe, je);
 }

@@ -200,6 +200,9 @@ int hsa_branches(const wa_hsa_fwd_args* a, const HsaLayout& l, char* ws, void* s
 // ---------------------------------------------------------------------------------------------
 // Backward
 // ---------------------------------------------------------------------------------------------
+// wa_bsa_bwd with its dQ pass on a second stream (bsa_bwd.hip)
+int wa_bsa_bwd_streams(const wa_bsa_bwd_args* a, void* stream, void* dq_stream, void* fork_event, void* join_event);
+
 namespace {
 
 struct HsaBwdLayout {
@@ -242,6 +245,7 @@ __global__ void __launch_bounds__(256) round_heads_kernel(const float* __restric
 }
 
 int hsa_bwd_sparse(const wa_hsa_bwd_args* a, const HsaBwdLayout& l, char* ws, void* stream) {
+  const bool dq_side = a->dq_stream && a->dq_stream != stream;
   const int64_t bs = a->block_size;
   wa_bsa_bwd_args g{};
   g.q = a->q; g.q_sb = a->q_sb; g.q_st = a->q_st; g.q_sh = a->q_sh;
@@ -256,7 +260,7 @@ int hsa_bwd_sparse(const wa_hsa_bwd_args* a, const HsaBwdLayout& l, char* ws, vo
   g.dk = a->dk; g.dk_sb = a->dk_sb; g.dk_st = a->dk_st; g.dk_sh = a->dk_sh;
   g.dv = a->dv; g.dv_sb = a->dv_sb; g.dv_st = a->dv_st; g.dv_sh = a->dv_sh; g.dkv_dtype = a->dkv_dtype;
   g.workspace = ws + l.bsa;
-  return wa_bsa_bwd(&g, stream);
+  return wa_bsa_bwd_streams(&g, stream, dq_side ? a->dq_stream : nullptr, a->dq_fork_event, a->dq_join_event);
 }
 
 int hsa_bwd_linear(const wa_hsa_bwd_args* a, const HsaBwdLayout& l, char* ws, void* ls) {
@@ -338,6 +342,8 @@ extern "C" int wa_hsa_bwd(const wa_hsa_bwd_args* a, void* stream) {
   WA_CHECK_ARG(wa_aligned16(a->workspace), "wa_hsa_bwd: workspace must be 16-byte aligned");
   WA_CHECK_ARG(a->side_stream == nullptr || (a->fork_event && a->join_event),
                "wa_hsa_bwd: a side stream needs its fork and join events");
+  WA_CHECK_ARG(a->dq_stream == nullptr || (a->dq_fork_event && a->dq_join_event),
+               "wa_hsa_bwd: a dQ stream needs its fork and join events");
   if (a->B == 0 || a->Lq == 0) return WA_OK;
   const HsaBwdLayout l = hsa_bwd_layout(a->B, a->H, a->Lq, a->Lkv, a->D, a->block_size, a->n_sparse, a->n_linear);
   char* ws = (char*)a->workspace;

@@ -319,6 +319,11 @@ class _HSA(torch.autograd.Function):
                 cast(dEk, ekd), cast(dEv, evd), cast(dgw, gwd), cast(dgb, gbd), None)
 
 
+# The one-call backward runs the sparse heads' dQ pass on a stream of its own, beside their dK/dV
+# pass and the linear heads (False: after the transposed lists, on the caller's stream).
+DQ_STREAM = True
+
+
 def _native_split_backward(ctx, dout):
     """The backward of the one-call forward in one library call (``wa_hsa_bwd``): the sparse heads'
     ``wa_bsa_bwd`` on the caller's stream, the linear heads' gate and elu1 backward on its side
@@ -345,6 +350,7 @@ def _native_split_backward(ctx, dout):
                      dtype=torch.uint8, device=dev)
     main = torch.cuda.current_stream(dev)
     side, fork, join = _fork_join(dev, main)
+    dqs, dq_fork, dq_join = _fork_join(dev, main, 1) if DQ_STREAM else (None, None, None)
     args = _lib.HsaBwdArgs(
         *_lib.blhd(q), *_lib.blhd(k), *_lib.blhd(v), *_lib.blhd(out), _lib.dtype_code(out),
         *_lib.blhd(dout), _lib.dtype_code(dout),
@@ -354,7 +360,9 @@ def _native_split_backward(ctx, dout):
         state.data_ptr(), zsum.data_ptr(),
         _lib.ptr(spec.w), _lib.ptr(spec.b), int(spec.pre_bf16), int(spec.out_bf16), int(ex["lin_round"]),
         *_lib.blhd(dq), _lib.dtype_code(dq), *_lib.blhd(dk), *_lib.blhd(dv), _lib.dtype_code(dk),
-        _lib.ptr(dgw), _lib.ptr(dgb), ws.data_ptr(), side.cuda_stream, fork.cuda_event, join.cuda_event)
+        _lib.ptr(dgw), _lib.ptr(dgb), ws.data_ptr(), side.cuda_stream, fork.cuda_event, join.cuda_event,
+        dqs.cuda_stream if dqs is not None else None, dq_fork.cuda_event if dq_fork is not None else None,
+        dq_join.cuda_event if dq_join is not None else None)
     _lib.call("wa_hsa_bwd", args, main.cuda_stream)
     qd, kd, vd, kcd, vcd, ekd, evd, gwd, gbd = ctx.dtypes
 

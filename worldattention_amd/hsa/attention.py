@@ -398,12 +398,13 @@ def hsa_forward(q, k, v, *, k_coarse, v_coarse, k_proj_mat, v_proj_mat, gate_lin
 _FORK_JOIN: dict = {}
 
 
-def _fork_join(dev: torch.device, main: torch.cuda.Stream):
+def _fork_join(dev: torch.device, main: torch.cuda.Stream, which: int = 0):
     """The side stream of the linear branch for work issued on ``main`` (default priority), with the
     fork / join events that :func:`_native_split_forward` hands to the library: one set per caller
     stream, so calls on different streams never wait on each other's linear branch. The events are
-    recorded once here so that they exist before their handles are passed on."""
-    key = (dev.index, main.cuda_stream)
+    recorded once here so that they exist before their handles are passed on. ``which`` = 1: a
+    second such set (the one-call backward's dQ stream)."""
+    key = (dev.index, main.cuda_stream, which)
     ent = _FORK_JOIN.get(key)
     if ent is None:
         side = torch.cuda.Stream(device=dev)
