@@ -447,23 +447,37 @@ def bench_cfg3(args, dev):
     # layer-0 keys, device -> pinned blob copies on the side stream)
     chunk_frames = 6
     n_chunks = hf // chunk_frames
-    bank = W.HKVCache(frame_seq_length=ft, page_size_frames=1, topk_pages=nret, stage1_topk_chunks=n_chunks,
-                      cpu_max_chunks=max(64, n_chunks), rerope=True)
     dev_k = [keys0[:, : hf * ft]] + [cfg["host_k"][layer].to(dev) for layer in range(1, layers)]
     dev_v = [cfg["host_v"][layer].to(dev) for layer in range(layers)]
     gp = torch.Generator().manual_seed(args.seed + 7)
     prompts = [torch.randn(1, 4, 64, generator=gp).to(dev) for _ in range(n_chunks + 1)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    # the online caches of each chunk, built before the timed region (their index tensors are
+    # device scalars: creating one is a blocking host -> device copy)
+    caches = []
     for c in range(n_chunks):
         s, e = c * chunk_frames * ft, (c + 1) * chunk_frames * ft
-        kv = [{"k": dev_k[layer][:, s:e], "v": dev_v[layer][:, s:e], "local_end_index": torch.tensor(e - s, device=dev),
-               "global_end_index": torch.tensor(e, device=dev)} for layer in range(layers)]
-        bank.store(kv, prompt_embeds=prompts[c], current_start_frame=(c + 1) * chunk_frames, temporal_freqs=band)
-    torch.cuda.synchronize()
-    store_ms = (time.perf_counter() - t0) * 1e3
+        caches.append([{"k": dev_k[layer][:, s:e], "v": dev_v[layer][:, s:e],
+                        "local_end_index": torch.tensor(e - s, device=dev),
+                        "global_end_index": torch.tensor(e, device=dev)} for layer in range(layers)])
+
+    def bank_history():
+        b = W.HKVCache(frame_seq_length=ft, page_size_frames=1, topk_pages=nret, stage1_topk_chunks=n_chunks,
+                       cpu_max_chunks=max(64, n_chunks), rerope=True)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        for c in range(n_chunks):
+            b.store(caches[c], prompt_embeds=prompts[c], current_start_frame=(c + 1) * chunk_frames,
+                    temporal_freqs=band)
+        torch.cuda.synchronize()
+        return b, (time.perf_counter() - t) * 1e3
+
+    # first pass: fresh pinned blobs (first touch of every page); then the steady state, whose blobs
+    # reuse the pinned blocks the first bank released (as a full host tier reuses evicted ones)
+    bank, store_cold_ms = bank_history()
+    del bank
+    bank, store_ms = bank_history()
     store_bytes = 2 * layers * hf * ft * heads * d * 2
-    del dev_k, dev_v
+    del dev_k, dev_v, caches
     for layer in range(1, layers):
         cfg["host_k"][layer] = cfg["host_v"][layer] = None
     cfg["host_v"][0] = None
@@ -606,6 +620,7 @@ def bench_cfg3(args, dev):
         "summary_hbm_frac": round(sum_bytes / (sum_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "store_ms_all_layers": round(store_ms, 3),
         "store_gbs": round(store_bytes / (store_ms * 1e-3) / 1e9, 2),
+        "store_gbs_first_pass": round(store_bytes / (store_cold_ms * 1e-3) / 1e9, 2),
         "retrieve_ms": round(retrieve_ms, 4),
         "recall_vs_planted": recall,
         "gather_bytes_per_layer": gather_bytes,

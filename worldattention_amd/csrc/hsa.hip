@@ -113,86 +113,93 @@ int hsa_branches(const wa_hsa_fwd_args* a, const HsaLayout& l, char* ws, void* s
   const int64_t bs = a->block_size, D = a->D;
   const int64_t nq = (a->Lq + bs - 1) / bs, nkv = (a->Lkv + bs - 1) / bs;
   int rc = WA_OK;
-  // the linear heads are issued first, as in the Python orchestration
-  if (a->n_linear > 0) {
-    wa_elu1_state_args s{};
-    s.k = a->k; s.k_sb = a->k_sb; s.k_st = a->k_st; s.k_sh = a->k_sh;
-    s.v = a->v; s.v_sb = a->v_sb; s.v_st = a->v_st; s.v_sh = a->v_sh; s.dtype = WA_BF16;
-    s.B = a->B; s.H = a->H; s.L = a->Lkv; s.D = D; s.heads = a->linear_heads; s.n_heads = a->n_linear;
-    s.state = a->state ? a->state : (float*)(ws + l.state);
-    s.zsum = a->zsum ? a->zsum : (float*)(ws + l.zsum);
-    s.workspace = ws + l.elu1;
-    if ((rc = wa_elu1_state(&s, ls)) != WA_OK) return rc;
+  // Issue order: the sparse heads' chain first. A captured graph starts its branches in the
+  // order they were captured, and the sparse chain (pool, route, attention) is the longer one.
+  auto linear = [&]() -> int {
+    if (a->n_linear > 0) {
+      wa_elu1_state_args s{};
+      s.k = a->k; s.k_sb = a->k_sb; s.k_st = a->k_st; s.k_sh = a->k_sh;
+      s.v = a->v; s.v_sb = a->v_sb; s.v_st = a->v_st; s.v_sh = a->v_sh; s.dtype = WA_BF16;
+      s.B = a->B; s.H = a->H; s.L = a->Lkv; s.D = D; s.heads = a->linear_heads; s.n_heads = a->n_linear;
+      s.state = a->state ? a->state : (float*)(ws + l.state);
+      s.zsum = a->zsum ? a->zsum : (float*)(ws + l.zsum);
+      s.workspace = ws + l.elu1;
+      if ((rc = wa_elu1_state(&s, ls)) != WA_OK) return rc;
 
-    wa_elu1_readout_args o{};
-    o.q = a->q; o.q_sb = a->q_sb; o.q_st = a->q_st; o.q_sh = a->q_sh; o.q_dtype = WA_BF16;
-    o.state = s.state; o.zsum = s.zsum;
-    o.B = a->B; o.H = a->H; o.L = a->Lq; o.D = D; o.heads = a->linear_heads; o.n_heads = a->n_linear;
-    if (a->lin) {
-      // training: the readout unfused into lin, then the gate (kept) and the gated output
-      o.o = a->lin; o.o_sb = a->lin_sb; o.o_st = a->lin_st; o.o_sh = a->lin_sh; o.o_dtype = WA_F32;
-      o.epilogue = WA_EPI_PLAIN;
-      if ((rc = wa_elu1_readout(&o, ls)) != WA_OK) return rc;
-      wa_hsa_fuse_args f{};
+      wa_elu1_readout_args o{};
+      o.q = a->q; o.q_sb = a->q_sb; o.q_st = a->q_st; o.q_sh = a->q_sh; o.q_dtype = WA_BF16;
+      o.state = s.state; o.zsum = s.zsum;
+      o.B = a->B; o.H = a->H; o.L = a->Lq; o.D = D; o.heads = a->linear_heads; o.n_heads = a->n_linear;
+      if (a->lin) {
+        // training: the readout unfused into lin, then the gate (kept) and the gated output
+        o.o = a->lin; o.o_sb = a->lin_sb; o.o_st = a->lin_st; o.o_sh = a->lin_sh; o.o_dtype = WA_F32;
+        o.epilogue = WA_EPI_PLAIN;
+        if ((rc = wa_elu1_readout(&o, ls)) != WA_OK) return rc;
+        wa_hsa_fuse_args f{};
+        f.q = a->q; f.q_sb = a->q_sb; f.q_st = a->q_st; f.q_sh = a->q_sh;
+        f.lin = a->lin; f.l_sb = a->lin_sb; f.l_st = a->lin_st; f.l_sh = a->lin_sh;
+        f.head_modes = a->lin_modes;
+        f.out = a->o; f.o_sb = a->o_sb; f.o_st = a->o_st; f.o_sh = a->o_sh; f.o_dtype = a->o_dtype;
+        f.gate = a->gate; f.g_sb = a->gate_sb; f.g_st = a->gate_st; f.g_sh = a->gate_sh;
+        f.gate_w = a->gate_w; f.gate_b = a->gate_b;
+        f.gate_pre_bf16 = a->gate_pre_bf16; f.gate_out_bf16 = a->gate_out_bf16;
+        f.attn_round_bf16 = 1; f.lin_round_bf16 = a->lin_round_bf16;
+        f.B = a->B; f.H = a->H; f.L = a->Lq; f.D = D;
+        if ((rc = wa_hsa_fuse_fwd(&f, ls)) != WA_OK) return rc;
+      } else {
+        o.o = a->o; o.o_sb = a->o_sb; o.o_st = a->o_st; o.o_sh = a->o_sh; o.o_dtype = a->o_dtype;
+        o.epilogue = WA_EPI_GATED; o.gate_w = a->gate_w; o.gate_b = a->gate_b;
+        o.gate_pre_bf16 = a->gate_pre_bf16; o.gate_out_bf16 = a->gate_out_bf16; o.lin_round_bf16 = a->lin_round_bf16;
+        if ((rc = wa_elu1_readout(&o, ls)) != WA_OK) return rc;
+      }
+    }
+    return WA_OK;
+  };
+  auto sparse = [&]() -> int {
+    if (a->n_sparse > 0) {
+      // pooled queries and keys of the sparse heads (fp32 [B, H, blocks, D]; the reference's rounding)
+      wa_pool_args pj[2] = {};
+      const void* xs[2] = {a->q, a->k};
+      const int64_t sb[2] = {a->q_sb, a->k_sb}, st[2] = {a->q_st, a->k_st}, sh[2] = {a->q_sh, a->k_sh};
+      const int64_t len[2] = {a->Lq, a->Lkv}, nb[2] = {nq, nkv};
+      const int64_t off[2] = {l.qp, l.kp};
+      for (int i = 0; i < 2; ++i) {
+        pj[i].x = xs[i]; pj[i].x_sb = sb[i]; pj[i].x_st = st[i]; pj[i].x_sh = sh[i]; pj[i].x_dtype = WA_BF16;
+        pj[i].B = a->B; pj[i].L = len[i]; pj[i].H = a->H; pj[i].D = D; pj[i].block_size = bs; pj[i].num_blocks = nb[i];
+        pj[i].heads = a->sparse_heads; pj[i].n_heads = a->n_sparse;
+        pj[i].out = (float*)(ws + off[i]); pj[i].emulate_rounding = 1;
+      }
+      if ((rc = wa_block_mean_pool_n(pj, 2, stream)) != WA_OK) return rc;
+
+      // top-k routing; it also zeroes the arrival counters of the sparse launch
+      wa_route_args r{};
+      r.q_pooled = (const float*)(ws + l.qp); r.k_pooled = (const float*)(ws + l.kp);
+      r.B = a->B; r.H = a->H; r.Nq = nq; r.Nkv = nkv; r.D = D; r.mode = WA_ROUTE_TOPK;
+      r.tau_min = 0.f; r.tau_span = 1.f; r.head_k = a->head_k;
+      r.heads = a->sparse_heads; r.n_heads = a->n_sparse;
+      r.index = a->index; r.num = a->num; r.thresholds = (float*)(ws + l.thresholds);
+      r.clear = (int32_t*)(ws + l.arrivals); r.n_clear = a->B * a->n_sparse * nq;
+      if ((rc = wa_route(&r, stream)) != WA_OK) return rc;
+
+      // block-sparse attention of the sparse heads, rounded to bf16 (their output)
+      wa_bsa_fwd_args f{};
       f.q = a->q; f.q_sb = a->q_sb; f.q_st = a->q_st; f.q_sh = a->q_sh;
-      f.lin = a->lin; f.l_sb = a->lin_sb; f.l_st = a->lin_st; f.l_sh = a->lin_sh;
-      f.head_modes = a->lin_modes;
-      f.out = a->o; f.o_sb = a->o_sb; f.o_st = a->o_st; f.o_sh = a->o_sh; f.o_dtype = a->o_dtype;
-      f.gate = a->gate; f.g_sb = a->gate_sb; f.g_st = a->gate_st; f.g_sh = a->gate_sh;
-      f.gate_w = a->gate_w; f.gate_b = a->gate_b;
-      f.gate_pre_bf16 = a->gate_pre_bf16; f.gate_out_bf16 = a->gate_out_bf16;
-      f.attn_round_bf16 = 1; f.lin_round_bf16 = a->lin_round_bf16;
-      f.B = a->B; f.H = a->H; f.L = a->Lq; f.D = D;
-      if ((rc = wa_hsa_fuse_fwd(&f, ls)) != WA_OK) return rc;
-    } else {
-      o.o = a->o; o.o_sb = a->o_sb; o.o_st = a->o_st; o.o_sh = a->o_sh; o.o_dtype = a->o_dtype;
-      o.epilogue = WA_EPI_GATED; o.gate_w = a->gate_w; o.gate_b = a->gate_b;
-      o.gate_pre_bf16 = a->gate_pre_bf16; o.gate_out_bf16 = a->gate_out_bf16; o.lin_round_bf16 = a->lin_round_bf16;
-      if ((rc = wa_elu1_readout(&o, ls)) != WA_OK) return rc;
+      f.k = a->k; f.k_sb = a->k_sb; f.k_st = a->k_st; f.k_sh = a->k_sh;
+      f.v = a->v; f.v_sb = a->v_sb; f.v_st = a->v_st; f.v_sh = a->v_sh;
+      f.o = a->o; f.o_sb = a->o_sb; f.o_st = a->o_st; f.o_sh = a->o_sh; f.o_dtype = a->o_dtype;
+      f.index = a->index; f.num = a->num; f.index_width = nkv;
+      f.heads = a->sparse_heads; f.n_heads = a->n_sparse;
+      f.B = a->B; f.H = a->H; f.Lq = a->Lq; f.Lkv = a->Lkv; f.D = D; f.block_size = bs;
+      f.lse = a->lse;
+      f.epilogue = WA_EPI_PLAIN; f.attn_round_bf16 = 1;
+      f.workspace = ws + l.bsa; f.units = a->units; f.n_units = a->n_units; f.max_visits = a->max_visits;
+      f.arrivals = (int32_t*)(ws + l.arrivals);
+      if ((rc = wa_bsa_fwd(&f, stream)) != WA_OK) return rc;
     }
-  }
-
-  if (a->n_sparse > 0) {
-    // pooled queries and keys of the sparse heads (fp32 [B, H, blocks, D]; the reference's rounding)
-    wa_pool_args pj[2] = {};
-    const void* xs[2] = {a->q, a->k};
-    const int64_t sb[2] = {a->q_sb, a->k_sb}, st[2] = {a->q_st, a->k_st}, sh[2] = {a->q_sh, a->k_sh};
-    const int64_t len[2] = {a->Lq, a->Lkv}, nb[2] = {nq, nkv};
-    const int64_t off[2] = {l.qp, l.kp};
-    for (int i = 0; i < 2; ++i) {
-      pj[i].x = xs[i]; pj[i].x_sb = sb[i]; pj[i].x_st = st[i]; pj[i].x_sh = sh[i]; pj[i].x_dtype = WA_BF16;
-      pj[i].B = a->B; pj[i].L = len[i]; pj[i].H = a->H; pj[i].D = D; pj[i].block_size = bs; pj[i].num_blocks = nb[i];
-      pj[i].heads = a->sparse_heads; pj[i].n_heads = a->n_sparse;
-      pj[i].out = (float*)(ws + off[i]); pj[i].emulate_rounding = 1;
-    }
-    if ((rc = wa_block_mean_pool_n(pj, 2, stream)) != WA_OK) return rc;
-
-    // top-k routing; it also zeroes the arrival counters of the sparse launch
-    wa_route_args r{};
-    r.q_pooled = (const float*)(ws + l.qp); r.k_pooled = (const float*)(ws + l.kp);
-    r.B = a->B; r.H = a->H; r.Nq = nq; r.Nkv = nkv; r.D = D; r.mode = WA_ROUTE_TOPK;
-    r.tau_min = 0.f; r.tau_span = 1.f; r.head_k = a->head_k;
-    r.heads = a->sparse_heads; r.n_heads = a->n_sparse;
-    r.index = a->index; r.num = a->num; r.thresholds = (float*)(ws + l.thresholds);
-    r.clear = (int32_t*)(ws + l.arrivals); r.n_clear = a->B * a->n_sparse * nq;
-    if ((rc = wa_route(&r, stream)) != WA_OK) return rc;
-
-    // block-sparse attention of the sparse heads, rounded to bf16 (their output)
-    wa_bsa_fwd_args f{};
-    f.q = a->q; f.q_sb = a->q_sb; f.q_st = a->q_st; f.q_sh = a->q_sh;
-    f.k = a->k; f.k_sb = a->k_sb; f.k_st = a->k_st; f.k_sh = a->k_sh;
-    f.v = a->v; f.v_sb = a->v_sb; f.v_st = a->v_st; f.v_sh = a->v_sh;
-    f.o = a->o; f.o_sb = a->o_sb; f.o_st = a->o_st; f.o_sh = a->o_sh; f.o_dtype = a->o_dtype;
-    f.index = a->index; f.num = a->num; f.index_width = nkv;
-    f.heads = a->sparse_heads; f.n_heads = a->n_sparse;
-    f.B = a->B; f.H = a->H; f.Lq = a->Lq; f.Lkv = a->Lkv; f.D = D; f.block_size = bs;
-    f.lse = a->lse;
-    f.epilogue = WA_EPI_PLAIN; f.attn_round_bf16 = 1;
-    f.workspace = ws + l.bsa; f.units = a->units; f.n_units = a->n_units; f.max_visits = a->max_visits;
-    f.arrivals = (int32_t*)(ws + l.arrivals);
-    if ((rc = wa_bsa_fwd(&f, stream)) != WA_OK) return rc;
-  }
-  return WA_OK;
+    return WA_OK;
+  };
+  if ((rc = sparse()) != WA_OK) return rc;
+  return linear();
 }
 
 }  // namespace
