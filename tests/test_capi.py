@@ -111,3 +111,53 @@ def test_noalloc_rejects_oversized_launches_and_workspaces_without_a_gpu():
     args.workspace = fake
     assert handle.wa_bsa_fwd_noalloc(ctypes.byref(args), None) == _lib.WA_ERR_ARG
     assert b"must be NULL" in handle.wa_last_error()
+
+
+def test_one_call_entry_points_reject_bad_arguments_without_a_gpu():
+    """wa_hsa_fwd / wa_hsa_bwd argument checks run on the host before any HIP call: dummy aligned
+    pointers, no stream, nothing dereferenced or launched."""
+    handle = _lib.lib()
+    fake = 1 << 20
+    assert handle.wa_hsa_bwd(None, None) == _lib.WA_ERR_ARG
+    b = _lib.HsaBwdArgs()
+    b.q = b.k = b.v = b.dout = b.dq = b.dk = b.dv = b.workspace = fake
+    b.B, b.H, b.Lq, b.Lkv, b.D, b.block_size = 1, 4, 256, 512, 128, 128
+    b.n_sparse, b.n_linear = 2, 2
+    b.block_size = 96
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG
+    assert b"block size" in handle.wa_last_error()
+    b.block_size = 128
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG  # sparse heads without routing
+    assert b"sparse heads need" in handle.wa_last_error()
+    b.sparse_heads = b.index = b.num = b.lse = b.o = fake
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG  # linear heads without their state
+    assert b"linear heads need" in handle.wa_last_error()
+    b.linear_heads = b.lin_modes = b.lin = b.gate = b.state = b.zsum = fake
+    b.gate_w = fake
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG  # gate weight without its gradients
+    assert b"dgate_w" in handle.wa_last_error()
+    b.dgate_w = b.dgate_b = fake
+    b.side_stream = fake
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG  # side stream without events
+    assert b"fork and join" in handle.wa_last_error()
+    b.side_stream = None
+    b.dq_stream = fake
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG
+    assert b"dQ stream" in handle.wa_last_error()
+    b.dq_stream = None
+    b.dq_dtype, b.dq_sb = _lib.WA_BF16, 3   # a bf16 dq with a stride that breaks 16-byte rows
+    assert handle.wa_hsa_bwd(ctypes.byref(b), None) == _lib.WA_ERR_ARG
+    assert b"bf16 dq" in handle.wa_last_error()
+    assert handle.wa_hsa_bwd_workspace_bytes(1, 12, 4680, 32760, 128, 128, 8, 4) > 0
+
+    f = _lib.HsaFwdArgs()
+    f.q = f.k = f.v = f.o = f.workspace = fake
+    f.B, f.H, f.Lq, f.Lkv, f.D, f.block_size = 1, 4, 256, 512, 128, 128
+    f.linear_heads, f.n_linear = fake, 2
+    f.lin = fake                             # an unfused readout without its gate and modes
+    assert handle.wa_hsa_fwd(ctypes.byref(f), None) == _lib.WA_ERR_ARG
+    assert b"lin_modes" in handle.wa_last_error()
+    f.gate = f.lin_modes = fake
+    f.state = fake                           # state without zsum
+    assert handle.wa_hsa_fwd(ctypes.byref(f), None) == _lib.WA_ERR_ARG
+    assert b"state and zsum" in handle.wa_last_error()

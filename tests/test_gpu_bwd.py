@@ -365,3 +365,23 @@ def test_one_call_backward_equals_the_composed_calls(which, monkeypatch):
     for name, a, b in zip(("out", "dq", "dk", "dv", "dW", "db"), one, composed):
         assert a.dtype == b.dtype, name
         assert torch.equal(a, b), f"{which} {name}: one-call path differs from the composed calls"
+
+
+def test_one_call_backward_with_and_without_the_dq_stream_is_identical(monkeypatch):
+    """The one-call backward's sparse dQ pass on its own stream (the default) or on the caller's
+    stream after the transposed lists: the same kernels on the same inputs, the same bits."""
+    from worldattention_amd.hsa import _autograd as A
+    cfg = workloads.cfg5(device=DEV, seed=8)
+    d = cfg["q"].shape[-1]
+    gate = torch.nn.Linear(d, d).to(DEV)
+    kw = dict(k_proj_mat=None, v_proj_mat=None, gate_lin=gate, block_size=128, routing="topk", topk=cfg["topk"],
+              head_modes=cfg["head_modes"], linear_mode="elu1", proj_segment_len=1560)
+    grads = []
+    for flag in (True, False):
+        monkeypatch.setattr(A, "DQ_STREAM", flag)
+        q, k, v = (cfg[n].detach().clone().requires_grad_() for n in ("q", "k", "v"))
+        W.hsa_attention(q, k, v, **kw).backward(cfg["do"])
+        torch.cuda.synchronize()
+        grads.append((q.grad, k.grad, v.grad))
+    for name, a, b in zip(("dq", "dk", "dv"), *grads):
+        assert torch.equal(a, b), f"{name} differs with the dQ pass on the caller's stream"
