@@ -70,10 +70,12 @@ def test_spill_reload_prefetch_and_in_flight_reuse(tmp_path):
     assert os.listdir(tmp_path) == [] and not tier._writes and not tier._reads
 
 
-def test_a_finished_spill_is_read_back_from_its_file(tmp_path):
+def test_a_finished_spill_is_read_back_from_its_file(tmp_path, monkeypatch):
     tier = HKVTierManager(cpu_max_chunks=1, nvme_enabled=True, nvme_dir=str(tmp_path))
+    monkeypatch.setattr(tier, "_reap", lambda: None)  # keep the write in flight-tracking for the test
     tier.put(0, _blob(5))
     tier.put(1, _blob(6))
+    monkeypatch.undo()
     handle, blob, _ = tier._writes[0]
     _wait(handle)                                   # let the write finish, then forget it
     del tier._writes[0]
@@ -91,8 +93,10 @@ def test_a_failed_spill_keeps_the_chunk_in_host_memory_and_raises(tmp_path, monk
     import time
     from worldattention_amd.hkv import tiering
     tier = HKVTierManager(cpu_max_chunks=1, nvme_enabled=True, nvme_dir=str(tmp_path))
+    monkeypatch.setattr(tier, "_reap", lambda: None)  # the puts must not reap the spill themselves
     tier.put(0, _blob(1))
     tier.put(1, _blob(2))                          # evicts chunk 0: its spill starts
+    monkeypatch.undo()
     path = tier._files[0]
     handle = tier._writes[0][0]
     while _lib.lib().wa_io_done(handle) != 1:
