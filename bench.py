@@ -871,9 +871,6 @@ def main():
                      "achieved": round(achieved, 3), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic()},
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args, cfg, proj, c2["useful_flop"])
-    del cfg
     torch.cuda.empty_cache()
     if "ref" in extras:
         result["reference_mode"] = bench_reference_mode(args, dev)
@@ -884,6 +881,11 @@ def main():
         result["train"] = bench_cfg5(args, dev)
     if "cfg4" in extras:
         result["wan14b"] = bench_cfg4(args, dev)
+    # the CPU baseline last: its 16 host threads keep spinning for a while after each call, which
+    # had slowed the host-issue-bound cfg 3 loop that ran after it
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, cfg, proj, c2["useful_flop"])
+    del cfg
     print(json.dumps(result), flush=True)
 
 
