@@ -52,6 +52,44 @@ def _copy(src: torch.Tensor, dst: torch.Tensor) -> PageCopy:
     return PageCopy(s[0], s[1], d[0], d[1], s[2], s[3])
 
 
+def _runs_beside(candidate: torch.cuda.Stream, other: torch.cuda.Stream) -> bool:
+    """Whether work on ``candidate`` runs while ``other`` is busy: a bounded spin kernel (~1 ms) is
+    queued on ``other`` and an event on ``candidate``; the event completes first only when the two
+    streams are on different hardware queues (on a shared queue it waits behind the kernel)."""
+    busy = torch.cuda.Event()
+    with torch.cuda.stream(other):
+        torch.cuda._sleep(2_000_000)
+        busy.record(other)
+    mark = torch.cuda.Event()
+    mark.record(candidate)
+    beside = False
+    while not busy.query():
+        if mark.query():
+            beside = True
+            break
+    busy.synchronize()
+    return beside
+
+
+def _copy_stream(device: torch.device, main: torch.cuda.Stream) -> torch.cuda.Stream:
+    """The page-copy stream (default priority): one whose work runs beside the caller's stream and
+    beside the side streams the attention call uses on it (its linear branch and dQ pass). The
+    runtime maps streams onto a few hardware queues (4 by default), so a new stream may share one
+    of theirs, depending on how many streams the process created before it; the installs would
+    then run in submission order with attention instead of beside it. Up to eight pooled streams
+    are tried; the first that runs beside all of them is kept (else the last). Not probed while a
+    graph is being captured."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.cuda.Stream(device=device)
+    from ..hsa.attention import _fork_join
+    others = [main, _fork_join(device, main)[0], _fork_join(device, main, 1)[0]]
+    for _ in range(8):
+        cand = torch.cuda.Stream(device=device)
+        if all(cand.cuda_stream != o.cuda_stream for o in others) and all(_runs_beside(cand, o) for o in others):
+            return cand
+    return cand
+
+
 class HKVCache:
     """KV bank with two-stage page retrieval and multi-tier residency.
 
@@ -103,7 +141,7 @@ class HKVCache:
 
     def _side(self, device: torch.device) -> torch.cuda.Stream:
         if self._side_stream is None or self._side_stream.device != device:
-            self._side_stream = torch.cuda.Stream(device=device)  # default priority
+            self._side_stream = _copy_stream(device, torch.cuda.current_stream(device))
         return self._side_stream
 
     def _keep(self, event, objs) -> None:
