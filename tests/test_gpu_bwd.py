@@ -385,3 +385,42 @@ def test_one_call_backward_with_and_without_the_dq_stream_is_identical(monkeypat
         grads.append((q.grad, k.grad, v.grad))
     for name, a, b in zip(("dq", "dk", "dv"), *grads):
         assert torch.equal(a, b), f"{name} differs with the dQ pass on the caller's stream"
+
+
+@pytest.mark.parametrize("d,bs", [(64, 64), (128, 128)])
+def test_one_call_path_batch_of_two_matches_composed_and_oracle(d, bs, monkeypatch):
+    """Two samples, ragged lengths (Lq = 300, Lkv = 1000: partial last query and key blocks),
+    top-k sparse heads and elu1 linear heads in bf16 through the one-call forward and backward:
+    output and gradients equal the composed launches bit for bit and the oracle within the
+    forward / backward tolerances."""
+    g = torch.Generator().manual_seed(d + bs)
+    h, lq, lkv = 4, 300, 1000
+    q = (torch.randn(2, lq, h, d, generator=g)).bfloat16()
+    k = (torch.randn(2, lkv, h, d, generator=g) + torch.randn(2, 1, h, d, generator=g)).bfloat16()
+    v = torch.randn(2, lkv, h, d, generator=g).bfloat16()
+    do = torch.randn(2, lq, h, d, generator=g)
+    w, b = torch.randn(d, d, generator=g) * 0.05, torch.randn(d, generator=g) * 0.05
+    kw = dict(block_size=bs, routing="topk", topk=[3, 0, 5, 0], head_modes=["sparse", "linear", "sparse", "linear"],
+              linear_mode="elu1", proj_segment_len=lkv)
+    gate = torch.nn.Linear(d, d).to(DEV)
+    with torch.no_grad():
+        gate.weight.copy_(w)
+        gate.bias.copy_(b)
+    results = []
+    for one_call in (True, False):
+        monkeypatch.setattr(WA, "ONE_CALL", one_call)
+        qg, kg, vg = (t.to(DEV).requires_grad_() for t in (q, k, v))
+        gate.weight.grad = gate.bias.grad = None
+        out = W.hsa_attention(qg, kg, vg, k_proj_mat=None, v_proj_mat=None, gate_lin=gate, **kw)
+        out.float().backward(do.to(DEV))
+        results.append((out.detach(), qg.grad, kg.grad, vg.grad, gate.weight.grad.clone(), gate.bias.grad.clone()))
+    torch.cuda.synchronize()
+    for name, a, c in zip(("out", "dq", "dk", "dv", "dW", "db"), *results):
+        assert torch.equal(a, c), f"B=2 {name}: one-call path differs from the composed calls"
+    ref = [t.float().clone().requires_grad_() for t in (q, k, v)]
+    wr, br = w.clone().requires_grad_(), b.clone().requires_grad_()
+    out_r = O.hsa_attention(*(t.bfloat16() for t in ref), gate_weight=wr, gate_bias=br, **kw)
+    out_r.float().backward(do)
+    assert_close(results[0][0], out_r, what="B=2 out")
+    for name, got, r in zip(("dq", "dk", "dv"), results[0][1:4], ref):
+        assert_close(got, r.grad, what=f"B=2 {name}")
