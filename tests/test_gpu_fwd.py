@@ -480,6 +480,41 @@ def test_bsa_large_logits_rescale_matches_oracle(order, split):
     assert_close(got, want, what=f"{order} logits, split {split}")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("split", [32, 64])
+@pytest.mark.parametrize("logits", ["plain", "rising"])
+def test_bsa_key_split_long_rows_match_oracle(d, split, logits):
+    """64-key blocks with units of at least 32 visits run the key-split kernel (two waves per query
+    tile, one per 32-key half of every step, merged in LDS): rows of 0 to 90 visits (several units
+    per row past `split`, each unit's slice visited in block order), a partial last key block whose
+    real keys end inside the first half of its step, a partial last query block, duplicates, and
+    logits that rise along the blocks so the halves' running maxima differ when they merge."""
+    from worldattention_amd.hsa.block_sparse import bsa_forward
+    torch.manual_seed(d + split)
+    bs, b, h, nq, nkv = 64, 1, 2, 3, 90
+    lq, lkv = nq * bs - 20, nkv * bs - 40
+    q = torch.randn(b, lq, h, d)
+    k = torch.randn(b, nkv * bs, h, d)
+    if logits == "rising":
+        q = q * 2
+        k = k * (torch.arange(nkv, dtype=torch.float32) * 0.25 + 1).repeat_interleave(bs).view(1, -1, 1, 1)
+    k = k[:, :lkv]
+    v = torch.randn(b, lkv, h, d)
+    q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    index = torch.stack([torch.randperm(nkv) for _ in range(b * h * nq)]).view(b, h, nq, nkv).int()
+    num = torch.tensor([[90, 0, 33], [64, 71, 20]], dtype=torch.int32).view(b, h, nq)
+    index[0, 1, 0, 10:13] = 17              # duplicates count
+    got, _ = bsa_forward(q.to(DEV), k.to(DEV), v.to(DEV), index=index.to(DEV), num=num.to(DEV), block_size=bs,
+                         layout="blhd", lq=lq, lkv=lkv, split=split, out_dtype=torch.float32)
+    qp = O.pad_to_len(q, nq * bs).transpose(1, 2)
+    kp, vp = (O.pad_to_len(t, nkv * bs).transpose(1, 2) for t in (k, v))
+    sizes = O.variable_block_sizes(lkv, nkv * bs, bs)
+    want = O.block_sparse_attention(qp.float(), kp.float(), vp.float(), index, num, sizes, bs).transpose(1, 2)[:, :lq]
+    assert torch.isfinite(got).all()
+    assert_close(got, want, what=f"key split d={d} split={split} {logits}")
+    assert torch.count_nonzero(got[0, bs:2 * bs, 0]) == 0
+
+
 def test_hsa_forward_graph_replays_equal_eager_calls():
     """The cfg 2 call captured in a HIP graph (as bench.py times it): every replay, with eager work
     and synchronizations between replays, equals the eager call bit for bit."""

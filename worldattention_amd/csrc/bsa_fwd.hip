@@ -405,11 +405,15 @@ __device__ __forceinline__ bool pipe_check(const float (&rs)[QT]) {
 // tiles vw = QT w .. QT w + QT - 1 (query rows [32 vw, 32 vw + 32) of the block). QT = 1: four
 // waves (BS = 128), two workgroups per CU sharing its SIMDs; QT = 2: two waves of 64 queries with
 // up to 512 registers each (one wave per SIMD), so every K / V fragment read feeds two products.
-template <int D, int BS, int QT>
-__global__ void __launch_bounds__(2 * BS / QT) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1)))
+// KS = 2 (64-key blocks): each query tile gets two waves, one per 32-key half of every step, which
+// share the K / V tiles and meet through LDS after the loop; a 64-query workgroup is then four
+// waves, so its two workgroups per CU (the LDS ring allows two) give each SIMD two waves.
+template <int D, int BS, int QT, int KS>
+__global__ void __launch_bounds__(2 * BS / QT * KS) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1)))
 bsa_unit_kernel(FwdParams p) {
-  constexpr int NW = BS / (32 * QT);
-  constexpr int NVW = NW * QT;  // 32-query tiles per workgroup
+  constexpr int NW = BS / (32 * QT);  // query waves
+  constexpr int NWT = NW * KS;        // waves
+  constexpr int NVW = NW * QT;        // 32-query tiles per workgroup
   constexpr int DC = D / 16, DT = D / 32;
   constexpr int TILE = 64 * D;  // elements of one K (or V) step tile
   // Two K and two V step tiles (64 KiB at D = 128: two workgroups per CU), one array per stage, fed
@@ -418,10 +422,11 @@ bsa_unit_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) bf16_t ks1[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t vs0[TILE];
   __shared__ __attribute__((aligned(1024))) bf16_t vs1[TILE];
-  __shared__ int steptab[NW][64][2];
+  __shared__ int steptab[NWT][64][2];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
+  const int qw = w % NW, kh = w / NW;  // query wave; key half (KS = 2)
 
   const int u = wa_xcd_remap(blockIdx.x, p.n_units);
   // The prologue's memory reads in two round trips: the unit entry with the head map beside it,
@@ -462,7 +467,7 @@ bsa_unit_kernel(FwdParams p) {
   bf16x8 qf[QT][DC];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    qi[qt] = qb * BS + (w * QT + qt) * 32 + l32;
+    qi[qt] = qb * BS + (qw * QT + qt) * 32 + l32;
     q_ok[qt] = qi[qt] < p.Lq;
     qrow[qt] = p.q + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh + (int64_t)(q_ok[qt] ? qi[qt] : 0) * p.q_st;
 #pragma unroll
@@ -486,14 +491,14 @@ bsa_unit_kernel(FwdParams p) {
   // block id, and split s of the row's ns units takes the sorted positions s, s + ns, s + 2 ns, ...:
   // every unit of a head (they run together on one XCD) then sweeps the whole key range in step
   // with the others, so the units that list a block fetch it at about the same time and share it in
-  // L2. The visit order only changes the summation order. Longer rows keep list order, one
-  // contiguous slice per unit.
+  // L2. The visit order only changes the summation order. A longer row gives each unit one
+  // contiguous slice of its list, sorted by block id the same way (a dense row is in order).
   const bool whole = n <= 64;
   const int lo = whole ? 0 : s_begin;
   const int take = whole ? n : s_end - s_begin;
   int my_j = 0;
   if (lane < take) my_j = p.index ? min(max(lo == 0 ? j0 : j1, 0), p.Nkv - 1) : lo + lane;
-  if (whole) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
+  if (whole || p.index) my_j = wave_sort_ascending(lane < take ? my_j : 0x7fffffff, lane);
   const bool mine = whole ? lane < n && lane % ns == split : lane < take;
   const int my_real = mine ? block_real(p, my_j, BS) : 0;
 
@@ -521,11 +526,11 @@ bsa_unit_kernel(FwdParams p) {
   // Tile loads: this lane's loop-invariant chunk offsets; each tile gets a buffer descriptor that
   // starts at its first row and ends at the slab's end (rows past the slab read zeros), and a step
   // past the end of the table an empty one (zeros, no memory traffic).
-  using NT = NextTile<D, NW>;
+  using NT = NextTile<D, NWT>;
   int k_off[NT::NI], v_off[NT::NI];
 #pragma unroll
   for (int i = 0; i < NT::NI; ++i) {
-    const int row = (i * NW + w) * NT::RPI + lane / NT::CPR, pos = lane % NT::CPR;
+    const int row = (i * NWT + w) * NT::RPI + lane / NT::CPR, pos = lane % NT::CPR;
     k_off[i] = (int)(row * p.k_st + (pos ^ k_swizzle<D>(row)) * 8) * 2;
     v_off[i] = (int)(row * p.v_st + (pos ^ v_swizzle(row)) * 8) * 2;
   }
@@ -539,7 +544,7 @@ bsa_unit_kernel(FwdParams p) {
   auto load_tile = [&](int s, bool is_k, bf16_t* lds) {
     const __amdgpu_buffer_rsrc_t rs = tile_rs(s, is_k);
 #pragma unroll
-    for (int i = 0; i < NT::NI; ++i) pipe_dma16(rs, lds + (i * NW + w) * NT::RPI * D, is_k ? k_off[i] : v_off[i]);
+    for (int i = 0; i < NT::NI; ++i) pipe_dma16(rs, lds + (i * NWT + w) * NT::RPI * D, is_k ? k_off[i] : v_off[i]);
   };
   // Q fragments in registers before the first tile loads (a later first use would wait for them)
 #pragma unroll
@@ -602,70 +607,153 @@ bsa_unit_kernel(FwdParams p) {
   }
   const float sl2 = p.scale_log2;
   const PipeLoad no_load{};
-  if (T > 0) {
-    load_tile(0, true, ks0);
-    load_tile(1, true, ks1);
-    load_tile(0, false, vs0);
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NT::NI) : "memory");
-    set_neg_m();
-    pipe_slot<D, NW, QT, 1, false, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
-                                                       k_off, no_load, v_off, w, rs);
-    int real_prev = __builtin_amdgcn_readlane(tab_real, 0);
-    if (real_prev < 32) pipe_mask<0, QT>(S[0], real_prev, g);
-    pipe_slot<D, NW, QT, 0, true, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
-                                                      k_off, no_load, v_off, w, rs);
-    if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 0>(S[0], P, oacc, m_i, l_i, rs, sl2);
-    add_l();
-
-    auto block = [&](auto par, int b) {
-      constexpr int PAR = decltype(par)::value;
-      bf16_t* const kcur = PAR ? ks1 : ks0;
-      bf16_t* const knext = PAR ? ks0 : ks1;
-      bf16_t* const vprev = PAR ? vs0 : vs1;
-      bf16_t* const vcur = PAR ? vs1 : vs0;
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
-      const PipeLoad ldk{tile_rs(b + 1, true), knext}, ldv{tile_rs(b, false), vcur};
+  if constexpr (KS == 1) {
+    if (T > 0) {
+      load_tile(0, true, ks0);
+      load_tile(1, true, ks1);
+      load_tile(0, false, vs0);
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NT::NI) : "memory");
       set_neg_m();
-      pipe_slot<D, NW, QT, 1, true, true, true, true>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, ldk, k_off,
-                                                      ldv, v_off, w, rs);
-      if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
-      add_l();
-      const int real = __builtin_amdgcn_readlane(tab_real, b);
-      if (real < 32) pipe_mask<0, QT>(S[0], real, g);
-      set_neg_m();
-      pipe_slot<D, NW, QT, 0, true, true, true, false>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, no_load,
-                                                       k_off, no_load, v_off, w, rs);
+      pipe_slot<D, NWT, QT, 1, false, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
+                                                         k_off, no_load, v_off, w, rs);
+      int real_prev = __builtin_amdgcn_readlane(tab_real, 0);
+      if (real_prev < 32) pipe_mask<0, QT>(S[0], real_prev, g);
+      pipe_slot<D, NWT, QT, 0, true, true, false, false>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2, no_load,
+                                                        k_off, no_load, v_off, w, rs);
       if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 0>(S[0], P, oacc, m_i, l_i, rs, sl2);
       add_l();
-      real_prev = real;
-    };
-    int b = 1;
-    for (; b + 1 < T; b += 2) {
-      block(std::integral_constant<int, 1>{}, b);
-      block(std::integral_constant<int, 0>{}, b + 1);
-    }
-    if (b < T) block(std::integral_constant<int, 1>{}, b);
 
-    auto last = [&](auto par) {
-      constexpr int PAR = decltype(par)::value;  // (T - 1) % 2: stage of V(T - 1)
-      bf16_t* const vprev = PAR ? vs1 : vs0;
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
-      set_neg_m();
-      pipe_slot<D, NW, QT, 1, true, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
-                                                        k_off, no_load, v_off, w, rs);
-      if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
-      add_l();
-      pipe_slot<D, NW, QT, 0, false, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+      auto block = [&](auto par, int b) {
+        constexpr int PAR = decltype(par)::value;
+        bf16_t* const kcur = PAR ? ks1 : ks0;
+        bf16_t* const knext = PAR ? ks0 : ks1;
+        bf16_t* const vprev = PAR ? vs0 : vs1;
+        bf16_t* const vcur = PAR ? vs1 : vs0;
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
+        const PipeLoad ldk{tile_rs(b + 1, true), knext}, ldv{tile_rs(b, false), vcur};
+        set_neg_m();
+        pipe_slot<D, NWT, QT, 1, true, true, true, true>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, ldk, k_off,
+                                                        ldv, v_off, w, rs);
+        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
+        add_l();
+        const int real = __builtin_amdgcn_readlane(tab_real, b);
+        if (real < 32) pipe_mask<0, QT>(S[0], real, g);
+        set_neg_m();
+        pipe_slot<D, NWT, QT, 0, true, true, true, false>(S, P, oacc, qf, kcur, vprev, k_rd, v_rd, neg_m, sl2, no_load,
                                                          k_off, no_load, v_off, w, rs);
+        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 0>(S[0], P, oacc, m_i, l_i, rs, sl2);
+        add_l();
+        real_prev = real;
+      };
+      int b = 1;
+      for (; b + 1 < T; b += 2) {
+        block(std::integral_constant<int, 1>{}, b);
+        block(std::integral_constant<int, 0>{}, b + 1);
+      }
+      if (b < T) block(std::integral_constant<int, 1>{}, b);
+
+      auto last = [&](auto par) {
+        constexpr int PAR = decltype(par)::value;  // (T - 1) % 2: stage of V(T - 1)
+        bf16_t* const vprev = PAR ? vs1 : vs0;
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (real_prev < 64) pipe_mask<1, QT>(S[1], real_prev, g);
+        set_neg_m();
+        pipe_slot<D, NWT, QT, 1, true, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+                                                          k_off, no_load, v_off, w, rs);
+        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, 1>(S[1], P, oacc, m_i, l_i, rs, sl2);
+        add_l();
+        pipe_slot<D, NWT, QT, 0, false, false, true, false>(S, P, oacc, qf, ks0, vprev, k_rd, v_rd, neg_m, sl2, no_load,
+                                                           k_off, no_load, v_off, w, rs);
+      };
+      if ((T - 1) & 1) last(std::integral_constant<int, 1>{});
+      else last(std::integral_constant<int, 0>{});
+    }
+  } else {
+    // Key split: this wave computes key half kh of every 64-key step. Step t's tiles are in stage
+    // t % 2; at its top this wave's loads of them have landed and the barrier extends that to the
+    // workgroup and frees the other stage (read by step t - 1), which then takes step t + 1's
+    // tiles. A half with no real key is skipped (the first half a wave computes then always holds
+    // one, so the running max starts finite); the exponentials are accepted by the same per-lane
+    // sum check as above, and rescaled before the PV product uses them.
+    auto run = [&](auto khc) {
+      constexpr int KH = decltype(khc)::value;
+      auto step = [&](auto par, int t) {
+        constexpr int PAR = decltype(par)::value;
+        bf16_t* const kc = PAR ? ks1 : ks0;
+        bf16_t* const vc = PAR ? vs1 : vs0;
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (t + 1 < T) {
+          load_tile(t + 1, true, PAR ? ks0 : ks1);
+          load_tile(t + 1, false, PAR ? vs0 : vs1);
+        }
+        const int real = __builtin_amdgcn_readlane(tab_real, t & 63);
+        if (real <= 32 * KH) return;  // uniform: this half holds no key
+        pipe_slot<D, NWT, QT, KH ^ 1, false, true, false, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2,
+                                                                 no_load, k_off, no_load, v_off, w, rs);
+        if (real < 32 * (KH + 1)) pipe_mask<KH, QT>(S[KH], real, g);
+        set_neg_m();
+        pipe_slot<D, NWT, QT, KH, true, false, false, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2, no_load,
+                                                             k_off, no_load, v_off, w, rs);
+        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, KH>(S[KH], P, oacc, m_i, l_i, rs, sl2);
+        add_l();
+        pipe_slot<D, NWT, QT, KH ^ 1, false, false, true, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2,
+                                                                 no_load, k_off, no_load, v_off, w, rs);
+      };
+      if (T > 0) {
+        load_tile(0, true, ks0);
+        load_tile(0, false, vs0);
+      }
+      for (int t = 0; t < T; t += 2) {
+        step(std::integral_constant<int, 0>{}, t);
+        if (t + 1 < T) step(std::integral_constant<int, 1>{}, t + 1);
+      }
     };
-    if ((T - 1) & 1) last(std::integral_constant<int, 1>{});
-    else last(std::integral_constant<int, 0>{});
+    if (kh == 0) run(std::integral_constant<int, 0>{});
+    else run(std::integral_constant<int, 1>{});
   }
 
   // every tile load has landed (block T waited for the last ones)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (KS == 2) {
+    // The two key halves of each query tile meet: the half-1 wave leaves its running max, row sums
+    // and accumulators in the drained ring, and the half-0 wave folds them into its own against the
+    // larger max (lanes hold the same queries and key subsets in both waves).
+    static_assert(QT * DT * 16 * 64 * 4 <= TILE * 2 && NW <= 2, "key-half exchange does not fit the ring");
+    __syncthreads();  // every wave is done with the last step's tiles
+    float* xo = (float*)(qw == 0 ? ks0 : ks1);
+    float* xs = (float*)vs0 + qw * 2 * QT * 64;
+    if (kh == 1) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) xo[((qt * DT + t) * 16 + r) * 64 + lane] = oacc[qt][t][r];
+        }
+        xs[(qt * 2) * 64 + lane] = m_i[qt];
+        xs[(qt * 2 + 1) * 64 + lane] = l_i[qt];
+      }
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const float m1 = xs[(qt * 2) * 64 + lane], l1 = xs[(qt * 2 + 1) * 64 + lane];
+        const float mm = fmaxf(m_i[qt], m1);
+        const float a0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i[qt] - mm);
+        const float a1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+        l_i[qt] = l_i[qt] * a0 + l1 * a1;
+        m_i[qt] = mm;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            oacc[qt][t][r] = oacc[qt][t][r] * a0 + xo[((qt * DT + t) * 16 + r) * 64 + lane] * a1;
+        }
+      }
+    }
+  }
   float inv[QT], lse2[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -693,7 +781,8 @@ bsa_unit_kernel(FwdParams p) {
     constexpr int SC1 = 16;  // cache policy: device-scope coherent
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const int vw = w * QT + qt;
+      if (KS == 2 && kh == 1) break;  // the half-0 wave holds the merged tile
+      const int vw = qw * QT + qt;
       if (g == 0)
         __hip_atomic_store(p.part_lse + (slot0 + split) * BS + vw * 32 + l32, lse2[qt], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -718,6 +807,7 @@ bsa_unit_kernel(FwdParams p) {
     }
     __syncthreads();
     if (!__builtin_amdgcn_readfirstlane(*s_last)) return;  // uniform: one LDS word for every lane
+    if (KS == 2 && kh == 1) return;
     // Another unit's partial comes in by direct-to-LDS loads into one free ring stage per query
     // tile (each wave reads back only what it loaded: no workgroup barrier), the first one together
     // with the first four log2-sum-exps, so a two-unit row merges after one round trip.
@@ -725,7 +815,7 @@ bsa_unit_kernel(FwdParams p) {
     char* wbuf[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const int vw = w * QT + qt;
+      const int vw = qw * QT + qt;
       wbuf[qt] = (char*)(vw == 0 ? ks0 : vw == 1 ? ks1 : vw == 2 ? vs0 : vs1);
     }
     auto fetch_part = [&](int sp) {
@@ -735,7 +825,7 @@ bsa_unit_kernel(FwdParams p) {
         for (int t = 0; t < DT; ++t) {
 #pragma unroll
           for (int rq = 0; rq < 4; ++rq)
-            lds_dma16_sc1(prs, wbuf[qt] + (t * 4 + rq) * 1024, frag_off(sp, w * QT + qt, t, rq));
+            lds_dma16_sc1(prs, wbuf[qt] + (t * 4 + rq) * 1024, frag_off(sp, qw * QT + qt, t, rq));
         }
       }
     };
@@ -744,7 +834,7 @@ bsa_unit_kernel(FwdParams p) {
     float lsv[QT][4];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const float* plse = p.part_lse + slot0 * BS + (w * QT + qt) * 32 + l32;
+      const float* plse = p.part_lse + slot0 * BS + (qw * QT + qt) * 32 + l32;
 #pragma unroll
       for (int sp = 0; sp < 4; ++sp)
         lsv[qt][sp] = sp >= ns ? -INFINITY
@@ -754,7 +844,7 @@ bsa_unit_kernel(FwdParams p) {
     auto lse_of = [&](int qt, int sp) {
       if (sp < 4) return lsv[qt][sp];
       if (sp == split) return lse2[qt];
-      return __hip_atomic_load(p.part_lse + slot0 * BS + (w * QT + qt) * 32 + l32 + sp * BS, __ATOMIC_RELAXED,
+      return __hip_atomic_load(p.part_lse + slot0 * BS + (qw * QT + qt) * 32 + l32 + sp * BS, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     };
     float M[QT], Z[QT];
@@ -819,6 +909,7 @@ bsa_unit_kernel(FwdParams p) {
       lse2[qt] = Z[qt] > 0.f ? M[qt] + log2f(Z[qt]) : -INFINITY;
     }
   }
+  if (KS == 2 && kh == 1) return;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     if (p.lse && g == 0 && q_ok[qt]) p.lse[((int64_t)b * p.H + h) * p.Lq + qi[qt]] = lse2[qt] * WA_LN2;
@@ -895,7 +986,7 @@ __global__ void __launch_bounds__(256) bsa_clear_arrivals_kernel(int* arrivals, 
 }
 
 template <int D, int BS>
-int launch(const FwdParams& fp, int64_t rows, bool cleared, hipStream_t stream) {
+int launch(const FwdParams& fp, int64_t rows, bool cleared, bool key_split, hipStream_t stream) {
   if (!cleared) {
     hipLaunchKernelGGL(bsa_clear_arrivals_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream,
                        fp.arrivals, rows);
@@ -904,8 +995,18 @@ int launch(const FwdParams& fp, int64_t rows, bool cleared, hipStream_t stream) 
   }
   // 32 queries per wave. (64 per wave, QT = 2, halves the LDS reads per product but needs more
   // than 256 registers: as compiled today its loop moves ~1,600 values between AGPRs and VGPRs.)
+  // 64-key blocks with long units split each step's keys between two waves (four waves per
+  // workgroup: 712 against 735 us for the reference mode's sparse launch at the Wan shape, 180
+  // visits per row); a short unit (the dense launch over ~9 compressed key blocks) does better
+  // with its two waves' pipelined loop (57 against 62 us).
   constexpr int QT = 1;
-  hipLaunchKernelGGL((bsa_unit_kernel<D, BS, QT>), dim3(fp.n_units), dim3(2 * BS / QT), 0, stream, fp);
+  if constexpr (BS == 64) {
+    if (key_split) {
+      hipLaunchKernelGGL((bsa_unit_kernel<D, BS, QT, 2>), dim3(fp.n_units), dim3(4 * BS / QT), 0, stream, fp);
+      return wa_launch_status("bsa_fwd_unit");
+    }
+  }
+  hipLaunchKernelGGL((bsa_unit_kernel<D, BS, QT, 1>), dim3(fp.n_units), dim3(2 * BS / QT), 0, stream, fp);
   return wa_launch_status("bsa_fwd_unit");
 }
 
@@ -1093,10 +1194,12 @@ int bsa_fwd_impl(const wa_bsa_fwd_args* a, void* workspace, void* stream) {
                        dim3((unsigned)rows), dim3(2 * a->block_size), 0, s, fp);
     return wa_launch_status("bsa_fwd_empty_rows");
   }
-  if (a->D == 64 && a->block_size == 64) return launch<64, 64>(fp, rows, cleared, s);
-  if (a->D == 64 && a->block_size == 128) return launch<64, 128>(fp, rows, cleared, s);
-  if (a->D == 128 && a->block_size == 64) return launch<128, 64>(fp, rows, cleared, s);
-  return launch<128, 128>(fp, rows, cleared, s);
+  // steps per unit: one per visit of a 64-key block
+  const bool key_split = a->block_size == 64 && (split < max_visits ? split : max_visits) >= 32;
+  if (a->D == 64 && a->block_size == 64) return launch<64, 64>(fp, rows, cleared, key_split, s);
+  if (a->D == 64 && a->block_size == 128) return launch<64, 128>(fp, rows, cleared, false, s);
+  if (a->D == 128 && a->block_size == 64) return launch<128, 64>(fp, rows, cleared, key_split, s);
+  return launch<128, 128>(fp, rows, cleared, false, s);
 }
 
 }  // namespace
