@@ -256,20 +256,15 @@ __global__ void __launch_bounds__(256) k2q_kernel(BwdParams p) {
   p.k2q_num[((int64_t)b * p.n_heads + hs) * p.Nkv + j] = cnt;
 }
 
-// The dq and dkdv passes keep one workgroup per CU (their accumulators and operand fragments
-// take 300-400 registers per lane), so they spend the CU's LDS on a 4-stage tile ring: the tiles of
-// steps t + 1 .. t + 2 stream in while step t is computed, and step t + 3 is issued into the stage
-// freed by step t - 1. Every step issues the same number of loads (an empty half-block streams
-// the slab's first rows), so the waits count them: at the top of step t only the loads of the (up to
-// two) later tiles may still be pending. Row lists (with each block's valid row count) are staged
-// in LDS once, so the loop issues no other memory reads while they fit.
-// Ring depth and staged list length of the dK/dV pass: one workgroup per CU (8 waves for 128-row
-// blocks) with a 3-stage ring, the staged list and the P exchange in its LDS; dQ fits two waves per
-// SIMD (256 registers), so two workgroups share a CU and it keeps a 2-stage ring (two rings fit the
-// CU's LDS).
-template <int BS> constexpr int bwd_stages() { return BS == 128 ? 3 : 2; }
-template <int BS> constexpr int bwd_list_max() { return BS == 128 ? 4096 : 1024; }
+// The dq and dkdv passes stream their tiles through a ring of LDS stages: the tile of step t + 1
+// streams in while step t is computed, issued into the stage step t - 1 freed. Every step issues the
+// same number of loads (an empty half-block streams the slab's first rows), so the waits count
+// them. Row lists (with each block's valid row count) are staged in LDS once, so the loop issues no
+// other memory reads while they fit. Both passes run two waves per SIMD (up to 256 registers) as
+// two workgroups per CU, each with a 2-stage ring, its staged list (and for dK/dV the P exchange)
+// in half the CU's LDS: while one workgroup sets up or writes its result, the other computes.
 constexpr int DQ_STAGES = 2, DQ_LIST_MAX = 1024;
+constexpr int DKDV_KEYS = 64, DKDV_STAGES = 2, DKDV_LIST_MAX = 1024;
 
 template <int N> using IC = std::integral_constant<int, N>;
 
@@ -517,43 +512,49 @@ __global__ void __launch_bounds__(KV_ORDER_T) kv_order_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// dkdv: one workgroup per (batch, head slot, key block); 64-query steps over the query blocks that
-// listed it; Q, dO and the rows' log-sum-exp and delta stream through the ring (the statistics as
-// 4-byte direct-to-LDS loads, scaled at use). Each 32-key group has two waves, w and w + NKG, which
-// share a SIMD:
-//   the S-wave (w < NKG) holds the group's K fragments and the dV accumulators: S = Q K^T,
-//     P = exp2(S scale - lse2) (fp32, to LDS), dV += P^T dO;
+// dkdv: one workgroup per (batch, head slot, key block, 64-key part: HB = BS / 64 per block);
+// 64-query steps over the query blocks that listed the block; Q, dO and the rows' log-sum-exp and
+// delta stream through the ring (the statistics as 4-byte direct-to-LDS loads, scaled at use). The
+// parts of a block walk the same list at neighbouring grid positions, so they share the tiles in
+// L2. Each 32-key group has two waves, w and w + 2:
+//   the S-wave (w < 2) holds the group's K fragments and the dV accumulators: S = Q K^T,
+//     P = exp2(S scale - lse2) (to LDS as fp16: 11 significant bits, 4x finer than the bf16 dS it
+//     feeds), dV += P^T dO;
 //   the dP-wave holds the V fragments and the dK accumulators: dP = dO V^T, then (P from LDS)
 //     dS = P (dP - delta), dK += dS^T Q.
-// Each wave keeps about half the registers of one wave per group (K/V fragments and both
-// accumulators, ~450 per lane), so two waves fit a SIMD and one's softmax runs beside the other's
-// MFMAs.
+// A workgroup of four waves takes 77 KiB of LDS, so two share a CU (two waves per SIMD): one's
+// set-up (the K / V fragments and first tiles, a memory round trip) and result stores run while
+// the other computes, and their step barriers fall at different times.
 // ---------------------------------------------------------------------------------------------
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
 template <int D, int BS>
-__global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
-  constexpr int NKG = BS / 32, NW = 2 * NKG, NT = 64 * NW, DC = D / 16, DT = D / 32;
-  constexpr int TILE = 64 * D, ST = bwd_stages<BS>(), LM = bwd_list_max<BS>();
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) bwd_dkdv_kernel(BwdParams p) {
+  constexpr int KW = DKDV_KEYS, HB = BS / KW, NKG = KW / 32, NW = 2 * NKG, NT = 64 * NW, DC = D / 16, DT = D / 32;
+  constexpr int TILE = 64 * D, ST = DKDV_STAGES, LM = DKDV_LIST_MAX;
   constexpr int QPB = BS / 64;                     // 64-query steps per query block
   using TS = TileStream<D, NW>;
   constexpr int PER = 2 * TS::NI + 2;              // Q and dO tiles, lse and delta rows
   // stage s: Q tile at [0, TILE), dO tile at [TILE, 2 TILE), then 64 lse and 64 delta floats
-  constexpr int SS = 2 * TILE + 256, XS2 = ST >= 3 ? SS : 8, XS3 = ST >= 4 ? SS : 8;
+  constexpr int SS = 2 * TILE + 256;
+  static_assert(ST == 2 && NW == 4, "two ring stages, four waves");
   __shared__ __attribute__((aligned(1024))) bf16_t qd0[SS];
   __shared__ __attribute__((aligned(1024))) bf16_t qd1[SS];
-  __shared__ __attribute__((aligned(1024))) bf16_t qd2[XS2];
-  __shared__ __attribute__((aligned(1024))) bf16_t qd3[XS3];
-  // P of each key group (fp32, accumulator order), register r of 32-query tile qt of lane L at
-  // [group][qt][r / 4][L]: every access is 16 bytes per lane, lanes contiguous
-  __shared__ __attribute__((aligned(1024))) f32x4 s_p[NKG][2][4][64];
+  bf16_t* const qd2 = qd0;  // (no third or fourth stage)
+  bf16_t* const qd3 = qd1;
+  // P of each key group (fp16, accumulator order), register r of 32-query tile qt of lane L at
+  // [group][qt][r / 4][L]: every access is 8 bytes per lane, lanes contiguous
+  __shared__ __attribute__((aligned(1024))) f16x4 s_p[NKG][2][4][64];
   __shared__ int32_t s_lst[LM];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int kg = w % NKG;
   const bool swave = w < NKG;  // wave-uniform role
-  // 1-D grid over (batch, head slot, key block): XCD by XCD through kv_info when there is one
-  // (else through the slabs in order), so an XCD's workgroups share their slabs' Q and dO tiles;
-  // one load gives the block, its list length and its first list entry
-  const int pos = wa_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  // 1-D grid over (batch, head slot, key block, part): XCD by XCD through kv_info when there is
+  // one (else through the slabs in order), so an XCD's workgroups share their slabs' Q and dO
+  // tiles; one load gives the block, its list length and its first list entry
+  const int gpos = wa_xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int pos = gpos / HB, hb = gpos % HB;
   int id, nl, e0;
   if (p.kv_info) {
     const int4 inf = p.kv_info[pos];
@@ -571,13 +572,14 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
   const int j = id % p.Nkv, hs = (id / p.Nkv) % p.n_heads, b = id / (p.Nkv * p.n_heads);
   const int h = head_of(p, hs);
   if (h < 0 || h >= p.H) return;
+  const int kb0 = j * BS + hb * KW;  // first key of this part
   if (nl == 0) {
     // no query block listed this key block: its written gradients are zero (accumulated ones
     // keep their values), with no tile streamed
-    const int rows = max(0, min(BS, p.Lkv - j * BS));
+    const int rows = max(0, min(KW, p.Lkv - kb0));
     constexpr int CPR = D / 8;
-    const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + (int64_t)j * BS * p.dk_st;
-    const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + (int64_t)j * BS * p.dv_st;
+    const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh + (int64_t)kb0 * p.dk_st;
+    const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh + (int64_t)kb0 * p.dv_st;
     if (p.dkv_vec) {
       for (int u = tid; u < rows * CPR; u += NT) {
         const int kk = u / CPR, c = u % CPR;
@@ -599,7 +601,8 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
     return;
   }
   const int real = kv_real(p, j, BS);
-  const int key = kg * 32 + l32;  // this lane's key within the block
+  const int kl = kg * 32 + l32;  // this lane's key within the part
+  const int key = hb * KW + kl;  // ... and within the block
   const bool k_ok = key < real;
   const int64_t srow = ((int64_t)b * p.n_heads + hs) * p.Lq;
   const int32_t* lst = p.k2q + (((int64_t)b * p.n_heads + hs) * p.Nkv + j) * p.Nq;
@@ -676,7 +679,7 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
             p4[i] = __builtin_amdgcn_exp2f(fmaf(sacc[qt][r], p.scale_log2, -l4[i])) * mult;
             ab[qt * 2 + (r >> 3)][r & 7] = (bf16_t)p4[i];
           }
-          s_p[kg][qt][rq][lane] = p4;
+          s_p[kg][qt][rq][lane] = f16x4{(_Float16)p4[0], (_Float16)p4[1], (_Float16)p4[2], (_Float16)p4[3]};
         }
       }
     }
@@ -687,11 +690,11 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
           const f32x4 d4 = *(const f32x4*)(st_dl + qt * 32 + 8 * rq + 4 * g);
-          const f32x4 p4 = s_p[kg][qt][rq][lane];
+          const f16x4 p4 = s_p[kg][qt][rq][lane];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = rq * 4 + i;
-            ab[qt * 2 + (r >> 3)][r & 7] = (bf16_t)(p4[i] * (sacc[qt][r] - d4[i]));
+            ab[qt * 2 + (r >> 3)][r & 7] = (bf16_t)((float)p4[i] * (sacc[qt][r] - d4[i]));
           }
         }
       }
@@ -755,15 +758,15 @@ __global__ void __launch_bounds__(4 * BS) bwd_dkdv_kernel(BwdParams p) {
         bf16x4 v4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v4[i] = (bf16_t)(k_ok ? acc[tt][rq * 4 + i] * osc : 0.f);
-        *(bf16x4*)(stg + key * D + (((4 * tt + rq) ^ swz(key)) << 3) + 4 * g) = v4;
+        *(bf16x4*)(stg + kl * D + (((4 * tt + rq) ^ swz(kl)) << 3) + 4 * g) = v4;
       }
     }
     __syncthreads();
     constexpr int CPR = D / 8;
     const int64_t dk0 = (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh;
     const int64_t dv0 = (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh;
-    for (int u = tid; u < BS * CPR; u += NT) {
-      const int kk = u / CPR, c = u % CPR, row = j * BS + kk;
+    for (int u = tid; u < KW * CPR; u += NT) {
+      const int kk = u / CPR, c = u % CPR, row = kb0 + kk;
       if (row >= p.Lkv) continue;
       const int at = kk * D + ((c ^ swz(kk)) << 3);
       *(bf16x8*)((bf16_t*)p.dk + dk0 + (int64_t)row * p.dk_st + c * 8) = *(const bf16x8*)(qd0 + at);
@@ -864,7 +867,8 @@ int launch_bwd(const BwdParams& bp, hipStream_t s, hipStream_t sq, hipEvent_t fo
     } else {
       kp.kv_info = nullptr;
     }
-    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv)), dim3(4 * BS), 0, s, kp);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<D, BS>), dim3((unsigned)(bp.B * nh * bp.Nkv * (BS / DKDV_KEYS))), dim3(256), 0,
+                       s, kp);
     if ((rc = wa_launch_status("bsa_bwd_dkdv"))) return joined(rc);
   }
   return joined(WA_OK);
