@@ -15,7 +15,8 @@
 //   k2q   — per (batch, head, key block) the ascending list of query blocks that listed it, with
 //           multiplicity (the transposed routing of block_sparse_triton.py:364);
 //   dq    — one workgroup per query block walks its key list (64-key steps, K/V streamed to LDS);
-//   dkdv  — one workgroup per key block walks its query list (64-query steps, Q/dO streamed).
+//   dkdv  — one workgroup per 64 keys of a key block walks the block's query list (64-query
+//           steps, Q/dO streamed).
 // Lanes own one column of every 32x32 score tile, so row statistics are per lane and the
 // probabilities / score gradients feed the next product straight from the accumulators.
 #include <algorithm>
