@@ -267,7 +267,7 @@ struct PipeLoad {
 // product half). SM / QK / PV / LD switch the pieces on for the pipeline's first and last blocks.
 // With QT = 2 every K and V fragment read from LDS feeds two products. rs[qt]: the slot's row sum
 // of exponentials of tile qt (this lane's 16 keys).
-template <int D, int NW, int QT, int SMH, bool SM, bool QK, bool PV, bool LD>
+template <int D, int NW, int QT, int SMH, bool SM, bool QK, bool PV, bool LD, int KROW = -1>
 __device__ __forceinline__ void pipe_slot(f32x16 (&S)[2][QT], bf16x8 (&P)[4][QT], f32x16 (&oacc)[QT][D / 32],
                                           const bf16x8 (&qf)[QT][D / 16], const bf16_t* kst, const bf16_t* vst,
                                           const int (&k_rd)[D / 16], const int (&v_rd)[2], const float (&neg_m)[QT],
@@ -275,12 +275,13 @@ __device__ __forceinline__ void pipe_slot(f32x16 (&S)[2][QT], bf16x8 (&P)[4][QT]
                                           const PipeLoad& ldv, const int (&voff)[NextTile<D, NW>::NI], int w,
                                           float (&rs)[QT]) {
   constexpr int H = SMH ^ 1, DC = D / 16, DT = D / 32;
+  constexpr int RH = KROW < 0 ? H : KROW;  // key half of the K / V rows (the key-split loop fixes it)
   constexpr int NI = NextTile<D, NW>::NI, RPI = NextTile<D, NW>::RPI;
-  // operands from LDS: K rows 32 H + l32 (A of S^T = K Q^T), V^T of keys 32 H .. +32 (A of O^T += V^T P^T)
+  // operands from LDS: K rows 32 RH + l32 (A of S^T = K Q^T), V^T of keys 32 RH .. +32 (A of O^T += V^T P^T)
   bf16x8 kf[DC];
   if constexpr (QK) {
 #pragma unroll
-    for (int c = 0; c < DC; ++c) kf[c] = *(const bf16x8*)(kst + k_rd[c] + H * 32 * D);
+    for (int c = 0; c < DC; ++c) kf[c] = *(const bf16x8*)(kst + k_rd[c] + RH * 32 * D);
   }
   bf16x8 vf[2][DT];
   if constexpr (PV) {
@@ -291,7 +292,7 @@ __device__ __forceinline__ void pipe_slot(f32x16 (&S)[2][QT], bf16x8 (&P)[4][QT]
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           const s16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              WA_LDS4(vst + v_rd[t & 1] + (16 * (2 * H + cc) + 8 * hf) * D + (t >> 1) * 64));
+              WA_LDS4(vst + v_rd[t & 1] + (16 * (2 * RH + cc) + 8 * hf) * D + (t >> 1) * 64));
           const bf16x4 vb4 = __builtin_bit_cast(bf16x4, vv);
 #pragma unroll
           for (int e = 0; e < 4; ++e) vf[cc][t][4 * hf + e] = vb4[e];
@@ -670,43 +671,67 @@ bsa_unit_kernel(FwdParams p) {
       else last(std::integral_constant<int, 0>{});
     }
   } else {
-    // Key split: this wave computes key half kh of every 64-key step. Step t's tiles are in stage
-    // t % 2; at its top this wave's loads of them have landed and the barrier extends that to the
-    // workgroup and frees the other stage (read by step t - 1), which then takes step t + 1's
-    // tiles. A half with no real key is skipped (the first half a wave computes then always holds
-    // one, so the running max starts finite); the exponentials are accepted by the same per-lane
-    // sum check as above, and rescaled before the PV product uses them.
+    // Key split: this wave computes key half kh of every 64-key step, pipelined over steps with
+    // one slot per step and K two steps ahead of V. Slot b (0 <= b < T) waits for K(b + 1) and
+    // V(b - 1) (this wave's loads, then the workgroup barrier, after which every wave is done with
+    // K(b) and V(b - 2)), loads K(b + 2) and V(b) into those stages, and runs the QK product of step
+    // b + 1, the exponentials of step b (scores S[b % 2] -> P[2 (b % 2)], P[2 (b % 2) + 1]) and the
+    // PV product of step b - 1 (the other P pair) as one interleaved slot; the sum check then
+    // accepts step b's exponentials or rescales (the accumulators include step b - 1). Every slot
+    // runs all three: a half without real keys is masked whole, so its exponentials are 0 — the
+    // running max starts at -1e30 instead of -inf so that such a half, even as the wave's first,
+    // rescales by exp2(0) = 1 rather than exp2(-inf + inf).
     auto run = [&](auto khc) {
       constexpr int KH = decltype(khc)::value;
-      auto step = [&](auto par, int t) {
-        constexpr int PAR = decltype(par)::value;
-        bf16_t* const kc = PAR ? ks1 : ks0;
-        bf16_t* const vc = PAR ? vs1 : vs0;
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (t + 1 < T) {
-          load_tile(t + 1, true, PAR ? ks0 : ks1);
-          load_tile(t + 1, false, PAR ? vs0 : vs1);
-        }
-        const int real = __builtin_amdgcn_readlane(tab_real, t & 63);
-        if (real <= 32 * KH) return;  // uniform: this half holds no key
-        pipe_slot<D, NWT, QT, KH ^ 1, false, true, false, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2,
-                                                                 no_load, k_off, no_load, v_off, w, rs);
-        if (real < 32 * (KH + 1)) pipe_mask<KH, QT>(S[KH], real, g);
+      auto mask_step = [&](auto par, int b) {
+        const int real = __builtin_amdgcn_readlane(tab_real, b & 63);
+        if (real < 32 * (KH + 1)) pipe_mask<KH, QT>(S[decltype(par)::value], real, g);
         set_neg_m();
-        pipe_slot<D, NWT, QT, KH, true, false, false, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2, no_load,
-                                                             k_off, no_load, v_off, w, rs);
-        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, KH>(S[KH], P, oacc, m_i, l_i, rs, sl2);
+      };
+      auto accept = [&](auto par) {
+        if (pipe_check<QT>(rs)) pipe_rescale<D, QT, decltype(par)::value>(S[decltype(par)::value], P, oacc, m_i, l_i, rs, sl2);
         add_l();
-        pipe_slot<D, NWT, QT, KH ^ 1, false, false, true, false>(S, P, oacc, qf, kc, vc, k_rd, v_rd, neg_m, sl2,
-                                                                 no_load, k_off, no_load, v_off, w, rs);
+      };
+      auto slot = [&](auto par, int b) {
+        constexpr int PAR = decltype(par)::value;  // b % 2
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        load_tile(b + 2, true, PAR ? ks1 : ks0);
+        load_tile(b, false, PAR ? vs1 : vs0);
+        mask_step(par, b);
+        pipe_slot<D, NWT, QT, PAR, true, true, true, false, KH>(S, P, oacc, qf, PAR ? ks0 : ks1, PAR ? vs0 : vs1, k_rd,
+                                                               v_rd, neg_m, sl2, no_load, k_off, no_load, v_off, w, rs);
+        accept(par);
       };
       if (T > 0) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) m_i[qt] = -1e30f;
         load_tile(0, true, ks0);
+        load_tile(1, true, ks1);
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(NT::NI) : "memory");
+        pipe_slot<D, NWT, QT, 1, false, true, false, false, KH>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2,
+                                                               no_load, k_off, no_load, v_off, w, rs);
+        // slot 0: no PV product yet
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        load_tile(2, true, ks0);
         load_tile(0, false, vs0);
-      }
-      for (int t = 0; t < T; t += 2) {
-        step(std::integral_constant<int, 0>{}, t);
-        if (t + 1 < T) step(std::integral_constant<int, 1>{}, t + 1);
+        mask_step(std::integral_constant<int, 0>{}, 0);
+        pipe_slot<D, NWT, QT, 0, true, true, false, false, KH>(S, P, oacc, qf, ks1, vs1, k_rd, v_rd, neg_m, sl2,
+                                                              no_load, k_off, no_load, v_off, w, rs);
+        accept(std::integral_constant<int, 0>{});
+        int b = 1;
+        for (; b + 1 < T; b += 2) {
+          slot(std::integral_constant<int, 1>{}, b);
+          slot(std::integral_constant<int, 0>{}, b + 1);
+        }
+        if (b < T) slot(std::integral_constant<int, 1>{}, b);
+        // the last step's PV product (its V stage is vs[(T - 1) % 2], its P pair (T - 1) % 2)
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if ((T - 1) & 1)
+          pipe_slot<D, NWT, QT, 0, false, false, true, false, KH>(S, P, oacc, qf, ks0, vs1, k_rd, v_rd, neg_m, sl2,
+                                                                 no_load, k_off, no_load, v_off, w, rs);
+        else
+          pipe_slot<D, NWT, QT, 1, false, false, true, false, KH>(S, P, oacc, qf, ks0, vs0, k_rd, v_rd, neg_m, sl2,
+                                                                 no_load, k_off, no_load, v_off, w, rs);
       }
     };
     if (kh == 0) run(std::integral_constant<int, 0>{});
