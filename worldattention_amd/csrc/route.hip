@@ -250,28 +250,61 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
     const float* kbase = p.kp + ((int64_t)b * p.H + h) * (int64_t)p.kp_blocks * p.D;
     const int grp = tid >> 3, tg = tid & 7;
     const bool vec = (p.D & 31) == 0;
-    for (int j0 = 0; j0 < N; j0 += 32) {
-      const int j = j0 + grp;
-      float s = 0.f;
-      if (j < N) {
-        const float* kr = kbase + (int64_t)j * p.D;
-        if (vec) {
-          for (int d = 4 * tg; d < p.D; d += 32) {
-            f32x4 kv[1] = {*(const f32x4*)(kr + d)};
-            pooled_key_row(p, kv, j);
-            s = fmaf(qrow[d], kv[0][0], s);
-            s = fmaf(qrow[d + 1], kv[0][1], s);
-            s = fmaf(qrow[d + 2], kv[0][2], s);
-            s = fmaf(qrow[d + 3], kv[0][3], s);
-          }
-        } else {
-          for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], pooled_key(p, kr[d], j), s);
-        }
-      }
+    auto finish = [&](float s, int j) {
       s += __shfl_xor(s, 1, 64);
       s += __shfl_xor(s, 2, 64);
       s += __shfl_xor(s, 4, 64);
       if (j < N && tg == 0) pr[j] = s * p.scale;
+    };
+    if (vec && p.D == 128) {
+      // four key groups per pass, their 16 loads in flight together (rows past N re-read the last)
+      constexpr int U = 4;
+      for (int j0 = 0; j0 < N; j0 += 32 * U) {
+        f32x4 kv[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float* kr = kbase + (int64_t)min(j0 + 32 * u + grp, N - 1) * 128;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) kv[u][c] = *(const f32x4*)(kr + 32 * c + 4 * tg);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = j0 + 32 * u + grp;
+          f32x4 kr4[4] = {kv[u][0], kv[u][1], kv[u][2], kv[u][3]};
+          pooled_key_row(p, kr4, min(j, N - 1));
+          float s = 0.f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int d = 32 * c + 4 * tg;
+            s = fmaf(qrow[d], kr4[c][0], s);
+            s = fmaf(qrow[d + 1], kr4[c][1], s);
+            s = fmaf(qrow[d + 2], kr4[c][2], s);
+            s = fmaf(qrow[d + 3], kr4[c][3], s);
+          }
+          finish(s, j);
+        }
+      }
+    } else {
+      for (int j0 = 0; j0 < N; j0 += 32) {
+        const int j = j0 + grp;
+        float s = 0.f;
+        if (j < N) {
+          const float* kr = kbase + (int64_t)j * p.D;
+          if (vec) {
+            for (int d = 4 * tg; d < p.D; d += 32) {
+              f32x4 kv[1] = {*(const f32x4*)(kr + d)};
+              pooled_key_row(p, kv, j);
+              s = fmaf(qrow[d], kv[0][0], s);
+              s = fmaf(qrow[d + 1], kv[0][1], s);
+              s = fmaf(qrow[d + 2], kv[0][2], s);
+              s = fmaf(qrow[d + 3], kv[0][3], s);
+            }
+          } else {
+            for (int d = tg; d < p.D; d += 8) s = fmaf(qrow[d], pooled_key(p, kr[d], j), s);
+          }
+        }
+        finish(s, j);
+      }
     }
     __syncthreads();
     float mx = -INFINITY;
@@ -649,49 +682,84 @@ __global__ void __launch_bounds__(256) route_wave_kernel(RouteParams p) {
 
 // Gini second pass: per-head threshold (mean of the head's row Ginis), then the count of sorted
 // slots whose exclusive prefix is below it. The prefix is the reference's: a sequential double
-// running sum rounded to fp32, minus the slot's own weight in fp32 (routing.py:95-113).
-__global__ void __launch_bounds__(64) gini_count_kernel(RouteParams p) {
-  extern __shared__ float sp[];  // [N] sorted probabilities, then keep flags
+// running sum rounded to fp32, minus the slot's own weight in fp32 (routing.py:95-113). Two
+// sequential chains run side by side, each on lane 0 of its own wave: the running sum (wave 0,
+// which leaves every slot's exclusive prefix in LDS) and the head's mean Gini (wave 1); then all
+// lanes compare the prefixes with the threshold and count.
+constexpr int GINI_STAGE_MAX = 8192;  // row Ginis of a head staged in LDS up to this many
+
+__global__ void __launch_bounds__(128) gini_count_kernel(RouteParams p) {
+  // [N] sorted probabilities, then the exclusive prefixes; then (up to GINI_STAGE_MAX) this head's
+  // row Ginis
+  extern __shared__ float sp[];
+  __shared__ float s_thr;
+  __shared__ int s_cnt[2];
   const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row = ((int64_t)b * p.H + h) * p.Nq + i;
   const int N = p.Nkv;
 
-  // the head's mean Gini in the reference's fp32 order (one lane), then the threshold (the
-  // product and the sum round separately, as the reference's two tensor operations do)
-  float thr = 0.f;
-  if (lane == 0) {
-    const float* gw = p.ws_gini;
-    const float s = tc_head_sum([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h);
-    const float mean = wa_div_rn(s, (float)(p.B * p.Nq));
-    thr = wa_add_rn(p.tau_min, wa_mul_rn(mean, p.tau_span));
-  }
-  thr = __shfl(thr, 0, 64);
-  if (b == 0 && i == 0 && lane == 0) p.thresholds[h] = thr;
-
-  for (int m = lane; m < N; m += 64) sp[m] = p.ws_sorted[row * N + m];
+  // the head's row Ginis g[(b H + h) Nq + i] to LDS in one round of loads (read inside the
+  // sequential sum, each global load waited for the previous add), with the row's sorted weights
+  const float* gw = p.ws_gini;
+  const int BN = p.B * p.Nq;
+  const bool staged = BN <= GINI_STAGE_MAX;
+  float* sg = sp + N;
+  if (staged)
+    for (int u = tid; u < BN; u += 128) sg[u] = gw[((int64_t)(u / p.Nq) * p.H + h) * p.Nq + u % p.Nq];
+  for (int m = tid; m < N; m += 128) sp[m] = p.ws_sorted[row * N + m];
   __syncthreads();
-  if (lane == 0) {
+  if (w == 1 && lane == 0) {
+    // the head's mean Gini in the reference's fp32 order, then the threshold (the product and the
+    // sum round separately, as the reference's two tensor operations do)
+    const int HN = p.H * p.Nq;
+    const float sum = staged ? tc_head_sum([&](int r) { return sg[(r / HN) * p.Nq + r % p.Nq]; }, p.B, p.H, p.Nq, h)
+                             : tc_head_sum([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h);
+    const float mean = wa_div_rn(sum, (float)(p.B * p.Nq));
+    const float thr = wa_add_rn(p.tau_min, wa_mul_rn(mean, p.tau_span));
+    s_thr = thr;
+    if (b == 0 && i == 0) p.thresholds[h] = thr;
+  }
+  if (w == 0 && lane == 0) {
+    // exclusive prefixes in place, 16 weights read ahead of the dependent sums
+    constexpr int BATCH = 16;
     double c = 0.0;
-    int count = 0;
-    for (int m = 0; m < N; ++m) {
+    int m = 0;
+    for (; m + BATCH <= N; m += BATCH) {
+      float v[BATCH];
+#pragma unroll
+      for (int e = 0; e < BATCH; ++e) v[e] = sp[m + e];
+#pragma unroll
+      for (int e = 0; e < BATCH; ++e) {
+        c += (double)v[e];
+        v[e] = wa_sub_rn((float)c, v[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < BATCH; ++e) sp[m + e] = v[e];
+    }
+    for (; m < N; ++m) {
       const float pm = sp[m];
       c += (double)pm;
-      const float excl = wa_sub_rn((float)c, pm);
-      const bool keep = excl < thr;
-      count += keep;
-      sp[m] = keep ? 1.f : 0.f;
+      sp[m] = wa_sub_rn((float)c, pm);
     }
-    p.num[row] = count;
   }
   __syncthreads();
-  if (p.mask) {
-    uint8_t* mrow = p.mask + row * N;
-    const int32_t* idx_row = p.index + row * N;
-    for (int m = lane; m < N; m += 64) mrow[idx_row[m]] = sp[m] != 0.f ? 1 : 0;
+  const float thr = s_thr;
+  int cnt = 0;
+  uint8_t* mrow = p.mask ? p.mask + row * N : nullptr;
+  const int32_t* idx_row = p.index + row * N;
+  for (int m = tid; m < N; m += 128) {
+    const bool keep = sp[m] < thr;
+    cnt += keep;
+    if (mrow) mrow[idx_row[m]] = keep ? 1 : 0;
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+  if (lane == 0) s_cnt[w] = cnt;
+  __syncthreads();
+  if (tid == 0) p.num[row] = s_cnt[0] + s_cnt[1];
 }
 
 // Mask -> ascending (index, num) per row, padded with -1 (block_sparse_triton.py:20-57).
@@ -886,8 +954,9 @@ extern "C" int wa_route(const wa_route_args* a, void* stream) {
   hipLaunchKernelGGL(route_kernel, grid, dim3(256), (size_t)rp.NP * sizeof(uint64_t), s, rp);
   int rc = wa_launch_status("route");
   if (rc != WA_OK || a->mode != WA_ROUTE_GINI) return rc;
-  hipLaunchKernelGGL(gini_count_kernel, dim3((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B), dim3(64),
-                     (size_t)a->Nkv * sizeof(float), s, rp);
+  const int64_t staged = a->B * a->Nq <= GINI_STAGE_MAX ? a->B * a->Nq : 0;
+  hipLaunchKernelGGL(gini_count_kernel, dim3((unsigned)a->Nq, (unsigned)nh, (unsigned)a->B), dim3(128),
+                     (size_t)(a->Nkv + staged) * sizeof(float), s, rp);
   return wa_launch_status("route_gini_count");
 }
 
