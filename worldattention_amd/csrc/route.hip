@@ -229,6 +229,7 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
   __shared__ float qrow[256];
   __shared__ double dscratch[8];
   __shared__ float fscratch[8];
+  __shared__ float fscratch32[32];
   if (clear_unrouted(p)) return;
   const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
@@ -390,10 +391,8 @@ __global__ void __launch_bounds__(256) route_kernel(RouteParams p) {
       if (m < N) tl[m] = terms[e];
     }
     __syncthreads();
-    if (tid == 0) {
-      const float s = tc_inner_sum([&](int m) { return tl[m]; }, 0, N);
-      p.ws_gini[row] = wa_div_rn(s, (float)N);
-    }
+    const float s = tc_inner_sum_wg([&](int m) { return tl[m]; }, 0, N, fscratch32);
+    if (tid == 0) p.ws_gini[row] = wa_div_rn(s, (float)N);
   }
 }
 

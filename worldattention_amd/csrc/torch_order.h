@@ -63,4 +63,29 @@ __device__ float tc_inner_sum(const Load& x, int start, int n) {
   return fin;
 }
 
+// tc_inner_sum with its 32 independent cascades (lane l's cascade k runs over elements
+// start + l + 8 k + 32 i) on threads 0..31 of the workgroup, then the same folds in the same order
+// on thread 0: the same fp32 value. Every thread of the workgroup calls it (it holds barriers);
+// `chain` is 32 floats of LDS; the result is valid on thread 0.
+template <typename Load>
+__device__ float tc_inner_sum_wg(const Load& x, int start, int n, float* chain) {
+  constexpr int L = 8;
+  const int tid = threadIdx.x;
+  if (n < L) return tid == 0 ? tc_row_sum(x, start, 1, n) : 0.f;
+  const int nv = n / L, groups = nv / 4;
+  if (tid < 32) chain[tid] = tc_cascade(x, start + (tid % 8) + 8 * (tid / 8), 4 * L, groups);
+  __syncthreads();
+  float fin = 0.f;
+  if (tid == 0) {
+    for (int k = nv * L; k < n; ++k) fin = wa_add_rn(fin, x(start + k));
+    for (int l = 0; l < L; ++l) {
+      float part = chain[l];
+      for (int i = groups * 4; i < nv; ++i) part = wa_add_rn(part, x(start + l + i * L));
+      for (int k = 1; k < 4; ++k) part = wa_add_rn(part, chain[l + 8 * k]);
+      fin = wa_add_rn(fin, part);
+    }
+  }
+  return fin;
+}
+
 }  // namespace
