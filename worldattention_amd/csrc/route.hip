@@ -202,6 +202,21 @@ __device__ bool clear_unrouted(const RouteParams& p) {
   return true;
 }
 
+// tc_head_sum with its contiguous inner sums spread over threads base .. base + 31
+// (tc_inner_sum_wg); every thread calls it, the result is valid on thread `base`.
+template <typename Load>
+__device__ float tc_head_sum_wg(const Load& g, int B, int H, int Nq, int h, float* chain, int base) {
+  if (H == 1) return tc_inner_sum_wg(g, 0, B * Nq, chain, base);
+  if (Nq == 1) return (int)threadIdx.x == base ? tc_head_sum(g, B, H, Nq, h) : 0.f;
+  float s = 0.f;
+  for (int b = 0; b < B; ++b) {
+    const float part = tc_inner_sum_wg(g, (b * H + h) * Nq, Nq, chain, base);
+    if ((int)threadIdx.x == base) s = wa_add_rn(s, part);
+    __syncthreads();  // the chain buffer is reused
+  }
+  return s;
+}
+
 // Sum over (batch, query block) of one head's row Ginis g[(b * H + h) * Nq + i], as torch sums
 // a [B, H, Nq] tensor over dims (0, 2): with H == 1 the two dims merge into one contiguous run;
 // with Nq == 1 it is an outer reduction over b of column h (columns in groups of 32 when H >= 8,
@@ -693,6 +708,7 @@ __global__ void __launch_bounds__(128) gini_count_kernel(RouteParams p) {
   extern __shared__ float sp[];
   __shared__ float s_thr;
   __shared__ int s_cnt[2];
+  __shared__ float s_chain[32];
   const int i = blockIdx.x, hs = blockIdx.y, b = blockIdx.z;
   const int h = p.heads ? p.heads[hs] : hs;
   if (h < 0 || h >= p.H) return;
@@ -710,38 +726,79 @@ __global__ void __launch_bounds__(128) gini_count_kernel(RouteParams p) {
     for (int u = tid; u < BN; u += 128) sg[u] = gw[((int64_t)(u / p.Nq) * p.H + h) * p.Nq + u % p.Nq];
   for (int m = tid; m < N; m += 128) sp[m] = p.ws_sorted[row * N + m];
   __syncthreads();
-  if (w == 1 && lane == 0) {
-    // the head's mean Gini in the reference's fp32 order, then the threshold (the product and the
-    // sum round separately, as the reference's two tensor operations do)
-    const int HN = p.H * p.Nq;
-    const float sum = staged ? tc_head_sum([&](int r) { return sg[(r / HN) * p.Nq + r % p.Nq]; }, p.B, p.H, p.Nq, h)
-                             : tc_head_sum([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h);
-    const float mean = wa_div_rn(sum, (float)(p.B * p.Nq));
-    const float thr = wa_add_rn(p.tau_min, wa_mul_rn(mean, p.tau_span));
-    s_thr = thr;
-    if (b == 0 && i == 0) p.thresholds[h] = thr;
-  }
-  if (w == 0 && lane == 0) {
-    // exclusive prefixes in place, 16 weights read ahead of the dependent sums
-    constexpr int BATCH = 16;
-    double c = 0.0;
-    int m = 0;
-    for (; m + BATCH <= N; m += BATCH) {
-      float v[BATCH];
+  // Exclusive prefixes in place. When every weight is 0 or at least 2^-29 and they sum below 2,
+  // all of them and every partial sum are multiples of 2^-52 below 2, so each double sum is exact
+  // whatever the order: wave 0 then forms them as a scan (lane L holds slots 8L .. 8L + 7) and gets
+  // the sequential sum's values bit for bit. Otherwise (or past 512 slots) lane 0 runs the
+  // sequential sum.
+  if (w == 0) {
+    bool fast = N <= 512;
+    float v[8];
+    double part = 0.0;
+    if (fast) {
 #pragma unroll
-      for (int e = 0; e < BATCH; ++e) v[e] = sp[m + e];
-#pragma unroll
-      for (int e = 0; e < BATCH; ++e) {
-        c += (double)v[e];
-        v[e] = wa_sub_rn((float)c, v[e]);
+      for (int e = 0; e < 8; ++e) {
+        const int m = lane * 8 + e;
+        v[e] = m < N ? sp[m] : 0.f;
+        part += (double)v[e];
       }
+      bool ok = true;
 #pragma unroll
-      for (int e = 0; e < BATCH; ++e) sp[m + e] = v[e];
+      for (int e = 0; e < 8; ++e) ok = ok && (v[e] == 0.f || v[e] >= 0x1p-29f);
+      double incl = part;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const double y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+      }
+      ok = ok && __shfl(incl, 63, 64) < 2.0;
+      fast = __all(ok);
+      if (fast) {
+        double c = incl - part;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          c += (double)v[e];
+          const int m = lane * 8 + e;
+          if (m < N) sp[m] = wa_sub_rn((float)c, v[e]);
+        }
+      }
     }
-    for (; m < N; ++m) {
-      const float pm = sp[m];
-      c += (double)pm;
-      sp[m] = wa_sub_rn((float)c, pm);
+    if (!fast && lane == 0) {
+      constexpr int BATCH = 16;
+      double c = 0.0;
+      int m = 0;
+      for (; m + BATCH <= N; m += BATCH) {
+        float u[BATCH];
+#pragma unroll
+        for (int e = 0; e < BATCH; ++e) u[e] = sp[m + e];
+#pragma unroll
+        for (int e = 0; e < BATCH; ++e) {
+          c += (double)u[e];
+          u[e] = wa_sub_rn((float)c, u[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < BATCH; ++e) sp[m + e] = u[e];
+      }
+      for (; m < N; ++m) {
+        const float pm = sp[m];
+        c += (double)pm;
+        sp[m] = wa_sub_rn((float)c, pm);
+      }
+    }
+  }
+  {
+    // the head's mean Gini in the reference's fp32 order, its independent cascades on wave 1
+    // (threads 64 .. 95) while thread 0 runs the prefix sum above, then the threshold (the product
+    // and the sum round separately, as the reference's two tensor operations do)
+    const int HN = p.H * p.Nq;
+    const float sum = staged ? tc_head_sum_wg([&](int r) { return sg[(r / HN) * p.Nq + r % p.Nq]; }, p.B, p.H, p.Nq, h,
+                                              s_chain, 64)
+                             : tc_head_sum_wg([&](int r) { return gw[r]; }, p.B, p.H, p.Nq, h, s_chain, 64);
+    if (tid == 64) {
+      const float mean = wa_div_rn(sum, (float)(p.B * p.Nq));
+      const float thr = wa_add_rn(p.tau_min, wa_mul_rn(mean, p.tau_span));
+      s_thr = thr;
+      if (b == 0 && i == 0) p.thresholds[h] = thr;
     }
   }
   __syncthreads();

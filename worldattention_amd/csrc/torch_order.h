@@ -64,19 +64,19 @@ __device__ float tc_inner_sum(const Load& x, int start, int n) {
 }
 
 // tc_inner_sum with its 32 independent cascades (lane l's cascade k runs over elements
-// start + l + 8 k + 32 i) on threads 0..31 of the workgroup, then the same folds in the same order
-// on thread 0: the same fp32 value. Every thread of the workgroup calls it (it holds barriers);
-// `chain` is 32 floats of LDS; the result is valid on thread 0.
+// start + l + 8 k + 32 i) on threads base .. base + 31 of the workgroup, then the same folds in the
+// same order on thread `base`: the same fp32 value. Every thread of the workgroup calls it (it
+// holds a barrier); `chain` is 32 floats of LDS; the result is valid on thread `base`.
 template <typename Load>
-__device__ float tc_inner_sum_wg(const Load& x, int start, int n, float* chain) {
+__device__ float tc_inner_sum_wg(const Load& x, int start, int n, float* chain, int base = 0) {
   constexpr int L = 8;
-  const int tid = threadIdx.x;
-  if (n < L) return tid == 0 ? tc_row_sum(x, start, 1, n) : 0.f;
+  const int t = (int)threadIdx.x - base;
+  if (n < L) return t == 0 ? tc_row_sum(x, start, 1, n) : 0.f;
   const int nv = n / L, groups = nv / 4;
-  if (tid < 32) chain[tid] = tc_cascade(x, start + (tid % 8) + 8 * (tid / 8), 4 * L, groups);
+  if (t >= 0 && t < 32) chain[t] = tc_cascade(x, start + (t % 8) + 8 * (t / 8), 4 * L, groups);
   __syncthreads();
   float fin = 0.f;
-  if (tid == 0) {
+  if (t == 0) {
     for (int k = nv * L; k < n; ++k) fin = wa_add_rn(fin, x(start + k));
     for (int l = 0; l < L; ++l) {
       float part = chain[l];

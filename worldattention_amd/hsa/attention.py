@@ -496,11 +496,15 @@ def _run_linear_heads(plan, linear_mode, q, k, v, qb, k_coarse, v_coarse, k_proj
             kcb, vcb = _lib.kernel_ready(kc), _lib.kernel_ready(vc)
             if save is not None:
                 save.update(kc=kc, vc=vc)
+            # The dense launch over the compressed keys tiles its queries freely: 128-query units at
+            # D = 128 walk the same 64-key steps in the same order (the same arithmetic per query)
+            # in half the units of the routed block size 64 (one round of units instead of ~1.7).
+            dense_block = 128 if qb.shape[-1] == 128 else block_size
             if plan.both:
-                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
+                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=dense_block, layout="blhd",
                             heads=plan.t["both"], out=lin_tmp, lq=q_len, scale=scale)
             if plan.linear_only:
-                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=block_size, layout="blhd",
+                bsa_forward(qb, kcb, vcb, index=None, num=None, block_size=dense_block, layout="blhd",
                             heads=plan.t["linear_only"], out=out, lq=q_len, epilogue=_lib.WA_EPI_GATED,
                             attn_round_bf16=lin_round, scale=scale, **gate.kwargs())
         else:
