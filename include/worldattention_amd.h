@@ -230,7 +230,8 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * arrivals (optional): [rows] int32 counters the units use to find each row's last unit; they
  * must be 0 on entry (e.g. cleared by wa_route's `clear`, or left so by the previous launch that
  * used them) and are 0 again when the launch completes. NULL: the launch clears counters in
- * `workspace` with one extra small kernel. Launches that overlap must not share arrivals. */
+ * `workspace` with one extra small kernel (none when every row takes a single unit, which counts
+ * nothing). Launches that overlap must not share arrivals. */
 #define WA_BSA_DEFAULT_SPLIT 16
 #define WA_BSA_DEFAULT_SPLIT_64 64
 typedef struct wa_bsa_fwd_args {

@@ -1012,7 +1012,7 @@ __global__ void __launch_bounds__(256) bsa_clear_arrivals_kernel(int* arrivals, 
 
 template <int D, int BS>
 int launch(const FwdParams& fp, int64_t rows, bool cleared, bool key_split, hipStream_t stream) {
-  if (!cleared) {
+  if (!cleared && fp.max_splits > 1) {  // (with one unit per row no unit counts arrivals)
     hipLaunchKernelGGL(bsa_clear_arrivals_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream,
                        fp.arrivals, rows);
     const int rc = wa_launch_status("bsa_fwd_clear");
