@@ -6,8 +6,9 @@ Headline (``value``, ``ms_per_step``, ``roofline``, ``cpu_baseline``): cfg 2, th
 A step is one ``hsa_forward`` call (routing + sparse branch + elu(x)+1 linear branch + fusion) on
 seeded synthetic inputs already resident in HBM: B=1, H=12 (8 sparse heads with per-head top-k from
 {8,16,32} + 4 linear heads), D=128, Lq=4,680, Lkv=32,760, block 128, bf16. The timed steps are
-plain eager calls, K of them between two device synchronizations (the same call captured once in a
-HIP graph and replayed is reported beside it). ``value`` is
+plain eager calls, K of them between two device synchronizations, taken after W warmup calls and
+after the config's other legs have run (the same timing from an idle GPU, and the call captured
+once in a HIP graph and replayed, are reported beside it). ``value`` is
 the effective sparse TFLOP/s of the whole call (useful sparse FLOP / call time); ``roofline`` is the
 sparse kernel's own rate, timed with HIP events on the stream it runs on. ``hbm_bound_launches``
 gives the HBM rate of the memory-bound launches of the same call (Q/K block pooling, elu1 state,
@@ -48,9 +49,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # the eager call reaches its steady time after ~100 calls (0.144 ms over calls 20-70, 0.131 over
-    # calls 170-220 in one run): the untimed warmup covers that
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-calls", type=int, default=12)
@@ -287,14 +286,21 @@ def bench_cfg2(args, dev):
     sparse_heads = [h for h, m in enumerate(cfg["head_modes"]) if m != "linear"]
     useful_flop, tile_flop = workloads.sparse_flops(route.num, route.index, q.shape[1], k.shape[1],
                                                     cfg["block_size"], d, heads=sparse_heads)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    def eager_ms():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # From an idle GPU the call speeds up over its first ~200 calls (0.155 -> 0.129 ms in batches of
+    # ten; a 50 ms idle pause starts the climb again): the eager timing is taken twice, first here
+    # (reported as the cold figure) and, for the headline, after this config's other legs have
+    # kept the GPU busy, as a serving loop does.
+    ms_cold = eager_ms()
     # The same call captured once in a HIP graph and replayed (a serving loop): the kernels and their
     # inputs are identical; the replay drops the per-call host work but runs the two streams' kernels
     # one after the other.
@@ -319,10 +325,12 @@ def bench_cfg2(args, dev):
         sparse_only()
     sparse_ms = stream_time_ms(sparse_only, max(args.steps, 20))
     achieved = useful_flop / (sparse_ms * 1e-3) / 1e12
-    log(f"cfg2: {ms_per_step:.4f} ms/call (eager; graph replay {graph_ms:.4f}), sparse kernel {sparse_ms:.4f} ms = "
+    log(f"cfg2: {ms_cold:.4f} ms/call (eager, cold start; graph replay {graph_ms:.4f}), sparse kernel {sparse_ms:.4f} ms = "
         f"{achieved:.1f} TFLOP/s")
     hbm = memory_legs(cfg, plan, route, gate, dev, max(args.steps, 20))
-    return cfg, proj, dict(ms_per_step=ms_per_step, graph_ms=graph_ms, useful_flop=useful_flop, tile_flop=tile_flop,
+    ms_per_step = eager_ms()
+    log(f"cfg2: {ms_per_step:.4f} ms/call eager after the other cfg2 legs ({ms_cold:.4f} from a cold start)")
+    return cfg, proj, dict(ms_per_step=ms_per_step, ms_cold=ms_cold, graph_ms=graph_ms, useful_flop=useful_flop, tile_flop=tile_flop,
                            sparse_ms=sparse_ms, achieved=achieved, hbm=hbm, cached=cached)
 
 
@@ -866,9 +874,13 @@ def main():
                                "8 sparse heads top-k from {8,16,32} + 4 elu1 linear heads",
                    "topk": cfg["topk"], "head_modes": cfg["head_modes"], "seed": args.seed},
         "hsa_fwd_ms_per_chunk": round(c2["ms_per_step"], 4),
+        "hsa_fwd_ms_per_chunk_cold": round(c2["ms_cold"], 4),
         "hsa_fwd_ms_per_chunk_graph": round(c2["graph_ms"], 4),
-        "timing": "ms_per_step: eager hsa_forward calls timed between two device synchronizations; "
-                  "hsa_fwd_ms_per_chunk_graph: the same call captured once in a HIP graph and replayed",
+        "timing": "ms_per_step: eager hsa_forward calls timed between two device synchronizations, after "
+                  "the warmup calls and after this config's other legs (graph replay, cached sums, sparse "
+                  "kernel, memory-bound launches) have run; hsa_fwd_ms_per_chunk_cold: the same timing "
+                  "taken first, from an idle GPU; hsa_fwd_ms_per_chunk_graph: the same call captured once "
+                  "in a HIP graph and replayed",
         "hsa_fwd_ms_per_chunk_cached_key_sums": c2["cached"],
         "sparse_kernel_ms": round(c2["sparse_ms"], 4),
         "sparse_useful_gflop": round(c2["useful_flop"] / 1e9, 3),
