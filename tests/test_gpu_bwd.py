@@ -269,6 +269,36 @@ def test_bf16_dk_dv_are_the_fp32_gradients_rounded(d):
                      dq=torch.zeros(q.shape, device=DEV), dk=dk16, dv=dv16, accumulate=True)
 
 
+@pytest.mark.parametrize("b,lkv,h,heads", [(1, 20, 2, [0]), (1, 64, 3, [0, 2]), (2, 777, 3, [1, 2]),
+                                           (1, 4100, 2, [0, 1])])
+def test_bf16_elu1_key_side_equals_the_fp32_path_rounded(b, lkv, h, heads):
+    """The elu1 key side with bf16 K / V and bf16 dK / dV at D = 128 (the streamed kernel: runs of
+    one, two and many 32-token tiles, a partial last tile, two batches, a subset of the heads) gives
+    the fp32 key side's values rounded to bf16, bit for bit, and leaves the other heads untouched."""
+    from worldattention_amd.hsa._autograd import elu1_backward
+    torch.manual_seed(lkv)
+    d, lq = 128, 300
+    q = torch.randn(b, lq, h, d, device=DEV).bfloat16()
+    k = torch.randn(b, lkv, h, d, device=DEV).bfloat16()
+    v = torch.randn(b, lkv, h, d, device=DEV).bfloat16()
+    heads_t = torch.tensor(heads, dtype=torch.int32, device=DEV)
+    s, z = WA.elu1_state(k, v, heads_t)
+    g = torch.randn(b, lq, h, d, device=DEV)
+    grads = []
+    for dt in (torch.float32, torch.bfloat16):
+        dq = torch.zeros(q.shape, device=DEV)
+        dk, dv = (torch.full(t.shape, 7.0, device=DEV, dtype=dt) for t in (k, v))
+        elu1_backward(q, k, v, g, s, z, heads_t, dq, dk, dv, kv_accumulate=False)
+        grads.append((dk, dv))
+    (dk32, dv32), (dk16, dv16) = grads
+    assert torch.equal(dk16[:, :, heads], dk32[:, :, heads].bfloat16())
+    assert torch.equal(dv16[:, :, heads], dv32[:, :, heads].bfloat16())
+    others = [x for x in range(h) if x not in heads]
+    if others:
+        assert bool((dk16[:, :, others] == 7.0).all()) and bool((dv16[:, :, others] == 7.0).all())
+    assert torch.isfinite(dk16.float()).all() and float(dk16[:, :, heads].float().abs().max()) > 0
+
+
 def test_hsa_bf16_inputs_get_bf16_gradients_within_tolerance():
     """Split heads with bf16 q / k / v: dK and dV come back bf16 straight from the kernels."""
     torch.manual_seed(12)

@@ -969,6 +969,164 @@ __global__ void __launch_bounds__(256) elu1_bwd_kv16_kernel(Elu1BwdParams p) {
   }
 }
 
+// Key side at D = 128, bf16 K / V in and bf16 dK / dV out, streamed. Wave w owns output column
+// tile w (32 channels) of both products for every token of the workgroup's run, with its operands
+// of the state gradient (column slice for dK, row slice for dV, bf16 hi + lo: 32 fragments) read
+// from LDS once into registers. K and V tiles of 32 tokens stream through a 3-stage LDS ring by
+// direct-to-LDS loads, two tiles ahead; phi(K) is formed once per tile into LDS, and the results
+// are staged in LDS and leave as whole 256-byte rows. Per tile a wave reads 16 KiB of B fragments
+// for its 32 MFMAs (elu1_bwd_kv16_kernel reads 128 KiB of state fragments for 128) and waits on no
+// load it issued itself. The fragments and their order are elu1_bwd_kv16_kernel's, so the results
+// are bit-identical to it (and to elu1_bwd_kv_kernel rounded to bf16).
+//
+// Every step issues the same vector memory operations per thread: 4 tile loads (2 K, 2 V; past
+// the run's last tile they read nothing, through an empty buffer range, into the stage just
+// consumed) and 4 stores (2 dK, 2 dV; rows past Lkv fall outside the store's buffer range). Tile
+// `it` is therefore waited for with a fixed count of younger operations (vector memory operations
+// complete in issue order): after the loads of tile it come those of tiles it + 1 and it + 2 and
+// the stores of the up to three steps before it.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) elu1_bwd_kvr_kernel(Elu1BwdParams p) {
+  static_assert(D == 128, "one 32-channel column tile per wave");
+  constexpr int DC = D / 16, TS = 32;
+  constexpr int TILE = TS * D;               // bf16 elements of one K or V tile (8 KiB)
+  constexpr int CPR = D / 8, RPI = 64 / CPR;  // 16-byte chunks per row, rows per wave instruction
+  constexpr int NI = TS / (RPI * 4);          // instructions per wave per tensor and tile
+  static_assert(NI == 2 && TS * CPR == 2 * 256, "fixed per-thread operation counts");
+  // Stage s: K at 2s TILE, V at (2s + 1) TILE. While the state gradient's fragments are read, its
+  // hi and lo tiles occupy TILEs 2-5 and 6-9; afterwards TILEs 2-5 are stages 1 and 2, TILE 6
+  // phi(K), TILEs 7 and 8 the staged dK and dV rows.
+  __shared__ __attribute__((aligned(1024))) bf16_t lds[10 * TILE];
+  bf16_t* const s_hi = lds + 2 * TILE;
+  bf16_t* const s_lo = lds + 6 * TILE;
+  bf16_t* const pt = lds + 6 * TILE;
+  bf16_t* const okt = lds + 7 * TILE;
+  bf16_t* const ovt = lds + 8 * TILE;
+
+  const int hs = blockIdx.y, b = blockIdx.z;
+  const int h = p.heads ? p.heads[hs] : hs;
+  if (h < 0 || h >= p.H) return;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t bh = (int64_t)b * p.n_heads + hs;
+  const int n_groups = (p.Lkv + TS - 1) / TS;
+  const int g0 = blockIdx.x * p.kv_groups_per_wg;
+  const int ntiles = min(n_groups, g0 + p.kv_groups_per_wg) - g0;
+  const bf16_t* kbase = (const bf16_t*)p.k + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
+  const bf16_t* vbase = (const bf16_t*)p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+  bf16_t* dkbase = (bf16_t*)p.dk + (int64_t)b * p.dk_sb + (int64_t)h * p.dk_sh;
+  bf16_t* dvbase = (bf16_t*)p.dv + (int64_t)b * p.dv_sb + (int64_t)h * p.dv_sh;
+
+  // direct-to-LDS lane offsets: instruction i of wave w fills rows (4 i + w) RPI .. + RPI; lane L
+  // writes row + L / CPR, slot L % CPR, which holds chunk slot ^ dual_swizzle(row)
+  int k_off[NI], v_off[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = (4 * i + w) * RPI + lane / CPR, pos = lane % CPR;
+    const int chunk = pos ^ dual_swizzle<D>(row);
+    k_off[i] = (int)(row * p.k_st + chunk * 8) * 2;
+    v_off[i] = (int)(row * p.v_st + chunk * 8) * 2;
+  }
+  auto issue = [&](int it, int s) {
+    const bool real = it < ntiles;
+    const int t0 = real ? (g0 + it) * TS : 0;
+    const int rows = real ? min(TS, p.Lkv - t0) : 0;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kbase + (int64_t)t0 * p.k_st), (short)0, rows ? (int)((rows - 1) * p.k_st + D) * 2 : 0, WA_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vbase + (int64_t)t0 * p.v_st), (short)0, rows ? (int)((rows - 1) * p.v_st + D) * 2 : 0, WA_BUF_DWORD3);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int r0 = (4 * i + w) * RPI;
+      lds_dma16(krs, lds + 2 * s * TILE + r0 * D, k_off[i]);
+      lds_dma16(vrs, lds + (2 * s + 1) * TILE + r0 * D, v_off[i]);
+    }
+  };
+
+  issue(0, 0);
+  // z at this lane's epilogue channels 32 w + 8 rq + 4 g + i
+  f32x4 zr[4];
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) zr[rq] = *(const f32x4*)(p.dz + bh * D + 32 * w + 8 * rq + 4 * g);
+  stage_hilo<D>(p.dstate + bh * D * D, s_hi, s_lo, tid);
+  __syncthreads();
+  bf16x8 akh[DC], akl[DC], avh[DC], avl[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) {
+    akh[c] = tile_tr8n<D>(s_hi, c, 32 * w, lane);
+    akl[c] = tile_tr8n<D>(s_lo, c, 32 * w, lane);
+    avh[c] = tile_row8<D>(s_hi, 32 * w + l32, 2 * c + g);
+    avl[c] = tile_row8<D>(s_lo, 32 * w + l32, 2 * c + g);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave holds its fragments
+  issue(1, 1);
+  issue(2, 2);
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int s = it % 3;
+    const bf16_t* kt = lds + 2 * s * TILE;
+    const bf16_t* vt = kt + TILE;
+    // tile it has landed in every wave's share, and the previous step's reads are done
+    if (it >= 3) asm volatile("s_waitcnt vmcnt(20)\n\ts_barrier" ::: "memory");
+    else if (it == 2) asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    else if (it == 1) asm volatile("s_waitcnt vmcnt(12)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    // phi(K) at the same swizzled positions (elementwise: a slot's chunk does not matter)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int ci = tid + 256 * u, r = ci / CPR, pos = ci % CPR;
+      bf16x8 x = *(const bf16x8*)(kt + r * D + pos * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = (bf16_t)elu1f((float)x[e]);
+      *(bf16x8*)(pt + r * D + pos * 8) = x;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // dK^T[e, t] = sum_d dS^T[d, e] v[t, d], dV^T[d, t] = sum_e dS^T[d, e] phi(k)[t, e] (lane = token)
+    f32x16 dk = f32x16{}, dv = f32x16{};
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const bf16x8 vb = tile_row8<D>(vt, l32, 2 * c + g);
+      const bf16x8 pb = tile_row8<D>(pt, l32, 2 * c + g);
+      dk = wa_mfma32(akh[c], vb, dk);
+      dk = wa_mfma32(akl[c], vb, dk);
+      dv = wa_mfma32(avh[c], pb, dv);
+      dv = wa_mfma32(avl[c], pb, dv);
+    }
+    // this lane's channels 32 w + 8 rq + 4 g + i of token l32, staged as 8-byte pieces
+#pragma unroll
+    for (int rq = 0; rq < 4; ++rq) {
+      const int at = l32 * D + (((4 * w + rq) ^ dual_swizzle<D>(l32)) * 8) + 4 * g;
+      const bf16x4 k4 = *(const bf16x4*)(kt + at);
+      bf16x4 ok4, ov4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ok4[i] = (bf16_t)((dk[rq * 4 + i] + zr[rq][i]) * elu1_grad((float)k4[i]));
+        ov4[i] = (bf16_t)dv[rq * 4 + i];
+      }
+      *(bf16x4*)(okt + at) = ok4;
+      *(bf16x4*)(ovt + at) = ov4;
+    }
+    // staged rows complete; stage s is free for tile it + 3
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(it + 3, s);
+    const int t0 = (g0 + it) * TS, rows = min(TS, p.Lkv - t0);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(dkbase + (int64_t)t0 * p.dk_st), (short)0, (int)((rows - 1) * p.dk_st + D) * 2, WA_BUF_DWORD3);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(dvbase + (int64_t)t0 * p.dv_st), (short)0, (int)((rows - 1) * p.dv_st + D) * 2, WA_BUF_DWORD3);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int ci = tid + 256 * u, r = ci / CPR, cc = ci % CPR;
+      const u32x4 ko = __builtin_bit_cast(u32x4, tile_row8<D>(okt, r, cc));
+      const u32x4 vo = __builtin_bit_cast(u32x4, tile_row8<D>(ovt, r, cc));
+      __builtin_amdgcn_raw_buffer_store_b128(ko, krs, (int)(r * p.dk_st + cc * 8) * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b128(vo, vrs, (int)(r * p.dv_st + cc * 8) * 2, 0, 0);
+    }
+  }
+  // the ring's last (empty) loads and the stores drain before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 __global__ void __launch_bounds__(256) elu1_bwd_reduce_kernel(Elu1BwdParams p, int D) {
   const int64_t per = (int64_t)D * D + D;
   const int64_t total = (int64_t)p.B * p.n_heads * per;
@@ -1136,7 +1294,12 @@ extern "C" int wa_elu1_bwd(const wa_elu1_bwd_args* a, void* stream) {
     const int64_t per_bh = std::max<int64_t>(1, std::min<int64_t>((n_groups + 3) / 4, (512 + a->B * nh - 1) / (a->B * nh)));
     bp.kv_groups_per_wg = (int)((n_groups + per_bh - 1) / per_bh);
     const dim3 gk16((unsigned)((n_groups + bp.kv_groups_per_wg - 1) / bp.kv_groups_per_wg), (unsigned)nh, (unsigned)a->B);
-    if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk16, dim3(256), 0, s, bp);
+    // the streamed kernel addresses a 32-token tile's rows with 32-bit byte offsets
+    const bool streamed = a->D == 128 && a->k_st < (1 << 24) && a->v_st < (1 << 24) && a->dk_st < (1 << 24) &&
+                          a->dv_st < (1 << 24) && a->k_st >= a->D && a->v_st >= a->D && a->dk_st >= a->D &&
+                          a->dv_st >= a->D;
+    if (streamed) hipLaunchKernelGGL(elu1_bwd_kvr_kernel<128>, gk16, dim3(256), 0, s, bp);
+    else if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv16_kernel<128>, gk16, dim3(256), 0, s, bp);
     else hipLaunchKernelGGL(elu1_bwd_kv16_kernel<64>, gk16, dim3(256), 0, s, bp);
   } else {
     if (a->D == 128) hipLaunchKernelGGL(elu1_bwd_kv_kernel<128>, gk, dim3(256), 0, s, bp);
