@@ -233,7 +233,7 @@ int wa_map_to_index(const uint8_t* mask, int64_t rows, int64_t ncols, int32_t* i
  * `workspace` with one extra small kernel (none when every row takes a single unit, which counts
  * nothing). Launches that overlap must not share arrivals. */
 #define WA_BSA_DEFAULT_SPLIT 16
-#define WA_BSA_DEFAULT_SPLIT_64 64
+#define WA_BSA_DEFAULT_SPLIT_64 48
 typedef struct wa_bsa_fwd_args {
   const void* q; int64_t q_sb, q_st, q_sh;
   const void* k; int64_t k_sb, k_st, k_sh;

@@ -120,7 +120,7 @@ BsaFwdArgs = _struct("wa_bsa_fwd_args", [
 ])
 
 BSA_DEFAULT_SPLIT = 16      # WA_BSA_DEFAULT_SPLIT (128-key blocks)
-BSA_DEFAULT_SPLIT_64 = 64   # WA_BSA_DEFAULT_SPLIT_64 (64-key blocks)
+BSA_DEFAULT_SPLIT_64 = 48   # WA_BSA_DEFAULT_SPLIT_64 (64-key blocks)
 
 
 def bsa_default_split(block_size: int) -> int:
